@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Packed decode-attention benchmark on one MI355X (BASELINE.json metric).
+
+Default workload: the headline 7B GQA shape -- 28 layers,
+batch 16, 28 q / 4 kv heads, head_dim 128, 256 packed pages (32768 tokens) +
+100 residual tokens + the new token per sequence, target_bit 2.5 (Key 3.0
+bits).  One *step* is one decode step of the attention path over all 28
+layers (distinct per-layer buffers, far larger than the 256 MB Infinity
+Cache); ``value`` is microseconds per layer-step.  Synthetic seeded data
+(logitfill_amd.synth), resident in HBM before timing starts.
+
+Prints one JSON line (the driver's contract) with ``roofline`` (dominant
+kernel: the fused decode kernel) and ``cpu_baseline`` (the CPU oracle's dense
+dequantise-then-attend path on a bounded sample, rank 0 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2_k4"])
+    p.add_argument("--layers", type=int, default=None)
+    p.add_argument("--kernel", default="auto", choices=["auto", "valu", "mfma"])
+    p.add_argument("--pages-per-split", type=int, default=None)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
+    return p.parse_args()
+
+
+def algorithmic_bytes(widths, words, n_kv, n_q, D, H, R1, k_group=128, v_group=128):
+    """Bytes one decode step of one sequence and layer must read/write (packed path).
+
+    K codes 4*(w2+w4+w8) + fp16 tier 2*width16 + V codes 4*D/16 + V scale/min
+    4*D/v_group per token and kv head; K scale/min 4 per (int-tier slot, Key
+    group); bf16 residual K+V 4*D per token (R1 = residual + new token); bf16 q
+    and output 4*D per q head.  Returns (total, payload) where payload counts
+    the K codes, the fp16 tier and the V codes only.
+    """
+    per_tok = 4 * sum(words) + 2 * widths[3] + 4 * D // 16 + 4 * (D // v_group)
+    payload_tok = 4 * sum(words) + 2 * widths[3] + 4 * D // 16
+    kscale = 4 * sum(widths[:3]) * (H // k_group)
+    total = n_kv * H * per_tok + n_kv * kscale + 4 * n_kv * R1 * D + 4 * n_q * D
+    return total, n_kv * H * payload_tok
+
+
+def build_state(cfg, layers, dev):
+    import torch
+
+    from logitfill_amd import synth
+    from logitfill_amd.packed import PackedKVManager
+
+    B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
+    pages, resid, tb = cfg["pages"], cfg["residual"], cfg["target_bit"]
+    levels = [synth.sample_tier_levels(n_kv, D, tb, seed=layer) for layer in range(layers)]
+    mgr = PackedKVManager(levels, n_q, n_kv, D, 128, 128, 128, 2, dev, batch_size=B,
+                          capacity_tokens=pages * 128)
+    inputs = []
+    for layer in range(layers):
+        d = synth.make_layer(B, n_q, n_kv, D, pages * 128 + resid, tb, seed=layer, device=dev)
+        st = mgr.layers[layer]
+        st.fill_pages(d.key, d.value, [pages] * B)
+        if resid:
+            st.set_tail(d.key[:, :, pages * 128:], d.value[:, :, pages * 128:], [resid] * B)
+        inputs.append((d.query.contiguous(), d.key_new.contiguous(), d.value_new.contiguous()))
+        del d
+        torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return mgr, inputs
+
+
+def time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split):
+    import torch
+
+    from logitfill_amd.packed.reference import decode_into
+
+    dev = mgr.device
+    outs = [torch.empty_like(q) for q, _, _ in inputs]
+    scaling = mgr.head_dim ** -0.5
+
+    def one_step():
+        for layer, (q, kn, vn) in enumerate(inputs):
+            decode_into(mgr, layer, q, kn, vn, scaling, outs[layer], kernel=kernel, pages_per_split=pages_per_split)
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        one_step()
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end)
+    return ms / steps, wall / steps * 1e3
+
+
+def cpu_baseline(cfg, n_seqs):
+    """The oracle's dense path (dequantise whole history, concatenate, repeat_kv, fp32
+    softmax attention) on one layer for ``n_seqs`` sequences, scaled to the batch."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from logitfill_amd import synth
+    from oracle import attention as oatt
+    from oracle import history as ohist
+
+    B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
+    pages, resid, tb = cfg["pages"], cfg["residual"], cfg["target_bit"]
+    cores = max(1, min(16, os.cpu_count() or 1))
+    times = []
+    with threadpool_limits(limits=cores):
+        for s in range(n_seqs):
+            d = synth.make_layer(1, n_q, n_kv, D, pages * 128 + resid, tb, seed=1000 + s)
+            key = d.key[0].float().numpy()
+            value = d.value[0].float().numpy()
+            store = ohist.pack_history(d.levels, key, value)
+            q = d.query[0].float().numpy()[:, None]
+            kn = d.key_new[0].float().numpy()[:, None]
+            vn = d.value_new[0].float().numpy()[:, None]
+            oatt.reference_attention(store, q, kn, vn, D ** -0.5, n_q, n_kv)      # warm-up
+            runs = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                oatt.reference_attention(store, q, kn, vn, D ** -0.5, n_q, n_kv, out_dtype="bf16")
+                runs.append(time.perf_counter() - t0)
+            times.append(float(np.median(runs)))
+    per_seq = float(np.mean(times))
+    return {"value": round(per_seq * B * 1e6, 1), "unit": "us/step/layer", "cores": cores, "kind": "port",
+            "sample": f"1 layer x {n_seqs} of {B} sequences at the full shape ({pages} pages + {resid} "
+                      f"residual + 1), median of 3 after 1 warm-up, scaled x{B // n_seqs if n_seqs else 0} "
+                      "to the batch; numpy float32 (BLAS threads = cores)"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of this "
+              "path is a design note, not a built component", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from logitfill_amd import _native, synth
+
+    cfg = dict(synth.CONFIGS[args.config])
+    layers = args.layers or cfg["layers"]
+    dev = torch.device("cuda", 0)
+    kernel = {"auto": _native.KERNEL_AUTO, "valu": _native.KERNEL_VALU, "mfma": _native.KERNEL_MFMA}[args.kernel]
+    print(f"[bench] building {layers} layers of {args.config} ...", file=sys.stderr, flush=True)
+    mgr, inputs = build_state(cfg, layers, dev)
+    print("[bench] timing ...", file=sys.stderr, flush=True)
+    ms_step, wall_ms = time_decode(mgr, inputs, args.steps, args.warmup, kernel, args.pages_per_split)
+
+    B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
+    H = cfg["pages"] * 128
+    R1 = cfg["residual"] + 1
+    tot_bytes = 0
+    pay_bytes = 0
+    for st in mgr.layers:
+        t, p = algorithmic_bytes(st.widths, st.words, n_kv, n_q, D, H, R1)
+        tot_bytes += t * B
+        pay_bytes += p * B
+    us_layer = ms_step * 1e3 / layers
+    launch_s = ms_step / 1e3 / layers
+    bytes_launch = tot_bytes / layers
+    achieved = bytes_launch / launch_s / 1e9
+    result = {
+        "metric": "packed decode-attn us/step + achieved HBM GB/s (% of peak), 7B GQA shape @32K ctx",
+        "value": round(us_layer, 2),
+        "unit": "us/step/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic (seeded logitfill_amd.synth: K~N(0,1)*LogNormal channel scale + outliers, V,Q~N)",
+        "config": {"workload": f"{args.config}: packed decode attention, {layers} layers x batch {B}, "
+                               f"{n_q}q/{n_kv}kv heads, D {D}, {cfg['pages']} pages + {cfg['residual']} residual, "
+                               f"target_bit {cfg['target_bit']}",
+                   "kernel": args.kernel, "layers": layers, "batch": B},
+        "hbm_gbs": round(achieved, 1),
+        "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+        "payload_gbs": round(pay_bytes / layers / launch_s / 1e9, 1),
+        "bytes_per_layer_step": int(bytes_launch),
+        "wall_ms_per_step": round(wall_ms, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seqs)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,186 @@
+/*
+ * logitfill_amd -- C ABI of the MI355X (gfx950) packed KV decode path.
+ *
+ * Replaces the reference's single native entry point, the pybind11/torch
+ * function ``logitfill_decode`` (reference src/logitfill/packed/kernel.cu:198-284,
+ * JIT-loaded by src/logitfill/packed/kernel_loader.py:14-35), and moves the
+ * reference's Python/torch page packer (src/logitfill/packed/layout.py:71-129,
+ * called from src/logitfill/packed/cache.py:64-81) onto the device.
+ *
+ * Conventions
+ *  - Plain C: device pointers, sizes and strides only; no torch types.
+ *  - The caller owns every buffer, including outputs and workspaces; the
+ *    library never allocates device memory and keeps no global state.
+ *  - ``stream`` is a hipStream_t passed as ``void*`` (NULL = default stream).
+ *    Nothing synchronises inside; all work is enqueued on ``stream``.
+ *  - Return value: 0 = success; negative = argument/shape error (LF_E_*),
+ *    nothing enqueued; positive = hipError_t of a failed launch.
+ *  - Float16 data is passed as ``uint16_t`` bit patterns.
+ */
+#ifndef LOGITFILL_AMD_H
+#define LOGITFILL_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LF_ABI_VERSION 1
+
+/* Element types of query / residual / output tensors. */
+enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
+
+/* Status codes (negative: rejected before launch). */
+enum lf_status {
+    LF_OK = 0,
+    LF_E_NULL = -1,          /* a required pointer is NULL                     */
+    LF_E_SHAPE = -2,         /* sizes inconsistent or out of supported range    */
+    LF_E_UNSUPPORTED = -3,   /* valid but not implemented (e.g. bit_v != 2)     */
+    LF_E_WORKSPACE = -4,     /* workspace too small                             */
+    LF_E_DTYPE = -5          /* unknown dtype code                              */
+};
+
+/*
+ * One layer's packed history for ``batch`` sequences, in the reference byte
+ * layout (src/logitfill/packed/cache.py:64-81 and layout.py:71-129) with a
+ * capacity stride on the growing axis:
+ *
+ *   k_code[t]   int32 [batch][n_kv][cap_tokens][k_words[t]]     t = 0,1,2 (int2/int4/int8)
+ *   k_scale[t]  fp16  [batch][n_kv][k_width[t]][cap_kgroups]    (page/group index innermost)
+ *   k_min[t]    fp16  [batch][n_kv][k_width[t]][cap_kgroups]
+ *   k_value16   fp16  [batch][n_kv][cap_tokens][k_width[3]]     (fp16 tier)
+ *   v_code      int32 [batch][n_kv][cap_tokens][v_words]        (bit_v < 16)
+ *   v_scale     fp16  [batch][n_kv][cap_tokens][v_groups]       (bit_v < 16)
+ *   v_min       fp16  [batch][n_kv][cap_tokens][v_groups]       (bit_v < 16)
+ *   v_value16   fp16  [batch][n_kv][cap_tokens][head_dim]       (bit_v >= 16)
+ *
+ * Sequence b's reference tensors are the slices [b][:, :hist_len, :] (codes,
+ * values) and [b][:, :, :hist_len/k_group] (Key scale/min).  The tier table
+ * (src/logitfill/packed/layout.py:49-68) is passed as ``tier_index[t]``
+ * int32 [n_kv][k_width[t]] (ascending channel ids, zero padded) and
+ * ``tier_count[t]`` int32 [n_kv].  Pointers of empty tiers may be NULL.
+ */
+typedef struct lf_packed_layer {
+    int32_t*  k_code[3];
+    uint16_t* k_scale[3];
+    uint16_t* k_min[3];
+    uint16_t* k_value16;
+    int32_t*  v_code;
+    uint16_t* v_scale;
+    uint16_t* v_min;
+    uint16_t* v_value16;
+    const int32_t* tier_index[4];
+    const int32_t* tier_count[4];
+    int32_t batch, n_kv, head_dim;
+    int32_t cap_tokens, cap_kgroups;
+    int32_t page_size, k_group, v_group, bit_v;
+    int32_t k_width[4];
+    int32_t k_words[3];
+    int32_t v_words, v_groups;
+} lf_packed_layer;
+
+/* ABI version (LF_ABI_VERSION) and a static build string. */
+int32_t lf_abi_version(void);
+const char* lf_build_info(void);
+const char* lf_status_string(int32_t status);
+
+/*
+ * Page compress.  Replaces quantize_key_page + quantize_value_page + the
+ * history concatenation of _LayerStore._flush
+ * (reference src/logitfill/packed/layout.py:71-129, cache.py:64-81).
+ *
+ * Packs ``n_jobs`` pages.  ``jobs`` is a DEVICE int32 array [n_jobs][3] of
+ * (b, src_token0, dst_page): the page is rows src_token0 .. src_token0 +
+ * page_size - 1 of sequence b of ``k_src``/``v_src`` (element strides
+ * src_stride_b/h/t, channel stride 1, dtype ``src_dtype``) and is written as
+ * page ``dst_page`` of sequence b of ``layer``.  Codes, scales and mins are
+ * bit-exact with the reference packer on finite inputs.
+ */
+int32_t lf_pack_pages(const lf_packed_layer* layer,
+                      const void* k_src, const void* v_src, int32_t src_dtype,
+                      int64_t src_stride_b, int64_t src_stride_h, int64_t src_stride_t,
+                      const int32_t* jobs, int32_t n_jobs, void* stream);
+
+/*
+ * Decode work plan (host function, no device access).  Splits each
+ * sequence's ``hist_pages[b]`` packed pages into items of at most
+ * ``pages_per_split`` pages, plus one residual item per sequence (tail page
+ * + new token).  Writes ``work_out`` [n][4] = (b, page_begin, page_end, kind)
+ * (kind 0 = packed pages, 1 = residual) and ``seq_work_out`` [batch][2] =
+ * (first item, item count).  Returns the item count n, or a negative
+ * LF_E_* when ``work_cap`` is too small.  Both arrays must be copied to the
+ * device before lf_decode_attention.
+ */
+int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split,
+                       int32_t* work_out, int32_t work_cap, int32_t* seq_work_out);
+
+/* Decode-attention call arguments (see lf_decode_attention). */
+typedef struct lf_decode_args {
+    const void* query;  int32_t q_dtype;      /* [batch][n_q][head_dim]                 */
+    const void* k_new;  const void* v_new;    /* [batch][n_kv][head_dim] or both NULL   */
+    int32_t new_dtype;
+    const void* tail_k; const void* tail_v;   /* [batch][n_kv][tail_cap][head_dim]      */
+    int32_t tail_dtype, tail_cap;
+    const int32_t* tail_len;                  /* device int32 [batch]                   */
+    void* out; int32_t out_dtype;             /* [batch][n_q][head_dim]                 */
+    int32_t n_q;
+    float scaling;                            /* softmax scale (reference: attn.scaling) */
+    const int32_t* work;  int32_t n_work;     /* device, from lf_plan_decode            */
+    const int32_t* seq_work;                  /* device, from lf_plan_decode            */
+    void* workspace; int64_t workspace_bytes; /* >= lf_decode_workspace_bytes(); its
+                                                 counter area must be zero before the
+                                                 first call (calls leave it zero)       */
+    int32_t kernel;                           /* 0 auto, 1 VALU, 2 MFMA                 */
+} lf_decode_args;
+
+/* Workspace bytes for lf_decode_attention with ``n_work`` items. */
+int64_t lf_decode_workspace_bytes(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim,
+                                  int32_t n_work);
+/* Byte offset, inside the workspace, of the int32 counters [batch][n_kv] that must
+ * start zeroed (always 0: the counters come first, the partials follow). */
+int64_t lf_decode_counter_offset(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim,
+                                 int32_t n_work);
+
+/*
+ * Decode attention for one new query token per sequence.  Replaces
+ * logitfill_decode (reference src/logitfill/packed/kernel.cu:112-280) and the
+ * dense fallback it protects (src/logitfill/packed/reference.py:30-56):
+ *
+ *   out[b, i] = softmax(scaling * q[b,i] . K_b^T) V_b,
+ *   K_b = [dequant(history_b) ; tail_k[b, :, :tail_len[b]] ; k_new[b]]  (V likewise),
+ *
+ * with q head i reading kv head i / (n_q / n_kv).  Split-K over packed pages
+ * plus a fused cross-split softmax merge; accumulation in fp32; output
+ * rounded to ``out_dtype``.  Requires bit_v == 2 (as the reference kernel,
+ * reference.py:62) and n_q % n_kv == 0.
+ */
+int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* args, void* stream);
+
+/*
+ * Dense fp32 dequantisation of sequence b's first ``tokens`` history tokens
+ * (reference src/logitfill/packed/layout.py:132-182, cache.py:83-90):
+ * k_out, v_out fp32 [n_kv][tokens][head_dim], contiguous.
+ */
+int32_t lf_dequantize(const lf_packed_layer* layer, int32_t b, int32_t tokens,
+                      float* k_out, float* v_out, void* stream);
+
+/*
+ * BF16 dense decode attention (comparator; no reference counterpart): the
+ * same split-K/merge over bf16 K/V [batch][n_kv][tokens][head_dim] (element
+ * strides kv_stride_b/h/t), query bf16 [batch][n_q][head_dim], out bf16.
+ * Workspace as lf_dense_decode_workspace_bytes().
+ */
+int64_t lf_dense_decode_workspace_bytes(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim,
+                                        int32_t tokens, int32_t tokens_per_split);
+int32_t lf_dense_decode(const void* query, const void* k, const void* v,
+                        int32_t batch, int32_t n_q, int32_t n_kv, int32_t head_dim, int32_t tokens,
+                        int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_t,
+                        float scaling, void* out, int32_t tokens_per_split,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOGITFILL_AMD_H */

@@ -1,0 +1,146 @@
+"""ctypes binding of ``liblogitfill_amd.so`` (C ABI in ``include/logitfill_amd.h``).
+
+The library is loaded lazily and only after ``torch`` is imported, so that its
+``libamdhip64.so.7`` dependency binds to the HIP runtime torch already loaded
+(one runtime, one set of streams per process).  A missing library raises
+``NativeLibraryMissing``; there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("liblogitfill_amd.so")
+
+LF_BF16, LF_FP16, LF_FP32 = 0, 1, 2
+KERNEL_AUTO, KERNEL_VALU, KERNEL_MFMA = 0, 1, 2
+
+
+class NativeLibraryMissing(RuntimeError):
+    """The HIP extension is not built; run ``python -m logitfill_amd.build``."""
+
+
+class LFError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, status: int, message: str, call: str):
+        super().__init__(f"{call} failed with status {status}: {message}")
+        self.status = status
+
+
+class PackedLayer(ctypes.Structure):
+    """``lf_packed_layer``."""
+
+    _fields_ = [
+        ("k_code", c_void_p * 3),
+        ("k_scale", c_void_p * 3),
+        ("k_min", c_void_p * 3),
+        ("k_value16", c_void_p),
+        ("v_code", c_void_p),
+        ("v_scale", c_void_p),
+        ("v_min", c_void_p),
+        ("v_value16", c_void_p),
+        ("tier_index", c_void_p * 4),
+        ("tier_count", c_void_p * 4),
+        ("batch", c_int32),
+        ("n_kv", c_int32),
+        ("head_dim", c_int32),
+        ("cap_tokens", c_int32),
+        ("cap_kgroups", c_int32),
+        ("page_size", c_int32),
+        ("k_group", c_int32),
+        ("v_group", c_int32),
+        ("bit_v", c_int32),
+        ("k_width", c_int32 * 4),
+        ("k_words", c_int32 * 3),
+        ("v_words", c_int32),
+        ("v_groups", c_int32),
+    ]
+
+
+class DecodeArgs(ctypes.Structure):
+    """``lf_decode_args``."""
+
+    _fields_ = [
+        ("query", c_void_p), ("q_dtype", c_int32),
+        ("k_new", c_void_p), ("v_new", c_void_p),
+        ("new_dtype", c_int32),
+        ("tail_k", c_void_p), ("tail_v", c_void_p),
+        ("tail_dtype", c_int32), ("tail_cap", c_int32),
+        ("tail_len", c_void_p),
+        ("out", c_void_p), ("out_dtype", c_int32),
+        ("n_q", c_int32),
+        ("scaling", c_float),
+        ("work", c_void_p), ("n_work", c_int32),
+        ("seq_work", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_int64),
+        ("kernel", c_int32),
+    ]
+
+
+_SIGNATURES = {
+    "lf_abi_version": (c_int32, []),
+    "lf_build_info": (c_char_p, []),
+    "lf_status_string": (c_char_p, [c_int32]),
+    "lf_pack_pages": (c_int32, [POINTER(PackedLayer), c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64,
+                                c_void_p, c_int32, c_void_p]),
+    "lf_plan_decode": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
+    "lf_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "lf_decode_counter_offset": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "lf_decode_attention": (c_int32, [POINTER(PackedLayer), POINTER(DecodeArgs), c_void_p]),
+    "lf_dequantize": (c_int32, [POINTER(PackedLayer), c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "lf_dense_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "lf_dense_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                  c_int64, c_int64, c_int64, c_float, c_void_p, c_int32, c_void_p, c_int64,
+                                  c_void_p]),
+}
+
+ABI_VERSION = 1
+_LIB = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the library (once).  Raises ``NativeLibraryMissing`` when it is not built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    import torch  # noqa: F401  -- binds libamdhip64.so.7 to torch's HIP runtime first
+
+    if not LIB_PATH.exists():
+        raise NativeLibraryMissing(
+            f"{LIB_PATH} is missing: build it with `python -m logitfill_amd.build` "
+            "(the packed path has no CPU fallback)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if lib.lf_abi_version() != ABI_VERSION:
+        raise NativeLibraryMissing(f"{LIB_PATH} has ABI {lib.lf_abi_version()}, expected {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def check(status: int, call: str) -> None:
+    if status != 0:
+        msg = load().lf_status_string(status)
+        raise LFError(status, msg.decode() if msg else "?", call)
+
+
+def dtype_code(dtype) -> int:
+    import torch
+
+    if dtype == torch.bfloat16:
+        return LF_BF16
+    if dtype == torch.float16:
+        return LF_FP16
+    if dtype == torch.float32:
+        return LF_FP32
+    raise TypeError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32")
+
+
+def current_stream_ptr(device) -> int:
+    import torch
+
+    return int(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,75 @@
+"""Build ``liblogitfill_amd.so`` in-tree with hipcc for gfx950.
+
+Every ``csrc/*.hip`` file is compiled to an object under ``logitfill_amd/_build``
+and linked into ``logitfill_amd/liblogitfill_amd.so``; the C ABI is declared in
+``include/logitfill_amd.h``.  Run ``python -m logitfill_amd.build``.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "liblogitfill_amd.so"
+ARCH = os.environ.get("LOGITFILL_AMD_ARCH", "gfx950")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 (hipcc's host pass warns that it
+# does not know the feature; the device pass applies it).
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-result",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-mcode-object-version=5",
+    f"-I{PKG.parent / 'include'}",
+]
+
+
+def _compile(src: Path) -> tuple[Path, str]:
+    obj = BUILD / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    log = "\n".join(
+        line for line in (proc.stdout + proc.stderr).splitlines()
+        if "packed-fp32-ops" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{log}")
+    return obj, log
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile all sources and link the shared library; returns its path."""
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2) // 2), 8)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        results = list(pool.map(_compile, sources))
+    for obj, log in results:
+        if verbose and log.strip():
+            print(f"[{obj.name}]\n{log}", file=sys.stderr)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-mcode-object-version=5", "-shared", "-fPIC", "-o", str(tmp),
+           *[str(o) for o, _ in results]]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    path = build(verbose=True)
+    print(path)

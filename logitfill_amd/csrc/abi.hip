@@ -1,0 +1,213 @@
+// extern "C" entry points of liblogitfill_amd.so (declared in include/logitfill_amd.h).
+//
+// Validation happens here, before anything is enqueued: a negative LF_E_* code
+// means nothing ran.  The library keeps no state and allocates nothing.
+#include "decode_common.hpp"
+
+namespace lf {
+int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v_src, int src_dtype,
+                      int64_t sb, int64_t sh, int64_t st, const int32_t* jobs, int n_jobs,
+                      hipStream_t stream);
+int launch_decode_valu(const DecodeParams& p, hipStream_t stream);
+int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled);
+int launch_dequantize(const lf_packed_layer& L, int b, int tokens, float* k_out, float* v_out,
+                      hipStream_t stream);
+int launch_dense_decode(const void* query, const void* k, const void* v, int batch, int n_q, int n_kv,
+                        int head_dim, int tokens, int64_t sb, int64_t sh, int64_t st, float scaling,
+                        void* out, int tokens_per_split, void* workspace, hipStream_t stream);
+int64_t dense_workspace_bytes(int batch, int n_kv, int n_q, int head_dim, int tokens, int tokens_per_split);
+}  // namespace lf
+
+namespace {
+
+bool valid_dtype(int32_t d) { return d == LF_BF16 || d == LF_FP16 || d == LF_FP32; }
+
+// Shape and pointer checks shared by every entry point that reads a layer.
+// ``need_k`` / ``need_v``: validate the Key tiers / the Value arrays.
+int32_t check_layer(const lf_packed_layer* L, bool need_k = true, bool need_v = true) {
+    if (!L) return LF_E_NULL;
+    if (L->batch <= 0 || L->n_kv <= 0 || L->head_dim <= 0 || L->page_size <= 0 || L->k_group <= 0)
+        return LF_E_SHAPE;
+    if (L->page_size % L->k_group != 0) return LF_E_SHAPE;
+    if (L->cap_tokens < 0 || L->cap_kgroups < 0) return LF_E_SHAPE;
+    if (static_cast<int64_t>(L->cap_kgroups) * L->k_group < L->cap_tokens) return LF_E_SHAPE;
+    if (need_k) {
+        int wsum = 0;
+        for (int t = 0; t < 4; ++t) {
+            if (L->k_width[t] < 0 || L->k_width[t] > L->head_dim) return LF_E_SHAPE;
+            wsum += L->k_width[t];
+            if (L->k_width[t] > 0 && (!L->tier_index[t] || !L->tier_count[t])) return LF_E_NULL;
+        }
+        if (wsum < L->head_dim) return LF_E_SHAPE;  // every channel has a tier
+        for (int t = 0; t < 3; ++t) {
+            const int per = 32 / (2 << t);
+            if (L->k_words[t] != (L->k_width[t] + per - 1) / per) return LF_E_SHAPE;
+            if (L->k_width[t] > 0 && (!L->k_code[t] || !L->k_scale[t] || !L->k_min[t])) return LF_E_NULL;
+        }
+        if (L->k_width[3] > 0 && !L->k_value16) return LF_E_NULL;
+    }
+    if (need_v) {
+        if (L->bit_v >= 16) {
+            if (!L->v_value16) return LF_E_NULL;
+        } else {
+            if (L->bit_v != 2 && L->bit_v != 4 && L->bit_v != 8) return LF_E_SHAPE;
+            if (L->v_group <= 0 || L->head_dim % L->v_group != 0) return LF_E_SHAPE;
+            if (L->v_groups != L->head_dim / L->v_group) return LF_E_SHAPE;
+            if ((L->head_dim * L->bit_v) % 32 != 0 || L->v_words != L->head_dim * L->bit_v / 32) return LF_E_SHAPE;
+            if (!L->v_code || !L->v_scale || !L->v_min) return LF_E_NULL;
+        }
+    }
+    return LF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t lf_abi_version(void) { return LF_ABI_VERSION; }
+
+const char* lf_build_info(void) {
+    return "logitfill_amd " __DATE__ " " __TIME__ " gfx950 wave64";
+}
+
+const char* lf_status_string(int32_t status) {
+    switch (status) {
+        case LF_OK: return "ok";
+        case LF_E_NULL: return "a required pointer is NULL";
+        case LF_E_SHAPE: return "inconsistent or unsupported shape";
+        case LF_E_UNSUPPORTED: return "configuration not implemented";
+        case LF_E_WORKSPACE: return "workspace too small";
+        case LF_E_DTYPE: return "unknown dtype code";
+        default: break;
+    }
+    return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown status";
+}
+
+int32_t lf_pack_pages(const lf_packed_layer* layer, const void* k_src, const void* v_src, int32_t src_dtype,
+                      int64_t src_stride_b, int64_t src_stride_h, int64_t src_stride_t,
+                      const int32_t* jobs, int32_t n_jobs, void* stream) {
+    const int32_t st = check_layer(layer);
+    if (st != LF_OK) return st;
+    if (!valid_dtype(src_dtype)) return LF_E_DTYPE;
+    if (n_jobs < 0) return LF_E_SHAPE;
+    if (n_jobs == 0) return LF_OK;
+    if (!k_src || !v_src || !jobs) return LF_E_NULL;
+    if (layer->page_size > 1024 || layer->head_dim > 512) return LF_E_SHAPE;
+    return lf::launch_pack_pages(*layer, k_src, v_src, src_dtype, src_stride_b, src_stride_h, src_stride_t,
+                                 jobs, n_jobs, static_cast<hipStream_t>(stream));
+}
+
+int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split,
+                       int32_t* work_out, int32_t work_cap, int32_t* seq_work_out) {
+    if (!hist_pages || !work_out || !seq_work_out) return LF_E_NULL;
+    if (batch <= 0 || pages_per_split <= 0) return LF_E_SHAPE;
+    int32_t n = 0;
+    for (int32_t b = 0; b < batch; ++b) {
+        const int32_t pages = hist_pages[b];
+        if (pages < 0) return LF_E_SHAPE;
+        const int32_t first = n;
+        for (int32_t p0 = 0; p0 < pages; p0 += pages_per_split) {
+            if (n >= work_cap) return LF_E_WORKSPACE;
+            const int32_t p1 = p0 + pages_per_split < pages ? p0 + pages_per_split : pages;
+            work_out[4 * n + 0] = b;
+            work_out[4 * n + 1] = p0;
+            work_out[4 * n + 2] = p1;
+            work_out[4 * n + 3] = 0;
+            ++n;
+        }
+        if (n >= work_cap) return LF_E_WORKSPACE;
+        work_out[4 * n + 0] = b;
+        work_out[4 * n + 1] = 0;
+        work_out[4 * n + 2] = 0;
+        work_out[4 * n + 3] = 1;
+        ++n;
+        seq_work_out[2 * b + 0] = first;
+        seq_work_out[2 * b + 1] = n - first;
+    }
+    return n;
+}
+
+int64_t lf_decode_workspace_bytes(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim, int32_t n_work) {
+    return lf::decode_workspace_total(batch, n_kv, n_q, head_dim, n_work);
+}
+
+int64_t lf_decode_counter_offset(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim, int32_t n_work) {
+    (void)batch;
+    (void)n_kv;
+    (void)n_q;
+    (void)head_dim;
+    (void)n_work;
+    return 0;
+}
+
+int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* args, void* stream) {
+    const int32_t st = check_layer(layer);
+    if (st != LF_OK) return st;
+    if (!args) return LF_E_NULL;
+    const lf_decode_args& A = *args;
+    if (!A.query || !A.out || !A.work || !A.seq_work || !A.workspace || !A.tail_len) return LF_E_NULL;
+    if ((A.k_new == nullptr) != (A.v_new == nullptr)) return LF_E_NULL;
+    if (!valid_dtype(A.q_dtype) || !valid_dtype(A.out_dtype) || !valid_dtype(A.tail_dtype)) return LF_E_DTYPE;
+    if (A.k_new && !valid_dtype(A.new_dtype)) return LF_E_DTYPE;
+    if (A.n_q <= 0 || A.n_q % layer->n_kv != 0) return LF_E_SHAPE;
+    const int g = A.n_q / layer->n_kv;
+    if (g > 16) return LF_E_UNSUPPORTED;
+    if (layer->bit_v != 2) return LF_E_UNSUPPORTED;  // as reference.py:62
+    const int D = layer->head_dim;
+    if (D != 64 && D != 128 && D != 256) return LF_E_UNSUPPORTED;
+    if (layer->v_groups > 8) return LF_E_UNSUPPORTED;
+    if (A.tail_cap < 0 || (A.tail_cap > 0 && (!A.tail_k || !A.tail_v))) return LF_E_NULL;
+    if (A.n_work <= 0) return LF_E_SHAPE;
+    if (A.workspace_bytes < lf_decode_workspace_bytes(layer->batch, layer->n_kv, A.n_q, D, A.n_work))
+        return LF_E_WORKSPACE;
+    if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
+
+    lf::DecodeParams p;
+    p.L = *layer;
+    p.A = A;
+    p.g = g;
+    p.qscale = A.scaling * lf::kLog2e;
+    p.counters = static_cast<int*>(A.workspace);
+    p.part = reinterpret_cast<float*>(static_cast<char*>(A.workspace) +
+                                      lf::decode_part_offset_bytes(layer->batch, layer->n_kv));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (A.kernel != 1) {
+        bool handled = false;
+        const int r = lf::launch_decode_mfma(p, s, &handled);
+        if (handled || A.kernel == 2) return handled ? r : LF_E_UNSUPPORTED;
+    }
+    return lf::launch_decode_valu(p, s);
+}
+
+int32_t lf_dequantize(const lf_packed_layer* layer, int32_t b, int32_t tokens, float* k_out, float* v_out,
+                      void* stream) {
+    if (!k_out && !v_out) return LF_E_NULL;
+    const int32_t st = check_layer(layer, k_out != nullptr, v_out != nullptr);
+    if (st != LF_OK) return st;
+    if (b < 0 || b >= layer->batch || tokens < 0 || tokens > layer->cap_tokens) return LF_E_SHAPE;
+    if (tokens == 0) return LF_OK;
+    return lf::launch_dequantize(*layer, b, tokens, k_out, v_out, static_cast<hipStream_t>(stream));
+}
+
+int64_t lf_dense_decode_workspace_bytes(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim,
+                                        int32_t tokens, int32_t tokens_per_split) {
+    return lf::dense_workspace_bytes(batch, n_kv, n_q, head_dim, tokens, tokens_per_split);
+}
+
+int32_t lf_dense_decode(const void* query, const void* k, const void* v, int32_t batch, int32_t n_q,
+                        int32_t n_kv, int32_t head_dim, int32_t tokens, int64_t kv_stride_b,
+                        int64_t kv_stride_h, int64_t kv_stride_t, float scaling, void* out,
+                        int32_t tokens_per_split, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!query || !k || !v || !out || !workspace) return LF_E_NULL;
+    if (batch <= 0 || n_kv <= 0 || n_q <= 0 || n_q % n_kv != 0 || tokens <= 0) return LF_E_SHAPE;
+    if (n_q / n_kv > 16) return LF_E_UNSUPPORTED;
+    if (head_dim != 128) return LF_E_UNSUPPORTED;
+    if (tokens_per_split <= 0 || tokens_per_split % 64 != 0) return LF_E_SHAPE;
+    if (workspace_bytes < lf::dense_workspace_bytes(batch, n_kv, n_q, head_dim, tokens, tokens_per_split))
+        return LF_E_WORKSPACE;
+    return lf::launch_dense_decode(query, k, v, batch, n_q, n_kv, head_dim, tokens, kv_stride_b, kv_stride_h,
+                                   kv_stride_t, scaling, out, tokens_per_split, workspace,
+                                   static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

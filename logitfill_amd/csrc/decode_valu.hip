@@ -1,0 +1,283 @@
+// Packed decode attention, vector-ALU variant (fp32 FMA, one wave per work item).
+//
+// Reference: logitfill_decode_kernel, src/logitfill/packed/kernel.cu:112-190
+// (dequantise Key through the tier map, int2 Value, online softmax), with the
+// dense semantics of src/logitfill/packed/reference.py:30-56.  Differences in
+// structure: one wave serves all g query heads of a kv head so the packed
+// bytes are read once per kv head (the reference re-reads them per query head);
+// the history is split across workgroups (split-K) and merged by the last one.
+//
+// Per 64-token chunk a lane owns one token for the scores and one or more
+// channels for the value accumulation.  The Key scale is folded into the
+// query once per Key group:
+//     score_i = sum_c q_ic (code_c s_c + m_c) = sum_slot (q s)_slot code_slot + sum_c q_ic m_c
+// This kernel is the general path (any g <= 16, D in {64,128,256}); the MFMA
+// kernel covers the fast shapes.
+#include "decode_common.hpp"
+
+namespace lf {
+namespace {
+
+constexpr int kMaxG = 16;
+
+template <int D>
+struct ValuSmem {
+    float qT[D][kMaxG];          // q * scaling * log2(e), channel-major
+    float p[64][kMaxG];          // probabilities of the current chunk
+    float vsc[64][8];            // V scale per token and channel group
+    float vmn[64][8];            // V min
+    uint32_t vcode[64][D / 16];  // V codes of the chunk
+    int flag;
+};
+
+__device__ __forceinline__ int slot_tier(const int* off, int slot) {
+    return slot < off[1] ? 0 : slot < off[2] ? 1 : slot < off[3] ? 2 : 3;
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
+    const lf_packed_layer& L = p.L;
+    const lf_decode_args& A = p.A;
+    const int item = blockIdx.x;
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int g = p.g;
+    const int* w4 = A.work + 4 * item;
+    const int b = w4[0];
+    const int pbeg = w4[1], pend = w4[2], kind = w4[3];
+
+    __shared__ ValuSmem<D> sm;
+    extern __shared__ float qp[];  // [n_slots][kMaxG]  (dynamic)
+
+    // q, pre-scaled into the log2 domain.
+    for (int idx = lane; idx < kMaxG * D; idx += 64) {
+        const int i = idx / D, c = idx % D;
+        float v = 0.f;
+        if (i < g) v = load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + i) * D + c, A.q_dtype);
+        sm.qT[c][i] = v * p.qscale;
+    }
+    __syncthreads();
+
+    int off[4];
+    off[0] = 0;
+    off[1] = L.k_width[0];
+    off[2] = off[1] + L.k_width[1];
+    off[3] = off[2] + L.k_width[2];
+    const int n_slots = off[3] + L.k_width[3];
+
+    float m[kMaxG], lsum[kMaxG];
+    constexpr int CPL = D / 64;  // channels per lane
+    float o[CPL][kMaxG];
+#pragma unroll
+    for (int i = 0; i < kMaxG; ++i) {
+        m[i] = -__builtin_inff();
+        lsum[i] = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) o[cc][i] = 0.f;
+    }
+
+    // Online-softmax update with this lane's scores; publishes p into LDS.
+    auto softmax_step = [&](float* score, bool active, float* alpha) {
+#pragma unroll
+        for (int i = 0; i < kMaxG; ++i) {
+            if (i < g) {
+                const float s = active ? score[i] : -__builtin_inff();
+                const float mnew = fmaxf(m[i], wave_max(s));
+                alpha[i] = __builtin_amdgcn_exp2f(m[i] - mnew);
+                const float pi = active ? __builtin_amdgcn_exp2f(s - mnew) : 0.f;
+                lsum[i] = lsum[i] * alpha[i] + pi;
+                m[i] = mnew;
+                sm.p[lane][i] = pi;
+            }
+        }
+    };
+
+    if (kind == 0) {
+        const int kg = L.k_group;
+        const int chunk = kg < 64 ? kg : 64;
+        const int vgs = L.v_groups;
+        const int64_t tok_end = static_cast<int64_t>(pend) * L.page_size;
+        for (int64_t tok = static_cast<int64_t>(pbeg) * L.page_size; tok < tok_end; tok += kg) {
+            const int64_t kgi = tok / kg;
+            {
+                // Fold this Key group's scale into q; collect sum_c q_c m_c.
+                float bias[kMaxG];
+#pragma unroll
+                for (int i = 0; i < kMaxG; ++i) bias[i] = 0.f;
+                __syncthreads();
+                for (int slot = lane; slot < n_slots; slot += 64) {
+                    const int t = slot_tier(off, slot);
+                    const int j = slot - off[t];
+                    const int cnt = L.tier_count[t][h];
+                    float* row = qp + slot * kMaxG;
+                    if (j >= cnt) {
+#pragma unroll
+                        for (int i = 0; i < kMaxG; ++i) row[i] = 0.f;
+                        continue;
+                    }
+                    const int c = L.tier_index[t][h * L.k_width[t] + j];
+                    if (t == 3) {
+#pragma unroll
+                        for (int i = 0; i < kMaxG; ++i) row[i] = sm.qT[c][i];
+                    } else {
+                        const int64_t gi = kgrp_idx(L, b, h, L.k_width[t], j, kgi);
+                        const float s = f16_to_f32(L.k_scale[t][gi]);
+                        const float mn = f16_to_f32(L.k_min[t][gi]);
+#pragma unroll
+                        for (int i = 0; i < kMaxG; ++i) {
+                            row[i] = sm.qT[c][i] * s;
+                            bias[i] += sm.qT[c][i] * mn;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < kMaxG; ++i) bias[i] = wave_sum(bias[i]);
+                __syncthreads();
+                // Process the group's chunks.
+                for (int64_t t0 = tok; t0 < tok + kg; t0 += chunk) {
+                    const bool active = lane < chunk;
+                    const int64_t row = tok_row(L, b, h, t0 + (active ? lane : 0));
+                    float score[kMaxG];
+#pragma unroll
+                    for (int i = 0; i < kMaxG; ++i) score[i] = bias[i];
+                    for (int t = 0; t < 3; ++t) {
+                        const int words = L.k_words[t];
+                        const int bits = 2 << t;
+                        const int per = 32 / bits;
+                        const uint32_t mask = (1u << bits) - 1u;
+                        const int width = L.k_width[t];
+                        for (int w = 0; w < words; ++w) {
+                            const uint32_t word = static_cast<uint32_t>(L.k_code[t][row * words + w]);
+                            const int kmax = min(per, width - w * per);
+                            for (int k = 0; k < kmax; ++k) {
+                                const float cf = static_cast<float>((word >> (k * bits)) & mask);
+                                const float* qrow = qp + (off[t] + w * per + k) * kMaxG;
+#pragma unroll
+                                for (int i = 0; i < kMaxG; ++i)
+                                    if (i < g) score[i] = fmaf(qrow[i], cf, score[i]);
+                            }
+                        }
+                    }
+                    for (int j = 0; j < L.k_width[3]; ++j) {
+                        const float v = f16_to_f32(L.k_value16[row * L.k_width[3] + j]);
+                        const float* qrow = qp + (off[3] + j) * kMaxG;
+#pragma unroll
+                        for (int i = 0; i < kMaxG; ++i)
+                            if (i < g) score[i] = fmaf(qrow[i], v, score[i]);
+                    }
+                    float alpha[kMaxG];
+                    softmax_step(score, active, alpha);
+                    if (active) {
+                        for (int vg = 0; vg < vgs; ++vg) {
+                            sm.vsc[lane][vg] = f16_to_f32(L.v_scale[row * vgs + vg]);
+                            sm.vmn[lane][vg] = f16_to_f32(L.v_min[row * vgs + vg]);
+                        }
+                        for (int w = 0; w < D / 16; ++w)
+                            sm.vcode[lane][w] = static_cast<uint32_t>(L.v_code[row * L.v_words + w]);
+                    }
+                    __syncthreads();
+#pragma unroll
+                    for (int cc = 0; cc < CPL; ++cc) {
+                        const int c = lane + 64 * cc;
+                        const int vg = c / L.v_group;
+#pragma unroll
+                        for (int i = 0; i < kMaxG; ++i) o[cc][i] *= alpha[i];
+                        for (int tt = 0; tt < chunk; ++tt) {
+                            const uint32_t code = (sm.vcode[tt][c >> 4] >> (2 * (c & 15))) & 3u;
+                            const float v = static_cast<float>(code) * sm.vsc[tt][vg] + sm.vmn[tt][vg];
+#pragma unroll
+                            for (int i = 0; i < kMaxG; ++i)
+                                if (i < g) o[cc][i] = fmaf(sm.p[tt][i], v, o[cc][i]);
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+        }
+    } else {
+        // Residual: the BF16 tail page then the new token (reference.py:35-44).
+        const int tl = A.tail_len[b];
+        const int has_new = A.k_new != nullptr;
+        const int n_res = tl + has_new;
+        for (int t0 = 0; t0 < n_res; t0 += 64) {
+            const int tt_lane = t0 + lane;
+            const bool active = tt_lane < n_res;
+            const void* kp;
+            int64_t kbase;
+            int kdt;
+            if (tt_lane < tl) {
+                kp = A.tail_k;
+                kbase = ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + tt_lane) * D;
+                kdt = A.tail_dtype;
+            } else {
+                kp = A.k_new;
+                kbase = (static_cast<int64_t>(b) * L.n_kv + h) * D;
+                kdt = A.new_dtype;
+            }
+            float score[kMaxG];
+#pragma unroll
+            for (int i = 0; i < kMaxG; ++i) score[i] = 0.f;
+            if (active) {
+                for (int c = 0; c < D; ++c) {
+                    const float k = load_as_f32(kp, kbase + c, kdt);
+#pragma unroll
+                    for (int i = 0; i < kMaxG; ++i)
+                        if (i < g) score[i] = fmaf(sm.qT[c][i], k, score[i]);
+                }
+            }
+            float alpha[kMaxG];
+            softmax_step(score, active, alpha);
+            __syncthreads();
+            const int cnt = min(64, n_res - t0);
+#pragma unroll
+            for (int cc = 0; cc < CPL; ++cc) {
+                const int c = lane + 64 * cc;
+#pragma unroll
+                for (int i = 0; i < kMaxG; ++i) o[cc][i] *= alpha[i];
+                for (int tt = 0; tt < cnt; ++tt) {
+                    const int tok = t0 + tt;
+                    float v;
+                    if (tok < tl)
+                        v = load_as_f32(A.tail_v, ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + tok) * D + c,
+                                        A.tail_dtype);
+                    else
+                        v = load_as_f32(A.v_new, (static_cast<int64_t>(b) * L.n_kv + h) * D + c, A.new_dtype);
+#pragma unroll
+                    for (int i = 0; i < kMaxG; ++i)
+                        if (i < g) o[cc][i] = fmaf(sm.p[tt][i], v, o[cc][i]);
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    // Partials: o per lane-channel, m uniform, l reduced across the wave.
+    for (int i = 0; i < g; ++i) {
+        float* r = part_rec(p, item, h, i);
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) r[lane + 64 * cc] = o[cc][i];
+        const float lt = wave_sum(lsum[i]);
+        if (lane == 0) {
+            r[D] = m[i];
+            r[D + 1] = lt;
+        }
+    }
+    if (last_split_arrives(p, b, h, &sm.flag)) merge_partials(p, b, h);
+}
+
+}  // namespace
+
+int launch_decode_valu(const DecodeParams& p, hipStream_t stream) {
+    const int D = p.L.head_dim;
+    const int n_slots = p.L.k_width[0] + p.L.k_width[1] + p.L.k_width[2] + p.L.k_width[3];
+    const size_t dyn = static_cast<size_t>(n_slots) * kMaxG * sizeof(float);
+    dim3 grid(p.A.n_work, p.L.n_kv), block(64);
+    if (D == 64) hipLaunchKernelGGL(decode_valu_kernel<64>, grid, block, dyn, stream, p);
+    else if (D == 128) hipLaunchKernelGGL(decode_valu_kernel<128>, grid, block, dyn, stream, p);
+    else if (D == 256) hipLaunchKernelGGL(decode_valu_kernel<256>, grid, block, dyn, stream, p);
+    else return LF_E_SHAPE;
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? LF_OK : static_cast<int>(err);
+}
+
+}  // namespace lf

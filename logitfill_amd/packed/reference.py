@@ -1,0 +1,196 @@
+"""Decode-attention call for the packed cache.
+
+Drop-in for the reference's ``logitfill.packed.reference``
+(``src/logitfill/packed/reference.py``):
+
+* ``packed_attention(manager, layer_idx, query, key_new, value_new, scaling)``
+  -- one query token per sequence goes to the HIP split-K decode kernel over
+  the packed pages, the residual page and the new token
+  (``lf_decode_attention``); this replaces ``_kernel_attention`` and the CUDA
+  kernel it launches (``reference.py:59-109``).
+* Calls the reference sends to its dense path -- several query tokens
+  (``reference.py:62``), ``bit_v != 2`` -- run ``reference_attention`` on the
+  device: HIP dequantisation of the history, then float32 softmax attention
+  with the right-aligned causal mask (``reference.py:18-56``).
+
+Nothing here runs on the CPU: a missing extension or a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import torch
+
+from logitfill_amd import _native
+from logitfill_amd.packed.cache import env_int
+
+
+def repeat_kv(states: torch.Tensor, repeats: int) -> torch.Tensor:
+    """``reference.py:10-15``: kv head h feeds query heads h*r .. h*r+r-1."""
+    if repeats == 1:
+        return states
+    batch, heads, tokens, dim = states.shape
+    states = states[:, :, None].expand(batch, heads, repeats, tokens, dim)
+    return states.reshape(batch, heads * repeats, tokens, dim)
+
+
+def _causal_mask(query_len: int, key_len: int, device) -> torch.Tensor | None:
+    """``reference.py:18-27``: float mask for queries aligned to the right edge of the keys."""
+    if query_len == 1:
+        return None
+    mask = torch.zeros(query_len, key_len, dtype=torch.float32, device=device)
+    for index in range(query_len):
+        visible = key_len - query_len + index + 1
+        if visible < key_len:
+            mask[index, visible:] = float("-inf")
+    return mask
+
+
+def reference_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
+                        value_new: torch.Tensor, scaling: float) -> torch.Tensor:
+    """Dense path on the device (``reference.py:30-56``), for every sequence of the batch.
+
+    ``query [B, n_q, q_len, D]``; ``key_new/value_new [B, n_kv, q_len, D]``.
+    History is dequantised by the HIP kernel; attention is float32.
+    """
+    layer = manager.layers[layer_idx]
+    if query.shape[0] != layer.batch:
+        raise ValueError(f"query batch {query.shape[0]} != cache batch {layer.batch}")
+    if not query.is_cuda:
+        raise RuntimeError("logitfill_amd runs on ROCm devices only (there is no CPU path)")
+    repeats = manager.n_q // manager.n_kv
+    tail_k, tail_v = layer.tail_buffers()
+    outs = []
+    for b in range(layer.batch):
+        key_hist, value_hist = layer.dequantize(b)
+        pieces_k, pieces_v = [key_hist], [value_hist]
+        tl = layer.tail_lens[b]
+        if tl:
+            pieces_k.append(tail_k[b, :, :tl].float())
+            pieces_v.append(tail_v[b, :, :tl].float())
+        pieces_k.append(key_new[b].float())
+        pieces_v.append(value_new[b].float())
+        key = repeat_kv(torch.cat(pieces_k, dim=1).unsqueeze(0), repeats)[0].contiguous()
+        value = repeat_kv(torch.cat(pieces_v, dim=1).unsqueeze(0), repeats)[0].contiguous()
+        q = query[b].float().contiguous()                                  # [n_q, q_len, D]
+        scores = torch.matmul(q, key.transpose(1, 2).contiguous()) * scaling
+        mask = _causal_mask(q.shape[1], key.shape[1], q.device)
+        if mask is not None:
+            scores = scores + mask
+        probs = torch.softmax(scores, dim=-1)
+        outs.append(torch.matmul(probs, value))
+    return torch.stack(outs).to(dtype=query.dtype)
+
+
+def choose_pages_per_split(total_page_heads: int, kernel: int) -> int:
+    """Pages per split-K item: enough workgroups to fill 256 CUs several times over."""
+    forced = env_int("LOGITFILL_AMD_PAGES_PER_SPLIT", 0)
+    if forced > 0:
+        return forced
+    target = 2048
+    return max(1, min(64, math.ceil(total_page_heads / target)))
+
+
+class DecodePlan:
+    """Device work list for one layer's current history lengths (rebuilt when they change)."""
+
+    def __init__(self, hist_pages: list[int], n_kv: int, pages_per_split: int, device):
+        lib = _native.load()
+        batch = len(hist_pages)
+        cap = sum(-(-p // pages_per_split) for p in hist_pages) + batch
+        hp = (ctypes.c_int32 * batch)(*hist_pages)
+        work = (ctypes.c_int32 * (4 * cap))()
+        seq = (ctypes.c_int32 * (2 * batch))()
+        n = lib.lf_plan_decode(hp, batch, pages_per_split, work, cap, seq)
+        if n < 0:
+            _native.check(n, "lf_plan_decode")
+        self.key = (tuple(hist_pages), pages_per_split)
+        self.n_work = int(n)
+        self.work = torch.tensor(list(work)[: 4 * n], dtype=torch.int32).to(device)
+        self.seq_work = torch.tensor(list(seq), dtype=torch.int32).to(device)
+        self.pages_per_split = pages_per_split
+
+
+def kernel_choice() -> int:
+    """``LOGITFILL_AMD_KERNEL``: auto (default), valu or mfma."""
+    name = os.environ.get("LOGITFILL_AMD_KERNEL", "auto").lower()
+    return {"auto": _native.KERNEL_AUTO, "valu": _native.KERNEL_VALU, "mfma": _native.KERNEL_MFMA}[name]
+
+
+def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new, scaling: float,
+                out: torch.Tensor, kernel: int | None = None, pages_per_split: int | None = None) -> None:
+    """Enqueue the fused decode kernel for layer ``layer_idx`` writing ``out [B, n_q, D]``.
+
+    ``query [B, n_q, D]``; ``key_new/value_new [B, n_kv, D]`` or None.  Everything is
+    enqueued on the current stream; nothing synchronises.
+    """
+    layer = manager.layers[layer_idx]
+    kernel = kernel_choice() if kernel is None else kernel
+    P = layer.page_size
+    hist_pages = [h // P for h in layer.hist_lens]
+    if pages_per_split is None:
+        pages_per_split = choose_pages_per_split(sum(hist_pages) * layer.n_kv, kernel)
+    plan = layer.decode_plan
+    if plan is None or plan.key != (tuple(hist_pages), pages_per_split):
+        plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device)
+        layer.decode_plan = plan
+    lib = _native.load()
+    nbytes = lib.lf_decode_workspace_bytes(layer.batch, layer.n_kv, manager.n_q, layer.head_dim, plan.n_work)
+    ws = manager.workspace(nbytes)
+    tail_k, tail_v = layer.tail_buffers()
+    a = _native.DecodeArgs()
+    a.query = query.data_ptr()
+    a.q_dtype = _native.dtype_code(query.dtype)
+    if key_new is not None:
+        a.k_new = key_new.data_ptr()
+        a.v_new = value_new.data_ptr()
+        a.new_dtype = _native.dtype_code(key_new.dtype)
+        if value_new.dtype != key_new.dtype:
+            raise TypeError("key_new and value_new must share a dtype")
+    if tail_k is not None:
+        a.tail_k = tail_k.data_ptr()
+        a.tail_v = tail_v.data_ptr()
+        a.tail_dtype = _native.dtype_code(tail_k.dtype)
+        a.tail_cap = int(tail_k.shape[2])
+    else:
+        a.tail_dtype = _native.LF_BF16
+        a.tail_cap = 0
+    a.tail_len = layer.tail_len_device().data_ptr()
+    a.out = out.data_ptr()
+    a.out_dtype = _native.dtype_code(out.dtype)
+    a.n_q = manager.n_q
+    a.scaling = float(scaling)
+    a.work = plan.work.data_ptr()
+    a.n_work = plan.n_work
+    a.seq_work = plan.seq_work.data_ptr()
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
+    a.kernel = kernel
+    st = lib.lf_decode_attention(layer.layer_struct(), a, _native.current_stream_ptr(layer.device))
+    _native.check(st, "lf_decode_attention")
+
+
+def _kernel_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
+                      value_new: torch.Tensor, scaling: float) -> torch.Tensor:
+    """One-token decode through the HIP kernel (replaces ``reference.py:59-109``)."""
+    B, n_q, q_len, D = query.shape
+    q = query.reshape(B, n_q, D)
+    if q.stride(-1) != 1 or not q.is_contiguous():
+        q = q.contiguous()
+    kn = key_new.reshape(B, manager.n_kv, D).contiguous()
+    vn = value_new.reshape(B, manager.n_kv, D).contiguous()
+    out = torch.empty(B, n_q, D, dtype=query.dtype, device=query.device)
+    decode_into(manager, layer_idx, q, kn, vn, scaling, out)
+    return out.view(B, n_q, 1, D)
+
+
+def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
+                     value_new: torch.Tensor, scaling: float) -> torch.Tensor:
+    """``reference.py:112-116``: ``query [B, n_q, q_len, D]`` -> ``[B, n_q, q_len, D]``."""
+    if not query.is_cuda:
+        raise RuntimeError("logitfill_amd runs on ROCm devices only (there is no CPU path)")
+    if query.shape[-2] == 1 and manager.bit_v == 2:
+        return _kernel_attention(manager, layer_idx, query, key_new, value_new, scaling)
+    return reference_attention(manager, layer_idx, query, key_new, value_new, scaling)

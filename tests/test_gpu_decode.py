@@ -1,0 +1,153 @@
+"""GPU parity of the decode-attention path against the oracle's dense
+dequantise-then-attend path (reference src/logitfill/packed/reference.py:30-56):
+bf16 output within max-abs 2e-3 and rel-L2 1e-3 (fp32 accumulation), on the
+same seeded inputs; plus split-count invariance and the reference's own
+kernel-test shape."""
+import numpy as np
+import pytest
+import torch
+
+from logitfill_amd import _native, synth
+from logitfill_amd.packed import PackedKVManager
+from logitfill_amd.packed.reference import decode_into, packed_attention, reference_attention
+from oracle import attention as oatt
+from tests.helpers import assert_decode_close, f32, oracle_decode, oracle_store
+
+pytestmark = pytest.mark.gpu
+
+KERNELS = {"valu": _native.KERNEL_VALU, "auto": _native.KERNEL_AUTO}
+
+
+def build(d, pages, tails, n_q, n_kv, D, dev, page=128, kg=128, vg=128):
+    """Manager whose sequence b holds pages[b] packed pages then tails[b] residual tokens of d."""
+    B = len(pages)
+    mgr = PackedKVManager([d.levels], n_q, n_kv, D, page, kg, vg, 2, dev, batch_size=B)
+    lens = [p * page + t for p, t in zip(pages, tails)]
+    mgr.commit(0, d.key[:, :, :max(lens)].to(dev), d.value[:, :, :max(lens)].to(dev), lengths=lens)
+    return mgr, lens
+
+
+def oracle_out(d, b, n, n_q, n_kv, scaling, page=128, kg=128, vg=128):
+    store = oracle_store(d.levels, f32(d.key[b, :, :n]), f32(d.value[b, :, :n]), page, kg, vg, 2)
+    return oracle_decode(store, f32(d.query[b]), f32(d.key_new[b]), f32(d.value_new[b]), scaling, n_q, n_kv)
+
+
+def run(mgr, d, dev, scaling, kernel, pages_per_split=None, out_dtype=None):
+    q = d.query.to(dev)
+    out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=dev)
+    decode_into(mgr, 0, q, d.key_new.to(dev), d.value_new.to(dev), scaling, out, kernel=kernel,
+                pages_per_split=pages_per_split)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("kernel", list(KERNELS))
+def test_config0_decode(gpu, kernel):
+    """1 seq, 4 kv / 28 q heads, 8 pages + the new token, target 2.5."""
+    d = synth.make_layer(1, 28, 4, 128, 1024, 2.5, seed=0)
+    mgr, lens = build(d, [8], [0], 28, 4, 128, gpu)
+    out = run(mgr, d, gpu, 128 ** -0.5, KERNELS[kernel])
+    assert_decode_close(out[0], oracle_out(d, 0, 1024, 28, 4, 128 ** -0.5))
+
+
+@pytest.mark.parametrize("kernel", list(KERNELS))
+def test_ragged_batch_decode(gpu, kernel):
+    """Ragged batch (GQA 5): histories of 0..12 pages, residual pages of 0..127 tokens."""
+    pages, tails = [0, 1, 5, 12, 3], [3, 0, 127, 50, 1]
+    d = synth.make_layer(5, 10, 2, 128, 12 * 128 + 127, 2.5, seed=4)
+    mgr, lens = build(d, pages, tails, 10, 2, 128, gpu)
+    out = run(mgr, d, gpu, 0.0883, KERNELS[kernel])
+    for b in range(5):
+        assert_decode_close(out[b], oracle_out(d, b, lens[b], 10, 2, 0.0883))
+
+
+@pytest.mark.parametrize("kernel", list(KERNELS))
+def test_split_count_invariance(gpu, kernel):
+    d = synth.make_layer(2, 14, 2, 128, 20 * 128 + 9, 3.0, seed=8)
+    mgr, lens = build(d, [20, 13], [9, 77], 14, 2, 128, gpu)
+    outs = [run(mgr, d, gpu, 0.09, KERNELS[kernel], pages_per_split=s, out_dtype=torch.float32)
+            for s in (1, 3, 64)]
+    for o in outs[1:]:
+        assert torch.allclose(o, outs[0], atol=1e-6, rtol=1e-5)
+    for b in range(2):
+        ref = oracle_out(d, b, lens[b], 14, 2, 0.09)
+        assert_decode_close(outs[0][b], ref, out_dtype="fp32")
+
+
+def test_reference_kernel_test_shape(gpu):
+    """tests/test_logitfill_offline.py:187-219: D 64, n_q = n_kv = 1, page = groups = 64,
+    all four tiers, float32 data; the reference compares kernel vs dense at 1e-3."""
+    g = torch.Generator().manual_seed(0)
+    levels = torch.randint(0, 4, (1, 64), generator=g)
+    key = torch.randn(1, 1, 64, 64, generator=g)
+    value = torch.randn(1, 1, 64, 64, generator=g)
+    mgr = PackedKVManager([levels], 1, 1, 64, 64, 64, 64, 2, gpu)
+    mgr.commit(0, key.to(gpu), value.to(gpu))
+    query = torch.randn(1, 1, 1, 64, generator=g)
+    new_k = torch.randn(1, 1, 1, 64, generator=g)
+    new_v = torch.randn(1, 1, 1, 64, generator=g)
+    fast = packed_attention(mgr, 0, query.to(gpu), new_k.to(gpu), new_v.to(gpu), scaling=64 ** -0.5)
+    slow = reference_attention(mgr, 0, query.to(gpu), new_k.to(gpu), new_v.to(gpu), scaling=64 ** -0.5)
+    assert fast.shape == (1, 1, 1, 64) and fast.dtype == torch.float32
+    assert torch.allclose(fast.float(), slow.float(), atol=1e-3, rtol=1e-3)
+    store = oracle_store(levels.numpy(), key[0].numpy(), value[0].numpy(), 64, 64, 64, 2)
+    ref = oatt.reference_attention(store, query[0].numpy(), new_k[0].numpy(), new_v[0].numpy(), 64 ** -0.5, 1, 1)
+    assert_decode_close(fast[0, :, 0], ref[:, 0], out_dtype="fp32", max_abs=1e-5, rel_l2=1e-5)
+
+
+@pytest.mark.parametrize("q_dtype", [torch.float16, torch.float32])
+def test_query_and_output_dtypes(gpu, q_dtype):
+    d = synth.make_layer(1, 8, 2, 128, 3 * 128 + 5, 2.5, seed=12)
+    mgr, lens = build(d, [3], [5], 8, 2, 128, gpu)
+    q = d.query.to(q_dtype).to(gpu)
+    out = torch.empty(q.shape, dtype=q_dtype, device=gpu)
+    decode_into(mgr, 0, q, d.key_new.to(gpu), d.value_new.to(gpu), 0.1, out)
+    torch.cuda.synchronize()
+    ref = oracle_decode(oracle_store(d.levels, f32(d.key[0, :, :lens[0]]), f32(d.value[0, :, :lens[0]])),
+                        f32(q[0]), f32(d.key_new[0]), f32(d.value_new[0]), 0.1, 8, 2)
+    assert_decode_close(out[0], ref, out_dtype="fp16" if q_dtype == torch.float16 else "fp32")
+
+
+def test_decode_commit_loop_crossing_flushes(gpu):
+    """Model order (attention, then commit; reference models/qwen2_attention.py:244-253)
+    for 140 decode steps starting 3 tokens before a page boundary."""
+    n_q, n_kv, D = 6, 2, 128
+    total = 128 + 125 + 140 + 1
+    d = synth.make_layer(1, n_q, n_kv, D, total, 2.5, seed=31)
+    mgr = PackedKVManager([d.levels], n_q, n_kv, D, 128, 128, 128, 2, gpu)
+    k, v = d.key.to(gpu), d.value.to(gpu)
+    mgr.commit(0, k[:, :, :253], v[:, :, :253])
+    qs = torch.randn(140, 1, n_q, 1, D, generator=torch.Generator().manual_seed(1)).bfloat16()
+    for step in range(140):
+        pos = 253 + step
+        out = packed_attention(mgr, 0, qs[step].to(gpu), k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], D ** -0.5)
+        if step in (0, 2, 3, 139):
+            store = oracle_store(d.levels, f32(d.key[0, :, :pos]), f32(d.value[0, :, :pos]))
+            ref = oatt.reference_attention(store, f32(qs[step][0]), f32(d.key[0, :, pos:pos + 1]),
+                                           f32(d.value[0, :, pos:pos + 1]), D ** -0.5, n_q, n_kv)
+            assert_decode_close(out[0, :, 0], ref[:, 0])
+        mgr.commit(0, k[:, :, pos:pos + 1], v[:, :, pos:pos + 1])
+    assert mgr.layers[0].hist_len == 384 and mgr.layers[0].tail_len == 9
+
+
+def test_multi_token_query_uses_device_dense_path(gpu):
+    """q_len > 1 (chunked scoring) takes the dense path with the right-aligned causal mask."""
+    n_q, n_kv, D = 4, 2, 128
+    d = synth.make_layer(1, n_q, n_kv, D, 2 * 128 + 30, 2.5, seed=40)
+    mgr, lens = build(d, [2], [20], n_q, n_kv, D, gpu)
+    q = torch.randn(1, n_q, 3, D, generator=torch.Generator().manual_seed(2)).bfloat16()
+    kn, vn = d.key[:, :, 276:279], d.value[:, :, 276:279]
+    out = packed_attention(mgr, 0, q.to(gpu), kn.to(gpu), vn.to(gpu), 0.1)
+    store = oracle_store(d.levels, f32(d.key[0, :, :276]), f32(d.value[0, :, :276]))
+    ref = oatt.reference_attention(store, f32(q[0]), f32(kn[0]), f32(vn[0]), 0.1, n_q, n_kv)
+    assert_decode_close(out[0], ref)
+
+
+def test_device_dequantize_matches_oracle(gpu):
+    d = synth.make_layer(2, 8, 4, 128, 5 * 128, 2.5, seed=50)
+    mgr, lens = build(d, [5, 2], [0, 11], 8, 4, 128, gpu)
+    for b in range(2):
+        kd, vd = mgr.layers[0].dequantize(b)
+        store = oracle_store(d.levels, f32(d.key[b, :, :lens[b]]), f32(d.value[b, :, :lens[b]]))
+        ok, ov = store.dequantize()
+        assert np.array_equal(kd.cpu().numpy(), ok) and np.array_equal(vd.cpu().numpy(), ov)

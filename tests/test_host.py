@@ -1,0 +1,122 @@
+"""CPU tests of the host side: tier tables, sampler, the C ABI library's exports,
+struct layouts against the C compiler, the host-only planner and argument
+validation (no device work is enqueued by any call here)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from logitfill_amd import _native, synth
+from logitfill_amd.packed import layout as product_layout
+from oracle import layout as oracle_layout
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "logitfill_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_product_tier_tables_match_oracle():
+    rng = np.random.default_rng(0)
+    for lv in [np.array([[0, 3, 1, 0], [2, 0, 0, 1]]), rng.integers(0, 4, (8, 128)),
+               synth.sample_tier_levels(4, 128, 2.5, 3), np.zeros((2, 64), np.int64)]:
+        ours = product_layout.tier_tables(torch.as_tensor(lv))
+        ref = oracle_layout.tier_tables(lv)
+        assert np.array_equal(ours["tier"].numpy(), ref["tier"])
+        for t in range(4):
+            for k in ("index", "count", "local"):
+                assert np.array_equal(ours["tiers"][t][k].numpy(), ref["tiers"][t][k]), (t, k)
+            assert ours["tiers"][t]["width"] == ref["tiers"][t]["width"]
+    with pytest.raises(ValueError):
+        product_layout.tier_tables(torch.tensor([[0, 4]]))
+
+
+@pytest.mark.parametrize("target", [2.5, 3.0, 4.0])
+def test_sampler_spends_exact_budget(target):
+    lv = synth.sample_tier_levels(8, 128, target, seed=11)
+    budget = synth.key_budget(target)
+    assert np.all(synth.LEVEL_EXTRA[lv].sum(-1) == budget)
+    assert synth.LEVEL_BITS[lv].mean() == 2 * target - 2
+    assert np.array_equal(lv, synth.sample_tier_levels(8, 128, target, seed=11))
+
+
+def test_budget_rule_matches_reference_selfcheck():
+    # reference allocators/allocate.py:20-25 and :160-164
+    assert synth.key_budget(2.5, 2, 128) == 128
+    with pytest.raises(ValueError):
+        synth.key_budget(1.5, 2, 128)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    names = declared_functions()
+    assert "lf_decode_attention" in names and "lf_pack_pages" in names
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _native._SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.lf_abi_version() == 1
+    assert b"gfx950" in lib.lf_build_info()
+
+
+def test_struct_layouts_match_c(tmp_path):
+    fields = {
+        "lf_packed_layer": [f for f, _ in _native.PackedLayer._fields_],
+        "lf_decode_args": [f for f, _ in _native.DecodeArgs._fields_],
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for st, fs in fields.items():
+        lines.append(f'printf("{st} %zu\\n", sizeof({st}));')
+        for f in fs:
+            lines.append(f'printf("{st}.{f} %zu\\n", offsetof({st}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
+    out = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                               check=True).stdout.split("\n") if line)
+    for st, cls in (("lf_packed_layer", _native.PackedLayer), ("lf_decode_args", _native.DecodeArgs)):
+        assert int(out[st]) == ctypes.sizeof(cls), st
+        for f in fields[st]:
+            assert int(out[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
+
+
+def test_plan_decode_known_answer():
+    lib = _native.load()
+    hp = (ctypes.c_int32 * 3)(5, 0, 2)
+    work = (ctypes.c_int32 * 40)()
+    seq = (ctypes.c_int32 * 6)()
+    n = lib.lf_plan_decode(hp, 3, 2, work, 10, seq)
+    assert n == 7
+    items = np.array(list(work)[:28]).reshape(7, 4).tolist()
+    assert items == [[0, 0, 2, 0], [0, 2, 4, 0], [0, 4, 5, 0], [0, 0, 0, 1],
+                     [1, 0, 0, 1],
+                     [2, 0, 2, 0], [2, 0, 0, 1]]
+    assert list(seq) == [0, 4, 4, 1, 5, 2]
+    assert lib.lf_plan_decode(hp, 3, 2, work, 6, seq) == -4          # LF_E_WORKSPACE
+    assert lib.lf_plan_decode(hp, 3, 0, work, 10, seq) == -2         # LF_E_SHAPE
+
+
+def test_workspace_layout():
+    lib = _native.load()
+    assert lib.lf_decode_counter_offset(16, 4, 28, 128, 100) == 0
+    assert lib.lf_decode_workspace_bytes(16, 4, 28, 128, 100) == 256 + 100 * 28 * 130 * 4
+    assert lib.lf_decode_workspace_bytes(100, 4, 28, 128, 1) == 1792 + 28 * 130 * 4
+
+
+def test_argument_validation_rejects_before_launch():
+    lib = _native.load()
+    assert lib.lf_pack_pages(None, None, None, 0, 0, 0, 0, None, 1, None) == -1
+    layer = _native.PackedLayer()
+    assert lib.lf_pack_pages(layer, None, None, 0, 0, 0, 0, None, 1, None) == -2   # zero shapes
+    assert lib.lf_decode_attention(layer, None, None) == -2
+    assert lib.lf_dequantize(layer, 0, 4, None, None, None) == -1
+    assert lib.lf_dense_decode(None, None, None, 1, 1, 1, 128, 1, 0, 0, 0, 1.0, None, 64, None, 0, None) == -1
