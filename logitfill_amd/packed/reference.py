@@ -113,6 +113,15 @@ class DecodePlan:
         self.pages_per_split = pages_per_split
 
 
+def _expect(t: torch.Tensor, shape, name: str) -> None:
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must be {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} is on {t.device}; logitfill_amd runs on ROCm devices only")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
 def kernel_choice() -> int:
     """``LOGITFILL_AMD_KERNEL``: auto (default), valu or mfma."""
     name = os.environ.get("LOGITFILL_AMD_KERNEL", "auto").lower()
@@ -127,6 +136,12 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     enqueued on the current stream; nothing synchronises.
     """
     layer = manager.layers[layer_idx]
+    B, D = layer.batch, layer.head_dim
+    _expect(query, (B, manager.n_q, D), "query")
+    _expect(out, (B, manager.n_q, D), "out")
+    if key_new is not None:
+        _expect(key_new, (B, manager.n_kv, D), "key_new")
+        _expect(value_new, (B, manager.n_kv, D), "value_new")
     kernel = kernel_choice() if kernel is None else kernel
     P = layer.page_size
     hist_pages = [h // P for h in layer.hist_lens]

@@ -51,19 +51,40 @@ def assert_history_equal(layer, b, store, *, tail=True):
             assert np.array_equal(f32(tv[b, :, :tl]), store.tail_v)
 
 
+def ulp(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Spacing of the output format at |x| (bf16: 8 significant bits, fp16: 11, fp32: 24)."""
+    bits = {"bf16": 8, "fp16": 11, "fp32": 24}[dtype]
+    ax = np.maximum(np.abs(x), np.finfo(np.float32).tiny)
+    return np.exp2(np.floor(np.log2(ax)) - (bits - 1))
+
+
 def decode_errors(ours: torch.Tensor, ref_fp32: np.ndarray, out_dtype="bf16"):
-    """(max-abs, rel-L2) of the device output against the oracle rounded to the output dtype."""
+    """(max-abs, rel-L2, worst excess) of the device output against the oracle rounded to
+    the output dtype.  ``excess`` is the largest |diff| among elements that are outside
+    the max-abs bar *and* differ by more than one output ulp (a rounding flip of the
+    output format is one ulp; for bf16 values above 0.5 one ulp already exceeds 2e-3)."""
     ref = oatt.round_to_dtype(ref_fp32.astype(np.float32), out_dtype).astype(np.float64)
     o = f32(ours).astype(np.float64).reshape(ref.shape)
-    diff = o - ref
-    max_abs = float(np.abs(diff).max()) if diff.size else 0.0
-    rel = float(np.linalg.norm(diff) / max(np.linalg.norm(ref), 1e-30))
-    return max_abs, rel
+    diff = np.abs(o - ref)
+    max_abs = float(diff.max()) if diff.size else 0.0
+    rel = float(np.linalg.norm(o - ref) / max(np.linalg.norm(ref), 1e-30))
+    bad = (diff > MAX_ABS) & (diff > ulp(ref, out_dtype) * 1.0001)
+    excess = float(diff[bad].max()) if bad.any() else 0.0
+    return max_abs, rel, excess
 
 
 def assert_decode_close(ours, ref_fp32, out_dtype="bf16", max_abs=MAX_ABS, rel_l2=REL_L2):
-    ma, rl = decode_errors(ours, ref_fp32, out_dtype)
-    assert ma <= max_abs and rl <= rel_l2, f"max_abs={ma:.3g} (bar {max_abs}), rel_l2={rl:.3g} (bar {rel_l2})"
+    """max-abs <= 2e-3 (or one output ulp, for outputs whose format
+    resolution is coarser than the bar) and rel-L2 <= 1e-3, fp32 accumulation."""
+    ref = oatt.round_to_dtype(ref_fp32.astype(np.float32), out_dtype).astype(np.float64)
+    o = f32(ours).astype(np.float64).reshape(ref.shape)
+    diff = np.abs(o - ref)
+    rl = float(np.linalg.norm(o - ref) / max(np.linalg.norm(ref), 1e-30))
+    bad = (diff > max_abs) & (diff > ulp(ref, out_dtype) * 1.0001)
+    ma = float(diff.max()) if diff.size else 0.0
+    assert not bad.any() and rl <= rel_l2, (
+        f"max_abs={ma:.3g} (bar {max_abs} or 1 ulp; {int(bad.sum())} elements outside), "
+        f"rel_l2={rl:.3g} (bar {rel_l2})")
     return ma, rl
 
 
