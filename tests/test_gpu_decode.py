@@ -15,7 +15,7 @@ from tests.helpers import assert_decode_close, f32, oracle_decode, oracle_store
 
 pytestmark = pytest.mark.gpu
 
-KERNELS = {"valu": _native.KERNEL_VALU, "auto": _native.KERNEL_AUTO}
+KERNELS = {"valu": _native.KERNEL_VALU, "mfma": _native.KERNEL_MFMA, "auto": _native.KERNEL_AUTO}
 
 
 def build(d, pages, tails, n_q, n_kv, D, dev, page=128, kg=128, vg=128):
@@ -156,3 +156,36 @@ def test_device_dequantize_matches_oracle(gpu):
         store = oracle_store(d.levels, f32(d.key[b, :, :lens[b]]), f32(d.value[b, :, :lens[b]]))
         ok, ov = store.dequantize()
         assert np.array_equal(kd.cpu().numpy(), ok) and np.array_equal(vd.cpu().numpy(), ov)
+
+
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+@pytest.mark.parametrize("g,levels_kind", [(1, "uniform"), (8, "uniform"), (7, "fp16heavy"), (5, "int8heavy")])
+def test_tier_mix_and_group_sizes(gpu, kernel, g, levels_kind):
+    """Tier tables far from the sampler's (wide int8 / fp16 tiers, every K-step path) and
+    GQA groups 1..8; 37-page histories split 40 pages per item (> one 16-page scale chunk)."""
+    n_kv, D = 2, 128
+    rng = np.random.default_rng(g)
+    if levels_kind == "uniform":
+        levels = rng.integers(0, 4, (n_kv, D))
+    elif levels_kind == "fp16heavy":
+        levels = rng.choice(4, (n_kv, D), p=[0.2, 0.1, 0.1, 0.6])
+    else:
+        levels = rng.choice(4, (n_kv, D), p=[0.1, 0.2, 0.6, 0.1])
+    d = synth.make_layer(2, g * n_kv, n_kv, D, 37 * 128 + 127, 2.5, seed=60 + g)
+    d.levels = levels
+    mgr, lens = build(d, [37, 20], [127, 0], g * n_kv, n_kv, D, gpu)
+    out = run(mgr, d, gpu, D ** -0.5, KERNELS[kernel], pages_per_split=40)
+    for b in range(2):
+        assert_decode_close(out[b], oracle_out(d, b, lens[b], g * n_kv, n_kv, D ** -0.5))
+
+
+def test_mfma_kernel_rejects_unsupported_shape(gpu):
+    """The MFMA kernel serves D 128 / page 128 / g <= 8; an explicit request elsewhere is an error."""
+    g = torch.Generator().manual_seed(0)
+    levels = torch.randint(0, 4, (1, 64), generator=g)
+    mgr = PackedKVManager([levels], 1, 1, 64, 64, 64, 64, 2, gpu)
+    mgr.commit(0, torch.randn(1, 1, 64, 64, generator=g).to(gpu), torch.randn(1, 1, 64, 64, generator=g).to(gpu))
+    q = torch.randn(1, 1, 64, device=gpu)
+    out = torch.empty_like(q)
+    with pytest.raises(_native.LFError):
+        decode_into(mgr, 0, q, q.clone(), q.clone(), 0.125, out, kernel=_native.KERNEL_MFMA)
