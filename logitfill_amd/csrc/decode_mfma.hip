@@ -152,28 +152,32 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a0, uint32_t a1, uint32
 struct Stage {
     uint4 c[kMaxStage];
     uint32_t v[4];
+    int64_t row0;
 };
 
-// Issue the global loads of page ``page`` of (b, h) into registers.
+// 16-byte chunk ``c`` of page ``row0``'s contiguous blocks (K tiers 0..2, fp16 tier, v scale, v min).
+__device__ __forceinline__ uint4 chunk_load(const lf_packed_layer& L, const MfmaLayout& y, int64_t row0, int c) {
+    const unsigned char* src;
+    int off;
+    if (c < y.seg_end[0]) { src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]); off = c; }
+    else if (c < y.seg_end[1]) { src = reinterpret_cast<const unsigned char*>(L.k_code[1] + row0 * L.k_words[1]); off = c - y.seg_end[0]; }
+    else if (c < y.seg_end[2]) { src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]); off = c - y.seg_end[1]; }
+    else if (c < y.seg_end[3]) { src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]); off = c - y.seg_end[2]; }
+    else if (c < y.seg_end[4]) { src = reinterpret_cast<const unsigned char*>(L.v_scale + row0); off = c - y.seg_end[3]; }
+    else { src = reinterpret_cast<const unsigned char*>(L.v_min + row0); off = c - y.seg_end[4]; }
+    return *reinterpret_cast<const uint4*>(src + 16 * static_cast<int64_t>(off));
+}
+
+// Issue the global loads of page ``page`` of (b, h) into registers (the first kMaxStage
+// chunks per thread; stage_store fetches any remainder itself).
 __device__ __forceinline__ void stage_load(Stage& s, const lf_packed_layer& L, const MfmaLayout& y, int b, int h,
                                            int page) {
     const int64_t row0 = tok_row(L, b, h, static_cast<int64_t>(page) * kPage);
+    s.row0 = row0;
 #pragma unroll
     for (int i = 0; i < kMaxStage; ++i) {
         const int c = threadIdx.x + i * kThreads;
-        uint4 v = {0u, 0u, 0u, 0u};
-        if (c < y.seg_end[5]) {
-            const unsigned char* src;
-            int off;
-            if (c < y.seg_end[0]) { src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]); off = c; }
-            else if (c < y.seg_end[1]) { src = reinterpret_cast<const unsigned char*>(L.k_code[1] + row0 * L.k_words[1]); off = c - y.seg_end[0]; }
-            else if (c < y.seg_end[2]) { src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]); off = c - y.seg_end[1]; }
-            else if (c < y.seg_end[3]) { src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]); off = c - y.seg_end[2]; }
-            else if (c < y.seg_end[4]) { src = reinterpret_cast<const unsigned char*>(L.v_scale + row0); off = c - y.seg_end[3]; }
-            else { src = reinterpret_cast<const unsigned char*>(L.v_min + row0); off = c - y.seg_end[4]; }
-            v = *reinterpret_cast<const uint4*>(src + 16 * static_cast<int64_t>(off));
-        }
-        s.c[i] = v;
+        s.c[i] = c < y.seg_end[5] ? chunk_load(L, y, row0, c) : uint4{0u, 0u, 0u, 0u};
     }
     // Value codes: 4 consecutive tokens of one word (token group tid/8, word tid%8).
     const int tg = threadIdx.x >> 3, w = threadIdx.x & 7;
@@ -182,40 +186,47 @@ __device__ __forceinline__ void stage_load(Stage& s, const lf_packed_layer& L, c
     for (int i = 0; i < 4; ++i) s.v[i] = static_cast<uint32_t>(vc[8 * i]);
 }
 
-// Write staged registers into page buffer ``pb``.
+// Write one 16-byte chunk into page buffer ``pb``.
+__device__ __forceinline__ void chunk_store(unsigned char* pb, const lf_packed_layer& L, const MfmaLayout& y, int c,
+                                            uint4 v) {
+    if (c < y.seg_end[0]) {
+        *reinterpret_cast<uint4*>(pb + y.pb_kt[0] + 16 * c) = v;
+    } else if (c < y.seg_end[1]) {
+        *reinterpret_cast<uint4*>(pb + y.pb_kt[1] + 16 * (c - y.seg_end[0])) = v;
+    } else if (c < y.seg_end[2]) {
+        *reinterpret_cast<uint4*>(pb + y.pb_kt[2] + 16 * (c - y.seg_end[1])) = v;
+    } else if (c < y.seg_end[3]) {
+        // 8 fp16 values of the [128][w16] block -> padded rows [128][w16p]
+        const int e0 = 8 * (c - y.seg_end[2]);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint16_t* dst = reinterpret_cast<uint16_t*>(pb + y.pb_v16);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int e = e0 + k;
+            const int tok = e / L.k_width[3], j = e - tok * L.k_width[3];
+            dst[tok * y.w16p + j] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+        }
+    } else {
+        const bool is_min = c >= y.seg_end[4];
+        const int t0 = 8 * (c - (is_min ? y.seg_end[4] : y.seg_end[3]));
+        float* dst = reinterpret_cast<float*>(pb + (is_min ? y.pb_vmn : y.pb_vsc)) + t0;
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dst[k] = f16_to_f32(static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1))));
+    }
+}
+
+// Write staged registers into page buffer ``pb``; chunks past the register budget are
+// fetched here directly.
 __device__ __forceinline__ void stage_store(const Stage& s, unsigned char* pb, const lf_packed_layer& L,
                                             const MfmaLayout& y) {
 #pragma unroll
     for (int i = 0; i < kMaxStage; ++i) {
         const int c = threadIdx.x + i * kThreads;
-        if (c >= y.seg_end[5]) continue;
-        const uint4 v = s.c[i];
-        if (c < y.seg_end[0]) {
-            *reinterpret_cast<uint4*>(pb + y.pb_kt[0] + 16 * c) = v;
-        } else if (c < y.seg_end[1]) {
-            *reinterpret_cast<uint4*>(pb + y.pb_kt[1] + 16 * (c - y.seg_end[0])) = v;
-        } else if (c < y.seg_end[2]) {
-            *reinterpret_cast<uint4*>(pb + y.pb_kt[2] + 16 * (c - y.seg_end[1])) = v;
-        } else if (c < y.seg_end[3]) {
-            // 8 fp16 values of the [128][w16] block -> padded rows [128][w16p]
-            const int e0 = 8 * (c - y.seg_end[2]);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-            uint16_t* dst = reinterpret_cast<uint16_t*>(pb + y.pb_v16);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int e = e0 + k;
-                const int tok = e / L.k_width[3], j = e - tok * L.k_width[3];
-                dst[tok * y.w16p + j] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
-            }
-        } else {
-            const bool is_min = c >= y.seg_end[4];
-            const int t0 = 8 * (c - (is_min ? y.seg_end[4] : y.seg_end[3]));
-            float* dst = reinterpret_cast<float*>(pb + (is_min ? y.pb_vmn : y.pb_vsc)) + t0;
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) dst[k] = f16_to_f32(static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1))));
-        }
+        if (c < y.seg_end[5]) chunk_store(pb, L, y, c, s.c[i]);
     }
+    for (int c = threadIdx.x + kMaxStage * kThreads; c < y.seg_end[5]; c += kThreads)
+        chunk_store(pb, L, y, c, chunk_load(L, y, s.row0, c));
     uint32_t o[4];
     byte_transpose4(s.v[0], s.v[1], s.v[2], s.v[3], o);
     const int tg = threadIdx.x >> 3, w = threadIdx.x & 7;
@@ -376,14 +387,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bq, acc1, 0, 0, 0);
                 }
             }
-            // hi + lo columns, + bias; lanes n16 >= 8 carry don't-care values.
+            // hi + lo columns, + bias; lanes n16 >= 8 carry don't-care values.  The accumulator
+            // elements are copied to scalars before the DPP move: applied directly to vector
+            // elements, this compiler emits a single DPP move for all of them.
             float sv[8];
+            const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sv[r] = acc0[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                      0, __builtin_bit_cast(int, acc0[r]), 0x108, 0xf, 0xf, false)) + bias;
-                sv[4 + r] = acc1[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                          0, __builtin_bit_cast(int, acc1[r]), 0x108, 0xf, 0xf, false)) + bias;
+            for (int r = 0; r < 8; ++r) {
+                const int xi = __builtin_bit_cast(int, accs[r]);
+                sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x108, 0xf, 0xf, false)) +
+                        bias;
             }
             // ---- online softmax (log2 domain) ----
             float mx = sv[0];
@@ -637,7 +650,6 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     seg += kPage * L.k_width[3] * 2 / 16; y.seg_end[3] = seg;
     seg += kPage * 2 / 16; y.seg_end[4] = seg;
     seg += kPage * 2 / 16; y.seg_end[5] = seg;
-    if (seg > kMaxStage * kThreads) return false;
     if (y.lds_bytes > 160 * 1024) return false;
     return true;
 }
@@ -652,11 +664,13 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
         return LF_OK;
     }
     *handled = true;
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        attr_set = true;
+    // Raise the dynamic-LDS limit to what this launch needs (static LDS counts against the same budget).
+    static int lds_limit = 64 * 1024;
+    if (mp.y.lds_bytes > lds_limit) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, mp.y.lds_bytes);
+        if (e != hipSuccess) return static_cast<int>(e);
+        lds_limit = mp.y.lds_bytes;
     }
     hipLaunchKernelGGL(decode_mfma_kernel, dim3(p.A.n_work, p.L.n_kv), dim3(kThreads), mp.y.lds_bytes, stream, mp);
     const hipError_t err = hipGetLastError();

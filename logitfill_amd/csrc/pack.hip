@@ -307,14 +307,16 @@ size_t pack_lds_bytes(const lf_packed_layer& L, int elem) {
 }
 
 template <typename T, bool IsHalf>
-void launch_one(const PackJobArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&pack_pages_kernel<T, IsHalf>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        attr_set = true;
+int launch_one(const PackJobArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+    static size_t lds_limit = 64 * 1024;
+    if (lds > lds_limit) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pack_pages_kernel<T, IsHalf>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return static_cast<int>(e);
+        lds_limit = lds;
     }
     hipLaunchKernelGGL((pack_pages_kernel<T, IsHalf>), grid, dim3(kPackThreads), lds, stream, a);
+    return LF_OK;
 }
 
 }  // namespace
@@ -338,10 +340,12 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
     const size_t lds = pack_lds_bytes(L, elem);
     if (lds > 160 * 1024) return LF_E_SHAPE;
     dim3 grid(n_jobs, L.n_kv);
-    if (src_dtype == LF_BF16) launch_one<uint16_t, false>(a, grid, lds, stream);
-    else if (src_dtype == LF_FP16) launch_one<uint16_t, true>(a, grid, lds, stream);
-    else if (src_dtype == LF_FP32) launch_one<float, false>(a, grid, lds, stream);
+    int rc;
+    if (src_dtype == LF_BF16) rc = launch_one<uint16_t, false>(a, grid, lds, stream);
+    else if (src_dtype == LF_FP16) rc = launch_one<uint16_t, true>(a, grid, lds, stream);
+    else if (src_dtype == LF_FP32) rc = launch_one<float, false>(a, grid, lds, stream);
     else return LF_E_DTYPE;
+    if (rc != LF_OK) return rc;
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? LF_OK : static_cast<int>(err);
 }
