@@ -44,7 +44,6 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kD = 128;
 constexpr int kPage = 128;
-constexpr int kChunkPages = 16;  // Key scale/min staged for this many pages at a time
 constexpr int kMaxStage = 4;     // 16-byte staging chunks per thread per page
 
 struct MfmaLayout {
@@ -56,8 +55,7 @@ struct MfmaLayout {
     int w16p;        // fp16-tier row stride in LDS (multiple of 8)
     int off_qperm;   // [nb][8 heads][8] fp32: q * scaling*log2e for each slot (0 for padding)
     int off_qs;      // [nb][16][8] fp16: per-page Qs hi (rows 0..7) / lo (rows 8..15)
-    int off_sc;      // [kChunkPages][nb_int][8] fp32 Key scale of each slot
-    int off_mn;      // [kChunkPages][nb_int][8] fp32 Key min
+    int off_tt;      // tier table of this kv head: ranks -> channel ids (int16), per tier
     int off_small;   // bias partials [4][8], alpha [4][8], wave m/l/mv [4][3][8]
     int off_pbuf;    // residual probabilities [4][32][8] fp32
     int off_pb[2];   // page buffers
@@ -66,7 +64,11 @@ struct MfmaLayout {
     int pb_vt;       // [32 token groups][4][8] u32 byte-transposed Value codes
     int pb_vsc;      // [128] fp32 Value scale
     int pb_vmn;      // [128] fp32 Value min
+    int pb_ksc;      // [nb_int][8] fp32 Key scale of each integer-tier slot (this page)
+    int pb_kmn;      // [nb_int][8] fp32 Key min
     int seg_end[6];  // cumulative 16-byte chunks: K0, K1, K2, fp16 tier, v scale, v min
+    int off_merge;    // merge scratch (aliases qperm/qs; free when the partial is stored)
+    int merge_floats;
     int lds_bytes;
 };
 
@@ -149,11 +151,22 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a0, uint32_t a1, uint32
     o[3] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);
 }
 
+constexpr int kMaxSlots = 2;  // integer-tier slots per thread (nb_int * 8 <= 512)
+
 struct Stage {
     uint4 c[kMaxStage];
     uint32_t v[4];
+    uint32_t ks[kMaxSlots];  // fp16 (min << 16 | scale) of the thread's Key slots
     int64_t row0;
 };
+
+// Tier and tier-local rank of integer-tier slot ``e`` = 8 * block + position.
+__device__ __forceinline__ void slot_of(const MfmaLayout& y, int e, int& tier, int& j) {
+    const int gb = e >> 3, pos = e & 7;
+    tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
+    const int lb = gb - 4 * y.kfirst[tier];
+    j = lb < y.nblk[tier] ? block_slot(tier, lb, pos) : 0x7fff;
+}
 
 // 16-byte chunk ``c`` of page ``row0``'s contiguous blocks (K tiers 0..2, fp16 tier, v scale, v min).
 __device__ __forceinline__ uint4 chunk_load(const lf_packed_layer& L, const MfmaLayout& y, int64_t row0, int c) {
@@ -184,6 +197,21 @@ __device__ __forceinline__ void stage_load(Stage& s, const lf_packed_layer& L, c
     const int32_t* vc = L.v_code + (row0 + 4 * tg) * 8 + w;
 #pragma unroll
     for (int i = 0; i < 4; ++i) s.v[i] = static_cast<uint32_t>(vc[8 * i]);
+    // Key scale/min of this page for the thread's integer-tier slots.
+#pragma unroll
+    for (int i = 0; i < kMaxSlots; ++i) {
+        const int e = threadIdx.x + i * kThreads;
+        uint32_t v = 0u;
+        if (e < y.nb_int * 8) {
+            int tier, j;
+            slot_of(y, e, tier, j);
+            if (j < L.k_width[tier]) {
+                const int64_t gi = kgrp_idx(L, b, h, L.k_width[tier], j, page);
+                v = static_cast<uint32_t>(L.k_scale[tier][gi]) | (static_cast<uint32_t>(L.k_min[tier][gi]) << 16);
+            }
+        }
+        s.ks[i] = v;
+    }
 }
 
 // Write one 16-byte chunk into page buffer ``pb``.
@@ -227,6 +255,14 @@ __device__ __forceinline__ void stage_store(const Stage& s, unsigned char* pb, c
     }
     for (int c = threadIdx.x + kMaxStage * kThreads; c < y.seg_end[5]; c += kThreads)
         chunk_store(pb, L, y, c, chunk_load(L, y, s.row0, c));
+#pragma unroll
+    for (int i = 0; i < kMaxSlots; ++i) {
+        const int e = threadIdx.x + i * kThreads;
+        if (e < y.nb_int * 8) {
+            reinterpret_cast<float*>(pb + y.pb_ksc)[e] = f16_to_f32(static_cast<uint16_t>(s.ks[i] & 0xffffu));
+            reinterpret_cast<float*>(pb + y.pb_kmn)[e] = f16_to_f32(static_cast<uint16_t>(s.ks[i] >> 16));
+        }
+    }
     uint32_t o[4];
     byte_transpose4(s.v[0], s.v[1], s.v[2], s.v[3], o);
     const int tg = threadIdx.x >> 3, w = threadIdx.x & 7;
@@ -261,7 +297,24 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     float* wstat = small + 64;            // [4 waves][3][8]: m, l, mv per head
     float* qlin = reinterpret_cast<float*>(smem + y.off_pb[0]);  // [8][128] q (residual path only)
 
-    // ---- q * scaling * log2(e) permuted into slot order (0 for padding slots / heads >= g) ----
+    // ---- q (scaled into the log2 domain) and this head's tier table, one coalesced pass ----
+    int16_t* tt = reinterpret_cast<int16_t*>(smem + y.off_tt);  // ranks -> channels, tiers back to back
+    int tt_off[4];
+    tt_off[0] = 0;
+    for (int t = 1; t < 4; ++t) tt_off[t] = tt_off[t - 1] + L.k_width[t - 1];
+    for (int e = tid; e < 8 * kD; e += kThreads) {
+        const int n = e / kD, c = e % kD;
+        qlin[e] = n < g ? load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD + c, A.q_dtype) *
+                              p.qscale
+                        : 0.f;
+    }
+    for (int e = tid; e < tt_off[3] + L.k_width[3]; e += kThreads) {
+        const int t = e >= tt_off[3] ? 3 : e >= tt_off[2] ? 2 : e >= tt_off[1] ? 1 : 0;
+        const int j = e - tt_off[t];
+        tt[e] = j < L.tier_count[t][h] ? static_cast<int16_t>(L.tier_index[t][h * L.k_width[t] + j]) : int16_t(-1);
+    }
+    __syncthreads();
+    // q permuted into slot order (0 for padding slots and heads >= g)
     for (int e = tid; e < y.nb * 64; e += kThreads) {
         const int gb = e >> 6, n = (e >> 3) & 7, pos = e & 7;
         int tier = 3;
@@ -269,11 +322,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             if (gb < 4 * (y.kfirst[t] + y.kst[t])) { tier = t; break; }
         const int lb = gb - 4 * y.kfirst[tier];
         float v = 0.f;
-        if (n < g && lb < y.nblk[tier]) {
+        if (lb < y.nblk[tier]) {
             const int j = block_slot(tier, lb, pos);
-            if (j < L.tier_count[tier][h]) {
-                const int c = L.tier_index[tier][h * L.k_width[tier] + j];
-                v = load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD + c, A.q_dtype) * p.qscale;
+            if (j < L.k_width[tier]) {
+                const int c = tt[tt_off[tier] + j];
+                if (c >= 0) v = qlin[n * kD + c];
             }
         }
         qperm[e] = v;
@@ -297,40 +350,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         Stage st;
         stage_load(st, L, y, b, h, pbeg);
         stage_store(st, smem + y.off_pb[0], L, y);
-        // (page buffer 0 is published by the barrier after the first scale staging)
-        float* sc = reinterpret_cast<float*>(smem + y.off_sc);
-        float* mn = reinterpret_cast<float*>(smem + y.off_mn);
+        __syncthreads();
         half8* qs = reinterpret_cast<half8*>(smem + y.off_qs);
         for (int page = pbeg; page < pend; ++page) {
             const int rel = page - pbeg;
             const int cbuf = rel & 1;
             unsigned char* pb = smem + y.off_pb[cbuf];
-            // Key scale/min of the next kChunkPages pages, in slot order.
-            if (rel % kChunkPages == 0) {
-                const int npg = min(kChunkPages, pend - page);
-                for (int e = tid; e < npg * y.nb_int * 8; e += kThreads) {
-                    const int pg = e / (y.nb_int * 8);
-                    const int slot = e - pg * y.nb_int * 8;
-                    const int gb = slot >> 3, pos = slot & 7;
-                    int tier = 0;
-                    if (gb >= 4 * y.kfirst[2]) tier = 2;
-                    else if (gb >= 4 * y.kfirst[1]) tier = 1;
-                    const int lb = gb - 4 * y.kfirst[tier];
-                    float s = 0.f, m0 = 0.f;
-                    if (lb < y.nblk[tier]) {
-                        const int j = block_slot(tier, lb, pos);
-                        if (j < L.k_width[tier]) {
-                            const int64_t gi = kgrp_idx(L, b, h, L.k_width[tier], j, page + pg);
-                            s = f16_to_f32(L.k_scale[tier][gi]);
-                            m0 = f16_to_f32(L.k_min[tier][gi]);
-                        }
-                    }
-                    sc[e] = s;
-                    mn[e] = m0;
-                }
-                __syncthreads();
-            }
-            const int crel = rel % kChunkPages;
+            const float* sc = reinterpret_cast<const float*>(pb + y.pb_ksc);
+            const float* mn = reinterpret_cast<const float*>(pb + y.pb_kmn);
             // Prefetch the next page into registers.
             const bool more = page + 1 < pend;
             if (more) stage_load(st, L, y, b, h, page + 1);
@@ -340,7 +367,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 const float* qrow = qperm + (gb * 8 + n) * 8;
                 float qv[8];
                 if (gb < y.nb_int) {
-                    const float* srow = sc + (crel * y.nb_int + gb) * 8;
+                    const float* srow = sc + gb * 8;
 #pragma unroll
                     for (int k = 0; k < 8; ++k) qv[k] = qrow[k] * srow[k];
                 } else {
@@ -361,7 +388,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 float acc = 0.f;
                 for (int gb = part; gb < y.nb_int; gb += 32) {
                     const float* qrow = qperm + (gb * 8 + n) * 8;
-                    const float* mrow = mn + (crel * y.nb_int + gb) * 8;
+                    const float* mrow = mn + gb * 8;
 #pragma unroll
                     for (int k = 0; k < 8; ++k) acc = fmaf(qrow[k], mrow[k], acc);
                 }
@@ -512,10 +539,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             const int kdt = t < tl ? A.tail_dtype : A.new_dtype;
             const int64_t kbase = t < tl ? ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + t) * kD
                                          : (static_cast<int64_t>(b) * L.n_kv + h) * kD;
-            for (int c = 0; c < kD; ++c) {
-                const float kv = load_as_f32(kp, kbase + c, kdt);
+            for (int c0 = 0; c0 < kD; c0 += 32) {
+                float kv[4][8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) s[i] = fmaf(qlin[i * kD + c], kv, s[i]);
+                for (int u = 0; u < 4; ++u) load8_as_f32(kp, kbase + c0 + 8 * u, kdt, kv[u]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) s[i] = fmaf(qlin[i * kD + c0 + 8 * u + k], kv[u][k], s[i]);
             }
         }
         float* pbuf = reinterpret_cast<float*>(smem + y.off_pbuf) + wave * 32 * 8;  // [32][8]
@@ -539,17 +572,23 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[cc][i] = 0.f;
+        const int64_t vrow0 = ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap) * kD;
+        const int64_t vnew = (static_cast<int64_t>(b) * L.n_kv + h) * kD;
+#pragma unroll 8
         for (int tt = 0; tt < cnt; ++tt) {
             const int tok = 32 * wave + tt;
+            float v0, v1;
+            if (tok < tl) {
+                v0 = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tok) * kD + 2 * lane, A.tail_dtype);
+                v1 = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tok) * kD + 2 * lane + 1, A.tail_dtype);
+            } else {
+                v0 = load_as_f32(A.v_new, vnew + 2 * lane, A.new_dtype);
+                v1 = load_as_f32(A.v_new, vnew + 2 * lane + 1, A.new_dtype);
+            }
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const int c = 2 * lane + cc;
-                const float v = tok < tl
-                    ? load_as_f32(A.tail_v, ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + tok) * kD + c,
-                                  A.tail_dtype)
-                    : load_as_f32(A.v_new, (static_cast<int64_t>(b) * L.n_kv + h) * kD + c, A.new_dtype);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[cc][i] = fmaf(pbuf[tt * 8 + i], v, acc[cc][i]);
+            for (int i = 0; i < 8; ++i) {
+                acc[0][i] = fmaf(pbuf[tt * 8 + i], v0, acc[0][i]);
+                acc[1][i] = fmaf(pbuf[tt * 8 + i], v1, acc[1][i]);
             }
         }
         float* red = reinterpret_cast<float*>(smem + y.off_pb[0]) + 8 * kD;  // [4][8][128], after qlin
@@ -599,7 +638,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         }
     }
     __shared__ int flag;
-    if (last_split_arrives(p, b, h, &flag)) merge_partials(p, b, h);
+    if (last_split_arrives(p, b, h, &flag))
+        merge_partials(p, b, h, reinterpret_cast<float*>(smem + y.off_merge), y.merge_floats);
 }
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
@@ -625,8 +665,9 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     int off = 0;
     y.off_qperm = off; off += y.nb * 64 * 4;
     y.off_qs = off; off += y.nb * 16 * 16;
-    y.off_sc = off; off += kChunkPages * y.nb_int * 8 * 4;
-    y.off_mn = off; off += kChunkPages * y.nb_int * 8 * 4;
+    y.off_merge = 0;
+    y.merge_floats = off / 4;
+    y.off_tt = off; off += round_up(2 * (L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3]), 16);
     y.off_small = off; off += (32 + 32 + 96) * 4;
     y.off_pbuf = off; off += 4 * 32 * 8 * 4;
     off = round_up(off, 16);
@@ -637,6 +678,8 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     y.pb_vt = pb; pb += 32 * 4 * 8 * 4;
     y.pb_vsc = pb; pb += kPage * 4;
     y.pb_vmn = pb; pb += kPage * 4;
+    y.pb_ksc = pb; pb += y.nb_int * 8 * 4;
+    y.pb_kmn = pb; pb += y.nb_int * 8 * 4;
     pb = round_up(pb, 16);
     // the reduction area [8][128] q + [4][8][128] wave outputs aliases the page buffers
     const int red_bytes = (8 + 32) * kD * 4;
@@ -650,7 +693,8 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     seg += kPage * L.k_width[3] * 2 / 16; y.seg_end[3] = seg;
     seg += kPage * 2 / 16; y.seg_end[4] = seg;
     seg += kPage * 2 / 16; y.seg_end[5] = seg;
-    if (y.lds_bytes > 160 * 1024) return false;
+    if (y.nb_int * 8 > kMaxSlots * kThreads) return false;
+    if (y.lds_bytes > 160 * 1024 - 64) return false;
     return true;
 }
 

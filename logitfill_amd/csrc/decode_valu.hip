@@ -262,7 +262,10 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
             r[D + 1] = lt;
         }
     }
-    if (last_split_arrives(p, b, h, &sm.flag)) merge_partials(p, b, h);
+    if (last_split_arrives(p, b, h, &sm.flag)) {
+        const int n_slots = off[3] + L.k_width[3];
+        merge_partials(p, b, h, qp, n_slots * kMaxG);
+    }
 }
 
 }  // namespace
