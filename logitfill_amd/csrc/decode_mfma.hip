@@ -6,32 +6,32 @@
 // page = Key group = 128 tokens, one Value group per token (v_group 128), int2
 // Values, 1 <= g = n_q/n_kv <= 8.  Anything else runs the VALU kernel.
 //
-// Work: one workgroup (4 waves) per (split item, kv head).  Pages of the item
-// are staged in LDS (double buffered through registers); each wave takes 32
-// of a page's 128 tokens.
+// Work: one workgroup (4 waves) per (split item, kv head).  Each page of the
+// item arrives by LDS-DMA (global_load_lds) in one of three raw LDS buffers,
+// two pages ahead of the page being computed, without passing through
+// registers; each wave computes 32 of the page's 128 tokens.  Partials
+// (m, l, o) of each item go to the workspace and decode_reduce_kernel merges
+// them (no inter-workgroup synchronisation).
 //
 // Scores.  With the Key scale folded into the query once per page,
-//     s[t][i] = sum_slot Qs[i][slot] * code[t][slot] + bias[i],
-//     Qs = q * scaling * log2(e) * scale_slot,  bias = sum_c q_c * min_c,
-// computed as S^T = Codes . Qs^T with the K dimension = the page's slots
-// ordered tier by tier in blocks of 8 codes (an int2 word gives two blocks,
-// an int4 word one, two int8 words one, eight fp16 values one); each K-step of
-// 32 covers four blocks of one tier.  Codes become exact fp16 integers
-// (magic-exponent OR, then -1024).  Qs is split hi + lo in fp16: columns
-// 0..7 hold hi, columns 8..15 lo (the GQA group has at most 8 heads), and
-// one DPP add recombines them, so the products carry ~22 bits.
+//     s[t][i] = sum_slot Qs[i][slot] * code[t][slot] + sum_c q_ic * min_c,
+//     Qs = q * scaling * log2(e) * scale_slot,
+// computed as S^T = Codes . Qs^T: the K dimension is the page's slots ordered
+// tier by tier in blocks of 8 codes; a K-step of 32 covers four blocks of one
+// tier.  A code becomes the fp16 value beta + code by placing its bits in the
+// mantissa under a fixed exponent (beta = 16 or 4 for int2, 256 or 16 for
+// int4, 1024 for int8, no transform for the fp16 tier); sum_slot Qs * beta
+// moves into the per-page bias.  Qs is split hi + lo in fp16 across columns
+// 0..7 / 8..15 (the GQA group has at most 8 heads) and one DPP add
+// recombines them.
 //
-// Values.  The S^T accumulator layout (lane: head n = lane%16, tokens
-// 4*kb+r of the two 16-token tiles, kb = lane/16) is exactly the A-operand
-// layout of O = P' . Codes_V with k = those 8 tokens, so probabilities feed
-// the second MFMA without data movement.  P' = p * vscale is again split
-// hi/lo across rows 0..7 / 8..15; the Value minimum enters through
-// sum_t p_t * vmin_t.  Value codes are byte-transposed at staging (one dword
-// = one byte column of 4 consecutive tokens) so each lane's 8 codes are two
-// LDS dwords.
-//
-// Softmax: per wave online max/sum in the log2 domain; the 4 waves' partials
-// merge in LDS; split items merge across workgroups (decode_common.hpp).
+// Values.  The S^T accumulator layout (lane: head n = lane%16, tokens 4*kb+r
+// of the wave's two 16-token tiles, kb = lane/16) is the A-operand layout of
+// O = P' . (code_V - 1.5), so probabilities feed the second MFMA in place.
+// P' = p * vscale is split hi/lo across rows 0..7 / 8..15; the Value midpoint
+// vmin + 1.5 * vscale enters through sum_t p_t * mid_t.  Value codes are
+// regrouped per page (one dword = one byte column of 4 consecutive tokens) so
+// each lane's 8 codes are two LDS dwords.
 #include "decode_common.hpp"
 
 namespace lf {
@@ -40,35 +40,39 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kThreads = 256;
 constexpr int kD = 128;
 constexpr int kPage = 128;
-constexpr int kMaxStage = 4;     // 16-byte staging chunks per thread per page
+constexpr int kNBuf = 3;       // raw page buffers (DMA runs kNBuf - 1 pages ahead)
+constexpr int kMaxDma = 8;     // 16-byte DMA instructions per wave per page
+constexpr int kMaxKsDma = 3;   // 4-byte Key scale/min DMA instructions per wave per page
+constexpr int kVcDma = 4;      // 4-byte Value-code DMA instructions per wave per page (1024 dwords)
 
 struct MfmaLayout {
-    int kst[4];      // K-steps per tier
-    int nblk[4];     // real 8-code blocks per tier
-    int kfirst[4];   // first K-step of each tier
-    int nb;          // padded blocks (4 per K-step)
-    int nb_int;      // padded blocks of the integer tiers
-    int w16p;        // fp16-tier row stride in LDS (multiple of 8)
-    int off_qperm;   // [nb][8 heads][8] fp32: q * scaling*log2e for each slot (0 for padding)
-    int off_qs;      // [nb][16][8] fp16: per-page Qs hi (rows 0..7) / lo (rows 8..15)
-    int off_tt;      // tier table of this kv head: ranks -> channel ids (int16), per tier
-    int off_small;   // bias partials [4][8], alpha [4][8], wave m/l/mv [4][3][8]
-    int off_pbuf;    // residual probabilities [4][32][8] fp32
-    int off_pb[2];   // page buffers
-    int pb_kt[3];    // [128][words_t] u32 Key codes of tier t
-    int pb_v16;      // [128][w16p] fp16 Key fp16 tier (zero padded)
-    int pb_vt;       // [32 token groups][4][8] u32 byte-transposed Value codes
-    int pb_vsc;      // [128] fp32 Value scale
-    int pb_vmn;      // [128] fp32 Value min
-    int pb_ksc;      // [nb_int][8] fp32 Key scale of each integer-tier slot (this page)
-    int pb_kmn;      // [nb_int][8] fp32 Key min
-    int seg_end[6];  // cumulative 16-byte chunks: K0, K1, K2, fp16 tier, v scale, v min
-    int off_merge;    // merge scratch (aliases qperm/qs; free when the partial is stored)
-    int merge_floats;
+    int kst[4];          // K-steps per tier (int2: even; K-step s takes half s&1 of 4 words)
+    int kfirst[4];       // first K-step of each tier
+    int nb;              // padded blocks (4 per K-step)
+    int nb_int;          // padded blocks of the integer tiers
+    int w16p;            // fp16-tier row stride in the cooked buffer (multiple of 8)
+    uint32_t w16_magic;  // ceil(2^32 / width16), width16 >= 2: e / width16 == umulhi(e, magic), e < 2^14
+    int seg_end[6];      // cumulative 16-byte chunks of a raw buffer: K0, K1, K2, fp16 tier, v scale, v min
+    int n_chunks;        // = seg_end[5]
+    int n_kslots;        // 2 * nb_int * 8: Key scale slots, then Key min slots
+    int raw_vc;          // raw: [32 groups][8 words][4 tokens] u32 Value codes
+    int raw_ks;          // raw: [n_kslots] u32 fp16 pairs (page & ~1, page | 1) of Key scale / min
+    int raw_bytes;
+    int ck_vt;           // cooked: [32 groups][36] u32 byte columns (4 per 8-word row) + 4 pad
+    int ck_v16;          // cooked: [128][w16p] fp16 Key fp16 tier, zero padded
+    int ck_vsc;          // cooked: [128] fp32 Value scale
+    int ck_vmid;         // cooked: [128] fp32 Value midpoint min + 1.5 * scale
+    int off_qperm;       // [nb][8 heads][8] fp32: q * scaling*log2e per slot (0 for padding)
+    int off_qs;          // [nb][16][8] fp16: Qs hi (rows 0..7) / lo (rows 8..15)
+    int off_tt;          // int16 tier table of this kv head (ranks -> channel ids), tiers back to back
+    int off_small;       // bias partials [4][8], alpha [4][8], wave m/l/mid [4][3][8]
+    int off_ck;
+    int off_raw[kNBuf];
     int lds_bytes;
 };
 
@@ -77,65 +81,112 @@ struct MfmaParams {
     MfmaLayout y;
 };
 
-__device__ __forceinline__ uint32_t lds_u32(const unsigned char* base, int byte) {
-    return *reinterpret_cast<const uint32_t*>(base + byte);
+// Barrier that orders LDS only: waits for this wave's LDS operations (and, in the
+// variant below, for its older LDS-DMA) but not for newer DMA still in flight.
+// The asm memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Slot (tier-local channel rank) of position ``pos`` (0..7) in local block ``lb``.
+// s_waitcnt vmcnt(n) lgkmcnt(0); s_barrier, for a run-time n (n >= 16 waits for everything).
+__device__ __forceinline__ void dma_barrier(int n) {
+#define LF_W(N) case N: asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    switch (n) {
+        LF_W(0) LF_W(1) LF_W(2) LF_W(3) LF_W(4) LF_W(5) LF_W(6) LF_W(7)
+        LF_W(8) LF_W(9) LF_W(10) LF_W(11) LF_W(12) LF_W(13) LF_W(14) LF_W(15)
+        default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    }
+#undef LF_W
+}
+
+// a[t] for a run-time t in 0..3 (or 0..2) through selects: a dynamic index into the kernel
+// argument would copy the whole argument block to scratch memory.
+template <class T>
+__device__ __forceinline__ T sel4(const T (&a)[4], int t) {
+    return t == 0 ? a[0] : t == 1 ? a[1] : t == 2 ? a[2] : a[3];
+}
+template <class T>
+__device__ __forceinline__ T sel3(const T (&a)[3], int t) {
+    return t == 0 ? a[0] : t == 1 ? a[1] : a[2];
+}
+
+// LDS-DMA: each lane's 16 (4) bytes at ``g`` land at lds + 16 (4) * lane.  Issued through
+// asm so the compiler does not order every later LDS read behind it (it cannot tell the
+// buffers apart and would wait for all DMA in flight); the waits are explicit instead.
+__device__ __forceinline__ uint32_t lds_addr(unsigned char* p) {
+    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)p)));
+}
+__device__ __forceinline__ void dma16(const unsigned char* g, unsigned char* lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+}
+__device__ __forceinline__ void dma4(const unsigned char* g, unsigned char* lds) {
+    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+}
+
+// (x & mask) | bits in one VOP3 instruction (mask in an SGPR, bits in a VGPR; VOP3 takes no literal).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t pk_add_h(uint32_t x, uint32_t c) {
+    const half2v r = __builtin_bit_cast(half2v, x) + __builtin_bit_cast(half2v, c);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Tier-local rank of position ``pos`` (0..7) of local block ``lb``.  Register r of a
+// block (positions 2r, 2r+1) holds the code pair the unpack helpers below produce.
 __device__ __forceinline__ int block_slot(int tier, int lb, int pos) {
     const int r = pos >> 1, odd = pos & 1;
-    if (tier == 0) {  // int2: word lb/2, half lb%2; register r = codes (4h+r, 4h+r+8)
-        return 16 * (lb >> 1) + 4 * (lb & 1) + r + 8 * odd;
+    if (tier == 0) {  // word 4*(lb/8) + lb%4, half (lb/4)%2: codes (4h + r, 4h + r + 8)
+        const int word = 4 * (lb >> 3) + (lb & 3), half = (lb >> 2) & 1;
+        return 16 * word + 4 * half + r + 8 * odd;
     }
-    if (tier == 1) {  // int4: register r = codes (r, r+4)
-        return 8 * lb + r + 4 * odd;
-    }
-    if (tier == 2) {  // int8 words 2lb, 2lb+1: register r = bytes ((r&1), (r&1)+2) of word 2lb + r/2
-        return 4 * (2 * lb + (r >> 1)) + (r & 1) + 2 * odd;
-    }
-    return 8 * lb + pos;  // fp16: natural order
+    if (tier == 1) return 8 * lb + r + 4 * odd;                          // int4 word lb: codes (r, r + 4)
+    if (tier == 2) return 4 * (2 * lb + (r >> 1)) + (r & 1) + 2 * odd;  // int8 words 2lb, 2lb+1: bytes (r&1, +2)
+    return 8 * lb + pos;                                                 // fp16: natural order
 }
 
-// Exact fp16 integers from magic-exponent patterns 0x6400|code (value 1024 + code).
-__device__ __forceinline__ uint32_t unbias(uint32_t x) {
-    half2v h = __builtin_bit_cast(half2v, x);
-    const half2v b = {static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
-    return __builtin_bit_cast(uint32_t, h + b);
+// Is local block ``lb`` of ``tier`` backed by stored words?
+__device__ __forceinline__ bool block_live(const lf_packed_layer& L, int tier, int lb) {
+    if (tier == 0) return 4 * (lb >> 3) + (lb & 3) < L.k_words[0];
+    if (tier == 1) return lb < L.k_words[1];
+    if (tier == 2) return 2 * lb < L.k_words[2];
+    return 8 * lb < L.k_width[3];
 }
 
-// The 8 fp16 codes of local block ``lb`` of ``tier`` for token row ``tok`` (A operand).
-__device__ __forceinline__ half8 load_block(const unsigned char* pb, const MfmaLayout& y, const lf_packed_layer& L,
-                                            int tier, int lb, int tok) {
-    uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-    if (lb < y.nblk[tier]) {
-        if (tier == 0) {
-            const uint32_t w = lds_u32(pb, y.pb_kt[0] + 4 * (tok * L.k_words[0] + (lb >> 1)));
-            const uint32_t x = w >> (8 * (lb & 1));
-            r0 = unbias((x & 0x00030003u) | 0x64006400u);
-            r1 = unbias(((x >> 2) & 0x00030003u) | 0x64006400u);
-            r2 = unbias(((x >> 4) & 0x00030003u) | 0x64006400u);
-            r3 = unbias(((x >> 6) & 0x00030003u) | 0x64006400u);
-        } else if (tier == 1) {
-            const uint32_t w = lds_u32(pb, y.pb_kt[1] + 4 * (tok * L.k_words[1] + lb));
-            r0 = unbias((w & 0x000F000Fu) | 0x64006400u);
-            r1 = unbias(((w >> 4) & 0x000F000Fu) | 0x64006400u);
-            r2 = unbias(((w >> 8) & 0x000F000Fu) | 0x64006400u);
-            r3 = unbias(((w >> 12) & 0x000F000Fu) | 0x64006400u);
-        } else if (tier == 2) {
-            const int wi = 2 * lb;
-            const uint32_t w0 = lds_u32(pb, y.pb_kt[2] + 4 * (tok * L.k_words[2] + wi));
-            const uint32_t w1 = (wi + 1 < L.k_words[2]) ? lds_u32(pb, y.pb_kt[2] + 4 * (tok * L.k_words[2] + wi + 1)) : 0u;
-            // bytes (0,2) and (1,3) of each word under a 0x64 high byte
-            r0 = unbias(__builtin_amdgcn_perm(w0, 0x64646464u, 0x00060004u));
-            r1 = unbias(__builtin_amdgcn_perm(w0, 0x64646464u, 0x00070005u));
-            r2 = unbias(__builtin_amdgcn_perm(w1, 0x64646464u, 0x00060004u));
-            r3 = unbias(__builtin_amdgcn_perm(w1, 0x64646464u, 0x00070005u));
-        } else {
-            const uint4 v = *reinterpret_cast<const uint4*>(pb + y.pb_v16 + 2 * (tok * y.w16p + 8 * lb));
-            r0 = v.x; r1 = v.y; r2 = v.z; r3 = v.w;
-        }
-    }
-    const uint4 u = {r0, r1, r2, r3};
+// Offset beta of position ``pos`` of an integer-tier block (the unpacked value is beta + code).
+__device__ __forceinline__ float slot_beta(int tier, int pos) {
+    if (tier == 0) return (pos & 2) ? 4.f : 16.f;
+    if (tier == 1) return (pos & 2) ? 16.f : 256.f;
+    return 1024.f;
+}
+
+// int2, half H of word w: registers r = (code 4H+r, code 4H+r+8); even r: bits to mantissa
+// 6..7 under exponent 16 (16 + c), odd r: bits 8..9 under exponent 4 (4 + c).
+template <int H>
+__device__ __forceinline__ half8 unpack2(uint32_t w) {
+    const uint32_t y1 = H == 0 ? (w << 6) : (w >> 2);
+    const uint32_t y2 = H == 0 ? (w << 2) : (w >> 6);
+    const uint4 u = {and_or(y1, 0x00C000C0u, 0x4C004C00u), and_or(y1, 0x03000300u, 0x44004400u),
+                     and_or(y2, 0x00C000C0u, 0x4C004C00u), and_or(y2, 0x03000300u, 0x44004400u)};
+    return __builtin_bit_cast(half8, u);
+}
+
+// int4 word: registers r = (code r, code r+4); even r: mantissa 2..5 under 256 (256 + c),
+// odd r: mantissa 6..9 under 16 (16 + c).
+__device__ __forceinline__ half8 unpack4(uint32_t w) {
+    const uint32_t y1 = w << 2, y2 = w >> 6;
+    const uint4 u = {and_or(y1, 0x003C003Cu, 0x5C005C00u), and_or(y1, 0x03C003C0u, 0x4C004C00u),
+                     and_or(y2, 0x003C003Cu, 0x5C005C00u), and_or(y2, 0x03C003C0u, 0x4C004C00u)};
+    return __builtin_bit_cast(half8, u);
+}
+
+// int8 words w0, w1: registers (bytes 0, 2), (1, 3) of each under a 0x64 high byte (1024 + c).
+__device__ __forceinline__ half8 unpack8(uint32_t w0, uint32_t w1) {
+    const uint4 u = {__builtin_amdgcn_perm(w0, 0x64646464u, 0x00060004u), __builtin_amdgcn_perm(w0, 0x64646464u, 0x00070005u),
+                     __builtin_amdgcn_perm(w1, 0x64646464u, 0x00060004u), __builtin_amdgcn_perm(w1, 0x64646464u, 0x00070005u)};
     return __builtin_bit_cast(half8, u);
 }
 
@@ -151,124 +202,109 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a0, uint32_t a1, uint32
     o[3] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);
 }
 
-constexpr int kMaxSlots = 2;  // integer-tier slots per thread (nb_int * 8 <= 512)
-
-struct Stage {
-    uint4 c[kMaxStage];
-    uint32_t v[4];
-    uint32_t ks[kMaxSlots];  // fp16 (min << 16 | scale) of the thread's Key slots
-    int64_t row0;
+// Per-lane DMA sources of the next page to fetch; dma_page advances them one page.
+struct DmaSrc {
+    const unsigned char* chunk[kMaxDma];
+    int chunk_stride[kMaxDma];  // bytes per page of the chunk's segment
+    const unsigned char* vc[kVcDma];
+    const unsigned char* ks[kMaxKsDma];
+    int n_chunk;  // 16-byte DMA instructions this wave issues per page
+    int n_ks;     // 4-byte scale DMA instructions this wave issues per page
 };
 
-// Tier and tier-local rank of integer-tier slot ``e`` = 8 * block + position.
-__device__ __forceinline__ void slot_of(const MfmaLayout& y, int e, int& tier, int& j) {
-    const int gb = e >> 3, pos = e & 7;
-    tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
-    const int lb = gb - 4 * y.kfirst[tier];
-    j = lb < y.nblk[tier] ? block_slot(tier, lb, pos) : 0x7fff;
-}
-
-// 16-byte chunk ``c`` of page ``row0``'s contiguous blocks (K tiers 0..2, fp16 tier, v scale, v min).
-__device__ __forceinline__ uint4 chunk_load(const lf_packed_layer& L, const MfmaLayout& y, int64_t row0, int c) {
-    const unsigned char* src;
-    int off;
-    if (c < y.seg_end[0]) { src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]); off = c; }
-    else if (c < y.seg_end[1]) { src = reinterpret_cast<const unsigned char*>(L.k_code[1] + row0 * L.k_words[1]); off = c - y.seg_end[0]; }
-    else if (c < y.seg_end[2]) { src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]); off = c - y.seg_end[1]; }
-    else if (c < y.seg_end[3]) { src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]); off = c - y.seg_end[2]; }
-    else if (c < y.seg_end[4]) { src = reinterpret_cast<const unsigned char*>(L.v_scale + row0); off = c - y.seg_end[3]; }
-    else { src = reinterpret_cast<const unsigned char*>(L.v_min + row0); off = c - y.seg_end[4]; }
-    return *reinterpret_cast<const uint4*>(src + 16 * static_cast<int64_t>(off));
-}
-
-// Issue the global loads of page ``page`` of (b, h) into registers (the first kMaxStage
-// chunks per thread; stage_store fetches any remainder itself).
-__device__ __forceinline__ void stage_load(Stage& s, const lf_packed_layer& L, const MfmaLayout& y, int b, int h,
-                                           int page) {
-    const int64_t row0 = tok_row(L, b, h, static_cast<int64_t>(page) * kPage);
-    s.row0 = row0;
+__device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout& y, int b, int h, int pbeg,
+                          int wave, int lane) {
+    const int64_t row0 = tok_row(L, b, h, static_cast<int64_t>(pbeg) * kPage);
+    s.n_chunk = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxStage; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        s.c[i] = c < y.seg_end[5] ? chunk_load(L, y, row0, c) : uint4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < kMaxDma; ++i) {
+        const int c0 = (4 * i + wave) * 64;
+        if (c0 < y.n_chunks) s.n_chunk = i + 1;
+        int c = c0 + lane;
+        if (c >= y.n_chunks) c = 0;  // spare lanes of the last instruction re-read chunk 0 into slack
+        const unsigned char* src;
+        int stride;
+        if (c < y.seg_end[0]) {
+            src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]) + 16 * c;
+            stride = kPage * L.k_words[0] * 4;
+        } else if (c < y.seg_end[1]) {
+            src = reinterpret_cast<const unsigned char*>(L.k_code[1] + row0 * L.k_words[1]) + 16 * (c - y.seg_end[0]);
+            stride = kPage * L.k_words[1] * 4;
+        } else if (c < y.seg_end[2]) {
+            src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]) + 16 * (c - y.seg_end[1]);
+            stride = kPage * L.k_words[2] * 4;
+        } else if (c < y.seg_end[3]) {
+            src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]) + 16 * (c - y.seg_end[2]);
+            stride = kPage * L.k_width[3] * 2;
+        } else if (c < y.seg_end[4]) {
+            src = reinterpret_cast<const unsigned char*>(L.v_scale + row0) + 16 * (c - y.seg_end[3]);
+            stride = kPage * 2;
+        } else {
+            src = reinterpret_cast<const unsigned char*>(L.v_min + row0) + 16 * (c - y.seg_end[4]);
+            stride = kPage * 2;
+        }
+        s.chunk[i] = src;
+        s.chunk_stride[i] = stride;
     }
-    // Value codes: 4 consecutive tokens of one word (token group tid/8, word tid%8).
-    const int tg = threadIdx.x >> 3, w = threadIdx.x & 7;
-    const int32_t* vc = L.v_code + (row0 + 4 * tg) * 8 + w;
+    // Value codes: dword e of the regrouped page = word (e/4)%8 of token 4*(e/32) + e%4.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s.v[i] = static_cast<uint32_t>(vc[8 * i]);
-    // Key scale/min of this page for the thread's integer-tier slots.
+    for (int i = 0; i < kVcDma; ++i) {
+        const int e = (4 * i + wave) * 64 + lane;
+        const int tok = 4 * (e >> 5) + (e & 3), word = (e >> 2) & 7;
+        s.vc[i] = reinterpret_cast<const unsigned char*>(L.v_code + (row0 + tok) * 8 + word);
+    }
+    // Key scale/min slots: one dword = the fp16 pair of pages (p & ~1, p | 1) of one slot.
+    // Padding slots read slot 0 of the first integer tier (their q is zero).
+    s.n_ks = 0;
+    const int t0 = L.k_width[0] ? 0 : L.k_width[1] ? 1 : 2;
+    const unsigned char* dummy = reinterpret_cast<const unsigned char*>(
+        sel3(L.k_scale, t0) + kgrp_idx(L, b, h, sel4(L.k_width, t0), 0, pbeg & ~1));
 #pragma unroll
-    for (int i = 0; i < kMaxSlots; ++i) {
-        const int e = threadIdx.x + i * kThreads;
-        uint32_t v = 0u;
-        if (e < y.nb_int * 8) {
-            int tier, j;
-            slot_of(y, e, tier, j);
-            if (j < L.k_width[tier]) {
-                const int64_t gi = kgrp_idx(L, b, h, L.k_width[tier], j, page);
-                v = static_cast<uint32_t>(L.k_scale[tier][gi]) | (static_cast<uint32_t>(L.k_min[tier][gi]) << 16);
+    for (int i = 0; i < kMaxKsDma; ++i) {
+        const int e0 = (4 * i + wave) * 64;
+        if (e0 < y.n_kslots) s.n_ks = i + 1;
+        const int e = e0 + lane;
+        const unsigned char* src = dummy;
+        if (e < y.n_kslots) {
+            const bool is_min = e >= y.n_kslots / 2;
+            const int slot = is_min ? e - y.n_kslots / 2 : e;
+            const int gb = slot >> 3, pos = slot & 7;
+            const int tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
+            const int lb = gb - 4 * sel4(y.kfirst, tier);
+            if (block_live(L, tier, lb)) {
+                const int j = block_slot(tier, lb, pos);
+                const int width = sel4(L.k_width, tier);
+                if (j < width) {
+                    const uint16_t* base = is_min ? sel3(L.k_min, tier) : sel3(L.k_scale, tier);
+                    src = reinterpret_cast<const unsigned char*>(base + kgrp_idx(L, b, h, width, j, pbeg & ~1));
+                }
             }
         }
-        s.ks[i] = v;
+        s.ks[i] = src;
     }
 }
 
-// Write one 16-byte chunk into page buffer ``pb``.
-__device__ __forceinline__ void chunk_store(unsigned char* pb, const lf_packed_layer& L, const MfmaLayout& y, int c,
-                                            uint4 v) {
-    if (c < y.seg_end[0]) {
-        *reinterpret_cast<uint4*>(pb + y.pb_kt[0] + 16 * c) = v;
-    } else if (c < y.seg_end[1]) {
-        *reinterpret_cast<uint4*>(pb + y.pb_kt[1] + 16 * (c - y.seg_end[0])) = v;
-    } else if (c < y.seg_end[2]) {
-        *reinterpret_cast<uint4*>(pb + y.pb_kt[2] + 16 * (c - y.seg_end[1])) = v;
-    } else if (c < y.seg_end[3]) {
-        // 8 fp16 values of the [128][w16] block -> padded rows [128][w16p]
-        const int e0 = 8 * (c - y.seg_end[2]);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        uint16_t* dst = reinterpret_cast<uint16_t*>(pb + y.pb_v16);
+// Issue the DMA of page ``page`` into raw buffer ``raw`` and advance the sources.
+__device__ __forceinline__ void dma_page(DmaSrc& s, unsigned char* raw, const MfmaLayout& y, int page, int wave) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int e = e0 + k;
-            const int tok = e / L.k_width[3], j = e - tok * L.k_width[3];
-            dst[tok * y.w16p + j] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
-        }
-    } else {
-        const bool is_min = c >= y.seg_end[4];
-        const int t0 = 8 * (c - (is_min ? y.seg_end[4] : y.seg_end[3]));
-        float* dst = reinterpret_cast<float*>(pb + (is_min ? y.pb_vmn : y.pb_vsc)) + t0;
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) dst[k] = f16_to_f32(static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1))));
-    }
-}
-
-// Write staged registers into page buffer ``pb``; chunks past the register budget are
-// fetched here directly.
-__device__ __forceinline__ void stage_store(const Stage& s, unsigned char* pb, const lf_packed_layer& L,
-                                            const MfmaLayout& y) {
-#pragma unroll
-    for (int i = 0; i < kMaxStage; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        if (c < y.seg_end[5]) chunk_store(pb, L, y, c, s.c[i]);
-    }
-    for (int c = threadIdx.x + kMaxStage * kThreads; c < y.seg_end[5]; c += kThreads)
-        chunk_store(pb, L, y, c, chunk_load(L, y, s.row0, c));
-#pragma unroll
-    for (int i = 0; i < kMaxSlots; ++i) {
-        const int e = threadIdx.x + i * kThreads;
-        if (e < y.nb_int * 8) {
-            reinterpret_cast<float*>(pb + y.pb_ksc)[e] = f16_to_f32(static_cast<uint16_t>(s.ks[i] & 0xffffu));
-            reinterpret_cast<float*>(pb + y.pb_kmn)[e] = f16_to_f32(static_cast<uint16_t>(s.ks[i] >> 16));
+    for (int i = 0; i < kMaxDma; ++i) {
+        if (i < s.n_chunk) {
+            dma16(s.chunk[i], raw + (4 * i + wave) * 1024);
+            s.chunk[i] += s.chunk_stride[i];
         }
     }
-    uint32_t o[4];
-    byte_transpose4(s.v[0], s.v[1], s.v[2], s.v[3], o);
-    const int tg = threadIdx.x >> 3, w = threadIdx.x & 7;
-    uint32_t* vt = reinterpret_cast<uint32_t*>(pb + y.pb_vt);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) vt[(tg * 4 + k) * 8 + w] = o[k];
+    for (int i = 0; i < kVcDma; ++i) {
+        dma4(s.vc[i], raw + y.raw_vc + (4 * i + wave) * 256);
+        s.vc[i] += kPage * 32;
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxKsDma; ++i) {
+        if (i < s.n_ks) {
+            dma4(s.ks[i], raw + y.raw_ks + (4 * i + wave) * 256);
+            if (page & 1) s.ks[i] += 4;
+        }
+    }
 }
 
 __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
@@ -280,9 +316,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int n16 = lane & 15;   // MFMA column / row index
-    const int kb = lane >> 4;    // lane group
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n16 = lane & 15;  // MFMA column / row index
+    const int kb = lane >> 4;   // lane group
     const int g = p.g;
     const int b = A.work[4 * item + 0];
     const int pbeg = A.work[4 * item + 1];
@@ -292,13 +328,19 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     extern __shared__ __align__(16) unsigned char smem[];
     float* qperm = reinterpret_cast<float*>(smem + y.off_qperm);
     float* small = reinterpret_cast<float*>(smem + y.off_small);
-    float* bpart = small;                 // [4 waves][8]: partial bias sums
-    float* alpha_lds = small + 32;        // [4 waves][8]: softmax rescale per head
-    float* wstat = small + 64;            // [4 waves][3][8]: m, l, mv per head
-    float* qlin = reinterpret_cast<float*>(smem + y.off_pb[0]);  // [8][128] q (residual path only)
+    float* bpart = small;           // [4 waves][8]: partial bias sums
+    float* alpha_lds = small + 32;  // [4 waves][8]: softmax rescale per head
+    float* wstat = small + 64;      // [4 waves][3][8]: m, l, mid per head
+    // Aliases of the raw buffers (free outside the page loop): q [8][128], wave outputs
+    // [4][8][128], residual probabilities [4][32][8].
+    float* qlin = reinterpret_cast<float*>(smem + y.off_raw[0]);
+    float* red = qlin + 8 * kD;
+    float* pbuf = red + 32 * kD;
+    unsigned char* ck = smem + y.off_ck;
+    half8* qs = reinterpret_cast<half8*>(smem + y.off_qs);
 
-    // ---- q (scaled into the log2 domain) and this head's tier table, one coalesced pass ----
-    int16_t* tt = reinterpret_cast<int16_t*>(smem + y.off_tt);  // ranks -> channels, tiers back to back
+    // ---- q (scaled into the log2 domain) and this head's tier table ----
+    int16_t* tt = reinterpret_cast<int16_t*>(smem + y.off_tt);
     int tt_off[4];
     tt_off[0] = 0;
     for (int t = 1; t < 4; ++t) tt_off[t] = tt_off[t - 1] + L.k_width[t - 1];
@@ -310,26 +352,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     }
     for (int e = tid; e < tt_off[3] + L.k_width[3]; e += kThreads) {
         const int t = e >= tt_off[3] ? 3 : e >= tt_off[2] ? 2 : e >= tt_off[1] ? 1 : 0;
-        const int j = e - tt_off[t];
-        tt[e] = j < L.tier_count[t][h] ? static_cast<int16_t>(L.tier_index[t][h * L.k_width[t] + j]) : int16_t(-1);
-    }
-    __syncthreads();
-    // q permuted into slot order (0 for padding slots and heads >= g)
-    for (int e = tid; e < y.nb * 64; e += kThreads) {
-        const int gb = e >> 6, n = (e >> 3) & 7, pos = e & 7;
-        int tier = 3;
-        for (int t = 0; t < 3; ++t)
-            if (gb < 4 * (y.kfirst[t] + y.kst[t])) { tier = t; break; }
-        const int lb = gb - 4 * y.kfirst[tier];
-        float v = 0.f;
-        if (lb < y.nblk[tier]) {
-            const int j = block_slot(tier, lb, pos);
-            if (j < L.k_width[tier]) {
-                const int c = tt[tt_off[tier] + j];
-                if (c >= 0) v = qlin[n * kD + c];
-            }
-        }
-        qperm[e] = v;
+        const int j = e - sel4(tt_off, t);
+        tt[e] = j < sel4(L.tier_count, t)[h] ? static_cast<int16_t>(sel4(L.tier_index, t)[h * sel4(L.k_width, t) + j])
+                                             : int16_t(-1);
     }
     __syncthreads();
 
@@ -338,41 +363,90 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) O[nt][r] = 0.f;
-    float m_run = -__builtin_inff(), l_run = 0.f, mv_run = 0.f;
+    float m_run = -__builtin_inff(), l_run = 0.f, mid_run = 0.f;
 
     if (kind == 0) {
-        // fp16-tier rows are padded to w16p columns; the padding must read as zero
-        for (int e = tid; e < kPage * y.w16p / 2; e += kThreads) {
-            reinterpret_cast<uint32_t*>(smem + y.off_pb[0] + y.pb_v16)[e] = 0u;
-            reinterpret_cast<uint32_t*>(smem + y.off_pb[1] + y.pb_v16)[e] = 0u;
+        // q permuted into slot order (0 for padding slots and heads >= g)
+        for (int e = tid; e < y.nb * 64; e += kThreads) {
+            const int gb = e >> 6, n = (e >> 3) & 7, pos = e & 7;
+            const int tier = gb >= 4 * y.kfirst[3] ? 3 : gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
+            const int lb = gb - 4 * sel4(y.kfirst, tier);
+            float v = 0.f;
+            if (block_live(L, tier, lb)) {
+                const int j = block_slot(tier, lb, pos);
+                if (j < sel4(L.k_width, tier)) {
+                    const int c = tt[sel4(tt_off, tier) + j];
+                    if (c >= 0) v = qlin[n * kD + c];
+                }
+            }
+            qperm[e] = v;
         }
-        __syncthreads();
-        Stage st;
-        stage_load(st, L, y, b, h, pbeg);
-        stage_store(st, smem + y.off_pb[0], L, y);
-        __syncthreads();
-        half8* qs = reinterpret_cast<half8*>(smem + y.off_qs);
+        // Qs rows of heads >= g are never rewritten: zero them once; fp16-tier padding columns too.
+        for (int e = tid; e < y.nb * 16; e += kThreads)
+            if ((e & 7) >= g) qs[e] = half8{};
+        for (int e = tid; e < kPage * y.w16p / 2; e += kThreads) reinterpret_cast<uint32_t*>(ck + y.ck_v16)[e] = 0u;
+        __syncthreads();  // qlin (raw buffer 0) is dead from here on
+
+        DmaSrc ds;
+        dma_setup(ds, L, y, b, h, pbeg, wave, lane);
+        const int per_page = ds.n_chunk + kVcDma + ds.n_ks;  // DMA instructions per page of this wave
+        if (pbeg < pend) dma_page(ds, smem + y.off_raw[0], y, pbeg, wave);
+        if (pbeg + 1 < pend) dma_page(ds, smem + y.off_raw[1], y, pbeg + 1, wave);
+
+        const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
+        const int w16 = L.k_width[3];
+        const int sh = 2 * (n16 & 3);
+        const int tok0 = 32 * wave + n16, tok1 = tok0 + 16;
         for (int page = pbeg; page < pend; ++page) {
             const int rel = page - pbeg;
-            const int cbuf = rel & 1;
-            unsigned char* pb = smem + y.off_pb[cbuf];
-            const float* sc = reinterpret_cast<const float*>(pb + y.pb_ksc);
-            const float* mn = reinterpret_cast<const float*>(pb + y.pb_kmn);
-            // Prefetch the next page into registers.
-            const bool more = page + 1 < pend;
-            if (more) stage_load(st, L, y, b, h, page + 1);
-            // Qs (hi rows 0..7, lo rows 8..15) for this page.
+            const unsigned char* raw = smem + y.off_raw[0] + (rel % kNBuf) * y.raw_bytes;
+            // this page's DMA complete (every wave), previous page's readers done
+            dma_barrier(page + 1 < pend ? per_page : 0);
+            if (page + 2 < pend) dma_page(ds, smem + y.off_raw[0] + ((rel + 2) % kNBuf) * y.raw_bytes, y, page + 2, wave);
+
+            // ---- per-page preparation: Value regroup, Value scale/mid, fp16 rows, Qs, bias ----
+            {
+                const int tg = tid >> 3, w = tid & 7;
+                const uint4 a = *reinterpret_cast<const uint4*>(raw + y.raw_vc + 16 * (tg * 8 + w));
+                uint32_t o[4];
+                byte_transpose4(a.x, a.y, a.z, a.w, o);
+                uint32_t* vt = reinterpret_cast<uint32_t*>(ck + y.ck_vt);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = o[k];
+            }
+            if (tid < kPage) {
+                const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + 16 * y.seg_end[3]);
+                const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + 16 * y.seg_end[4]);
+                const float s = f16_to_f32(vs[tid]);
+                reinterpret_cast<float*>(ck + y.ck_vsc)[tid] = s;
+                reinterpret_cast<float*>(ck + y.ck_vmid)[tid] = fmaf(1.5f, s, f16_to_f32(vm[tid]));
+            }
+            if (w16 > 0) {
+                const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw + 16 * y.seg_end[2]);
+                uint16_t* dst = reinterpret_cast<uint16_t*>(ck + y.ck_v16);
+                for (int e = tid; e < kPage * w16; e += kThreads) {
+                    const int tok = w16 == 1 ? e : static_cast<int>(__umulhi(static_cast<uint32_t>(e), y.w16_magic));
+                    dst[tok * y.w16p + (e - tok * w16)] = f16[e];
+                }
+            }
+            const int par = 16 * (page & 1);
+            const uint32_t* ksr = reinterpret_cast<const uint32_t*>(raw + y.raw_ks);
             for (int e = tid; e < y.nb * 16; e += kThreads) {
                 const int gb = e >> 4, row = e & 15, n = row & 7;
+                if (n >= g) continue;
                 const float* qrow = qperm + (gb * 8 + n) * 8;
-                float qv[8];
+                const float4 q0 = *reinterpret_cast<const float4*>(qrow);
+                const float4 q1 = *reinterpret_cast<const float4*>(qrow + 4);
+                float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
                 if (gb < y.nb_int) {
-                    const float* srow = sc + gb * 8;
+                    const uint4 s0 = *reinterpret_cast<const uint4*>(ksr + gb * 8);
+                    const uint4 s1 = *reinterpret_cast<const uint4*>(ksr + gb * 8 + 4);
+                    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) qv[k] = qrow[k] * srow[k];
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) qv[k] = qrow[k];
+                    for (int k = 0; k < 8; ++k) {
+                        const float sc = f16_to_f32(static_cast<uint16_t>(sw[k] >> par));
+                        qv[k] = qv[k] != 0.f ? qv[k] * sc : 0.f;  // padding slots stay exactly 0
+                    }
                 }
                 half8 hv;
 #pragma unroll
@@ -382,48 +456,82 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 }
                 qs[e] = hv;
             }
-            // bias[n] = sum over integer-tier slots of q * min
             {
+                // bias[n] = sum over integer-tier slots of q * (min - beta * scale)
                 const int n = tid & 7, part = tid >> 3;  // 32 parts
                 float acc = 0.f;
                 for (int gb = part; gb < y.nb_int; gb += 32) {
+                    const int tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
                     const float* qrow = qperm + (gb * 8 + n) * 8;
-                    const float* mrow = mn + gb * 8;
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) acc = fmaf(qrow[k], mrow[k], acc);
+                    for (int k = 0; k < 8; ++k) {
+                        const float sc = f16_to_f32(static_cast<uint16_t>(ksr[gb * 8 + k] >> par));
+                        const float mn = f16_to_f32(static_cast<uint16_t>(ksr[y.n_kslots / 2 + gb * 8 + k] >> par));
+                        const float term = qrow[k] * fmaf(-slot_beta(tier, k), sc, mn);
+                        acc += qrow[k] != 0.f ? term : 0.f;
+                    }
                 }
                 acc += __shfl_xor(acc, 8, kWave);
                 acc += __shfl_xor(acc, 16, kWave);
                 acc += __shfl_xor(acc, 32, kWave);
                 if (lane < 8) bpart[wave * 8 + lane] = acc;
             }
-            __syncthreads();
+            lds_barrier();
             const float bias = (n16 < 8) ? bpart[n16] + bpart[8 + n16] + bpart[16 + n16] + bpart[24 + n16] : 0.f;
 
-            // ---- scores for this wave's 32 tokens ----
+            // ---- scores of this wave's 32 tokens ----
+            // Integer tiers read up to 7 dwords past their segment (still inside the raw
+            // buffer): those blocks have Qs == 0 and unpack to finite values.
             float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-            const int tok0 = 32 * wave + n16, tok1 = tok0 + 16;
-            for (int t = 0; t < 4; ++t) {
-                for (int s = 0; s < y.kst[t]; ++s) {
-                    const int gks = y.kfirst[t] + s;
-                    const half8 bq = qs[(4 * gks + kb) * 16 + n16];
-                    const int lb = 4 * s + kb;
-                    const half8 a0 = load_block(pb, y, L, t, lb, tok0);
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bq, acc0, 0, 0, 0);
-                    const half8 a1 = load_block(pb, y, L, t, lb, tok1);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bq, acc1, 0, 0, 0);
+            {
+                const uint32_t* k0 = reinterpret_cast<const uint32_t*>(raw);
+                for (int s2 = 0; s2 < y.kst[0] / 2; ++s2) {
+                    const int word = 4 * s2 + kb;
+                    const uint32_t wa = k0[tok0 * kw0 + word];
+                    const uint32_t wb = k0[tok1 * kw0 + word];
+                    const half8 bq0 = qs[(8 * s2 + kb) * 16 + n16];
+                    const half8 bq1 = qs[(8 * s2 + 4 + kb) * 16 + n16];
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wa), bq0, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wb), bq0, acc1, 0, 0, 0);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wa), bq1, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wb), bq1, acc1, 0, 0, 0);
+                }
+                const uint32_t* k1 = reinterpret_cast<const uint32_t*>(raw + 16 * y.seg_end[0]);
+                for (int s = 0; s < y.kst[1]; ++s) {
+                    const int word = 4 * s + kb;
+                    const half8 bq = qs[(4 * (y.kfirst[1] + s) + kb) * 16 + n16];
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok0 * kw1 + word]), bq, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok1 * kw1 + word]), bq, acc1, 0, 0, 0);
+                }
+                const uint32_t* k2 = reinterpret_cast<const uint32_t*>(raw + 16 * y.seg_end[1]);
+                for (int s = 0; s < y.kst[2]; ++s) {
+                    const int w0 = 2 * (4 * s + kb);
+                    const half8 bq = qs[(4 * (y.kfirst[2] + s) + kb) * 16 + n16];
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok0 * kw2 + w0], k2[tok0 * kw2 + w0 + 1]), bq,
+                                                                  acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok1 * kw2 + w0], k2[tok1 * kw2 + w0 + 1]), bq,
+                                                                  acc1, 0, 0, 0);
+                }
+                const unsigned char* v16 = ck + y.ck_v16;
+                for (int s = 0; s < y.kst[3]; ++s) {
+                    const int col = 8 * (4 * s + kb);
+                    const bool ok = col < y.w16p;
+                    const uint4 ua = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok0 * y.w16p + col)) : uint4{0, 0, 0, 0};
+                    const uint4 ub = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok1 * y.w16p + col)) : uint4{0, 0, 0, 0};
+                    const half8 bq = qs[(4 * (y.kfirst[3] + s) + kb) * 16 + n16];
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ua), bq, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ub), bq, acc1, 0, 0, 0);
                 }
             }
-            // hi + lo columns, + bias; lanes n16 >= 8 carry don't-care values.  The accumulator
-            // elements are copied to scalars before the DPP move: applied directly to vector
-            // elements, this compiler emits a single DPP move for all of them.
+            // hi + lo columns (row_shl:8, zero outside the row), + bias.  The accumulator
+            // elements are copied to scalars before the DPP move: applied to vector elements
+            // directly, this compiler emits one move for all of them.
             float sv[8];
             const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 const int xi = __builtin_bit_cast(int, accs[r]);
-                sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x108, 0xf, 0xf, false)) +
-                        bias;
+                sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true)) + bias;
             }
             // ---- online softmax (log2 domain) ----
             float mx = sv[0];
@@ -434,27 +542,27 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
-            const float* vsc = reinterpret_cast<const float*>(pb + y.pb_vsc);
-            const float* vmn = reinterpret_cast<const float*>(pb + y.pb_vmn);
+            const float* vsc = reinterpret_cast<const float*>(ck + y.ck_vsc);
+            const float* vmd = reinterpret_cast<const float*>(ck + y.ck_vmid);
             const float4 s_lo = *reinterpret_cast<const float4*>(vsc + 32 * wave + 4 * kb);
             const float4 s_hi = *reinterpret_cast<const float4*>(vsc + 32 * wave + 16 + 4 * kb);
-            const float4 m_lo = *reinterpret_cast<const float4*>(vmn + 32 * wave + 4 * kb);
-            const float4 m_hi = *reinterpret_cast<const float4*>(vmn + 32 * wave + 16 + 4 * kb);
+            const float4 d_lo = *reinterpret_cast<const float4*>(vmd + 32 * wave + 4 * kb);
+            const float4 d_hi = *reinterpret_cast<const float4*>(vmd + 32 * wave + 16 + 4 * kb);
             const float vs[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
-            const float vm[8] = {m_lo.x, m_lo.y, m_lo.z, m_lo.w, m_hi.x, m_hi.y, m_hi.z, m_hi.w};
+            const float vd[8] = {d_lo.x, d_lo.y, d_lo.z, d_lo.w, d_hi.x, d_hi.y, d_hi.z, d_hi.w};
             float pp[8];
-            float psum = 0.f, pmin = 0.f;
+            float psum = 0.f, pmid = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float pi = __builtin_amdgcn_exp2f(sv[i] - m_new);
                 psum += pi;
-                pmin = fmaf(pi, vm[i], pmin);
+                pmid = fmaf(pi, vd[i], pmid);
                 pp[i] = pi * vs[i];
             }
             l_run = l_run * alpha + psum;
-            mv_run = mv_run * alpha + pmin;
-            // A operand of the value product: k order (t0,t2),(t1,t3),(t4,t6),(t5,t7) of the lane's
-            // tokens; hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8.
+            mid_run = mid_run * alpha + pmid;
+            // A operand of the value product: k order (t0,t2),(t1,t3),(t4,t6),(t5,t7) of the
+            // lane's tokens; hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8.
             uint32_t ahi[4], alo[4];
             const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
 #pragma unroll
@@ -473,60 +581,61 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             au.z = __builtin_amdgcn_update_dpp(ahi[2], alo[2], 0x118, 0xf, 0xc, false);
             au.w = __builtin_amdgcn_update_dpp(ahi[3], alo[3], 0x118, 0xf, 0xc, false);
             const half8 ap = __builtin_bit_cast(half8, au);
-            // alpha of the 4 output rows this lane holds (rows 4*kb + r, head (4*kb + r) % 8)
-            // (same-wave LDS write then read: ordered by the LDS queue)
+            // alpha of the 4 output rows this lane holds (rows 4*kb + r, head (4*kb + r) % 8);
+            // a same-wave LDS write then read is ordered by the LDS queue
             if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = alpha;
             __builtin_amdgcn_wave_barrier();
             const float4 arow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * (kb & 1));
             // ---- value product ----
-            const uint32_t* vt = reinterpret_cast<const uint32_t*>(pb + y.pb_vt);
-            const uint4 d0a = *reinterpret_cast<const uint4*>(vt + ((8 * wave + kb) * 4 + (n16 >> 2)) * 8);
-            const uint4 d0b = *reinterpret_cast<const uint4*>(vt + ((8 * wave + kb) * 4 + (n16 >> 2)) * 8 + 4);
-            const uint4 d1a = *reinterpret_cast<const uint4*>(vt + ((8 * wave + 4 + kb) * 4 + (n16 >> 2)) * 8);
-            const uint4 d1b = *reinterpret_cast<const uint4*>(vt + ((8 * wave + 4 + kb) * 4 + (n16 >> 2)) * 8 + 4);
+            const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + y.ck_vt);
+            const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
+            const uint4 d0b = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8 + 4);
+            const uint4 d1a = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8);
+            const uint4 d1b = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8 + 4);
             const uint32_t dlo[8] = {d0a.x, d0a.y, d0a.z, d0a.w, d0b.x, d0b.y, d0b.z, d0b.w};
             const uint32_t dhi[8] = {d1a.x, d1a.y, d1a.z, d1a.w, d1b.x, d1b.y, d1b.z, d1b.w};
-            const int sh = 2 * (n16 & 3);
-            const half2v inv256 = {static_cast<_Float16>(1.0f / 256.0f), static_cast<_Float16>(1.0f / 256.0f)};
-            const half2v m4 = {static_cast<_Float16>(-4.0f), static_cast<_Float16>(-4.0f)};
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
-                const uint32_t xl = dlo[nt] >> sh, xh = dhi[nt] >> sh;
+                // tokens (0, 2): code bits to mantissa 6..7 (16 + c), minus 17.5;
+                // tokens (1, 3): bits 8..9 (4 + c), minus 5.5  ->  c - 1.5
                 uint4 bu;
-                bu.x = unbias((xl & 0x00030003u) | 0x64006400u);                     // tokens (0, 2)
-                bu.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, (xl & 0x03000300u) | 0x64006400u) * inv256 + m4);  // (1, 3)
-                bu.z = unbias((xh & 0x00030003u) | 0x64006400u);
-                bu.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, (xh & 0x03000300u) | 0x64006400u) * inv256 + m4);
+                bu.x = pk_add_h(and_or(dlo[nt] << (6 - sh), 0x00C000C0u, 0x4C004C00u), 0xCC60CC60u);
+                bu.y = pk_add_h(and_or(dlo[nt] >> sh, 0x03000300u, 0x44004400u), 0xC580C580u);
+                bu.z = pk_add_h(and_or(dhi[nt] << (6 - sh), 0x00C000C0u, 0x4C004C00u), 0xCC60CC60u);
+                bu.w = pk_add_h(and_or(dhi[nt] >> sh, 0x03000300u, 0x44004400u), 0xC580C580u);
                 const half8 bv = __builtin_bit_cast(half8, bu);
                 float4v o4 = {O[nt][0] * arow.x, O[nt][1] * arow.y, O[nt][2] * arow.z, O[nt][3] * arow.w};
                 o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, bv, o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }
-            // Publish the prefetched page into the other buffer; the barrier also retires this page.
-            if (more) stage_store(st, smem + y.off_pb[cbuf ^ 1], L, y);
-            __syncthreads();
         }
-        // Reduce l and the value-minimum term over the 4 lane groups of each head.
+        // Reduce l and the midpoint term over the 4 lane groups of each head.
         l_run += __shfl_xor(l_run, 16, kWave);
         l_run += __shfl_xor(l_run, 32, kWave);
-        mv_run += __shfl_xor(mv_run, 16, kWave);
-        mv_run += __shfl_xor(mv_run, 32, kWave);
+        mid_run += __shfl_xor(mid_run, 16, kWave);
+        mid_run += __shfl_xor(mid_run, 32, kWave);
         // Rows r (hi, lanes kb 0..1) + rows r+8 (lo, lanes kb 2..3).
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) O[nt][r] += __shfl_xor(O[nt][r], 32, kWave);
+        __syncthreads();  // every wave is done with the raw buffers that ``red`` aliases
+        if (kb < 2) {
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[(wave * 8 + 4 * kb + r) * kD + 16 * nt + n16] = O[nt][r];
+        }
+        if (kb == 0 && n16 < 8) {
+            wstat[(wave * 3 + 0) * 8 + n16] = m_run;
+            wstat[(wave * 3 + 1) * 8 + n16] = l_run;
+            wstat[(wave * 3 + 2) * 8 + n16] = mid_run;
+        }
+        __syncthreads();
     } else {
         // ---- residual item: the tail page and the new token (at most page_size tokens) ----
         // VALU: wave w scores tokens 32w..32w+31 (lane = token), then accumulates them into
         // channels 2*lane, 2*lane+1.  One pass, so each wave's max is final.
-        for (int e = tid; e < 8 * kD; e += kThreads) {
-            const int n = e / kD, c = e % kD;
-            qlin[e] = n < g ? load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD + c, A.q_dtype) *
-                                  p.qscale
-                            : 0.f;
-        }
-        __syncthreads();
         const int tl = A.tail_len[b];
         const int n_res = tl + (A.k_new != nullptr ? 1 : 0);
         const int t = 32 * wave + lane;
@@ -551,14 +660,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                         for (int i = 0; i < 8; ++i) s[i] = fmaf(qlin[i * kD + c0 + 8 * u + k], kv[u][k], s[i]);
             }
         }
-        float* pbuf = reinterpret_cast<float*>(smem + y.off_pbuf) + wave * 32 * 8;  // [32][8]
+        float* pw = pbuf + wave * 32 * 8;  // [32][8]
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float x = act ? s[i] : -__builtin_inff();
             const float mx = wave_max(x);
             const float pi = act ? __builtin_amdgcn_exp2f(x - mx) : 0.f;
             const float lt = wave_sum(pi);
-            if (lane < 32) pbuf[lane * 8 + i] = pi;
+            if (lane < 32) pw[lane * 8 + i] = pi;
             if (lane == 0) {
                 wstat[(wave * 3 + 0) * 8 + i] = mx;
                 wstat[(wave * 3 + 1) * 8 + i] = lt;
@@ -575,8 +684,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         const int64_t vrow0 = ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap) * kD;
         const int64_t vnew = (static_cast<int64_t>(b) * L.n_kv + h) * kD;
 #pragma unroll 8
-        for (int tt = 0; tt < cnt; ++tt) {
-            const int tok = 32 * wave + tt;
+        for (int k = 0; k < cnt; ++k) {
+            const int tok = 32 * wave + k;
             float v0, v1;
             if (tok < tl) {
                 v0 = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tok) * kD + 2 * lane, A.tail_dtype);
@@ -587,11 +696,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                acc[0][i] = fmaf(pbuf[tt * 8 + i], v0, acc[0][i]);
-                acc[1][i] = fmaf(pbuf[tt * 8 + i], v1, acc[1][i]);
+                acc[0][i] = fmaf(pw[k * 8 + i], v0, acc[0][i]);
+                acc[1][i] = fmaf(pw[k * 8 + i], v1, acc[1][i]);
             }
         }
-        float* red = reinterpret_cast<float*>(smem + y.off_pb[0]) + 8 * kD;  // [4][8][128], after qlin
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
@@ -600,23 +708,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     }
 
     // ---- merge the 4 waves and store this item's partial ----
-    float* red = reinterpret_cast<float*>(smem + y.off_pb[0]) + 8 * kD;  // [4][8][128]
-    if (kind == 0) {
-        __syncthreads();
-        // head rows held by lanes kb 0..1: row 4*kb + r, channel 16*nt + n16
-        if (kb < 2) {
-#pragma unroll
-            for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) red[(wave * 8 + 4 * kb + r) * kD + 16 * nt + n16] = O[nt][r];
-        }
-        if (kb == 0 && n16 < 8) {
-            wstat[(wave * 3 + 0) * 8 + n16] = m_run;
-            wstat[(wave * 3 + 1) * 8 + n16] = l_run;
-            wstat[(wave * 3 + 2) * 8 + n16] = mv_run;
-        }
-        __syncthreads();
-    }
     for (int e = tid; e < g * kD; e += kThreads) {
         const int i = e / kD, c = e % kD;
         float M = -__builtin_inff();
@@ -637,65 +728,98 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             rec[kD + 1] = l;
         }
     }
-    __shared__ int flag;
-    if (last_split_arrives(p, b, h, &flag))
-        merge_partials(p, b, h, reinterpret_cast<float*>(smem + y.off_merge), y.merge_floats);
+}
+
+// One workgroup per (sequence, kv head): merge the sequence's partials into the output.
+__global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p, int lds_floats) {
+    extern __shared__ float wsc[];
+    const int b = blockIdx.x / p.L.n_kv;
+    const int h = blockIdx.x % p.L.n_kv;
+    merge_partials(p, b, h, wsc, lds_floats);
 }
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
 
 // Host: LDS layout for this layer; false when the shape is outside this kernel.
 bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     if (L.head_dim != kD || L.page_size != kPage || L.k_group != kPage || L.bit_v != 2 || L.v_group != kD)
         return false;
     if (g < 1 || g > 8) return false;
-    y.nblk[0] = 2 * L.k_words[0];
-    y.nblk[1] = L.k_words[1];
-    y.nblk[2] = (L.k_words[2] + 1) / 2;
-    y.nblk[3] = (L.k_width[3] + 7) / 8;
+    if (L.cap_kgroups % 2 != 0) return false;  // Key scale/min are fetched as page pairs
+    if (L.k_width[0] + L.k_width[1] + L.k_width[2] == 0) return false;
+    for (int t = 0; t < 3; ++t)
+        if (L.k_width[t] && (!aligned(L.k_code[t], 16) || !aligned(L.k_scale[t], 4) || !aligned(L.k_min[t], 4)))
+            return false;
+    if (L.k_width[3] && !aligned(L.k_value16, 16)) return false;
+    if (!aligned(L.v_code, 4) || !aligned(L.v_scale, 16) || !aligned(L.v_min, 16)) return false;
+    y.kst[0] = 2 * ((L.k_words[0] + 3) / 4);
+    y.kst[1] = (L.k_words[1] + 3) / 4;
+    y.kst[2] = ((L.k_words[2] + 1) / 2 + 3) / 4;
+    y.kst[3] = ((L.k_width[3] + 7) / 8 + 3) / 4;
     int ks = 0;
     for (int t = 0; t < 4; ++t) {
-        y.kst[t] = (y.nblk[t] + 3) / 4;
         y.kfirst[t] = ks;
         ks += y.kst[t];
     }
     y.nb = 4 * ks;
     y.nb_int = 4 * (y.kst[0] + y.kst[1] + y.kst[2]);
     y.w16p = round_up(L.k_width[3], 8);
-    int off = 0;
-    y.off_qperm = off; off += y.nb * 64 * 4;
-    y.off_qs = off; off += y.nb * 16 * 16;
-    y.off_merge = 0;
-    y.merge_floats = off / 4;
-    y.off_tt = off; off += round_up(2 * (L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3]), 16);
-    y.off_small = off; off += (32 + 32 + 96) * 4;
-    y.off_pbuf = off; off += 4 * 32 * 8 * 4;
-    off = round_up(off, 16);
-    int pb = 0;
-    for (int t = 0; t < 3; ++t) { y.pb_kt[t] = pb; pb += kPage * L.k_words[t] * 4; }
-    y.pb_v16 = pb; pb += kPage * y.w16p * 2;
-    pb = round_up(pb, 16);
-    y.pb_vt = pb; pb += 32 * 4 * 8 * 4;
-    y.pb_vsc = pb; pb += kPage * 4;
-    y.pb_vmn = pb; pb += kPage * 4;
-    y.pb_ksc = pb; pb += y.nb_int * 8 * 4;
-    y.pb_kmn = pb; pb += y.nb_int * 8 * 4;
-    pb = round_up(pb, 16);
-    // the reduction area [8][128] q + [4][8][128] wave outputs aliases the page buffers
-    const int red_bytes = (8 + 32) * kD * 4;
-    if (2 * pb < red_bytes) pb = round_up(red_bytes, 32) / 2;
-    y.off_pb[0] = off;
-    y.off_pb[1] = off + pb;
-    off += 2 * pb;
-    y.lds_bytes = off;
+    y.w16_magic = L.k_width[3] >= 2 ? static_cast<uint32_t>(((1ull << 32) + L.k_width[3] - 1) / L.k_width[3]) : 0u;
     int seg = 0;
-    for (int t = 0; t < 3; ++t) { seg += kPage * L.k_words[t] * 4 / 16; y.seg_end[t] = seg; }
-    seg += kPage * L.k_width[3] * 2 / 16; y.seg_end[3] = seg;
-    seg += kPage * 2 / 16; y.seg_end[4] = seg;
-    seg += kPage * 2 / 16; y.seg_end[5] = seg;
-    if (y.nb_int * 8 > kMaxSlots * kThreads) return false;
-    if (y.lds_bytes > 160 * 1024 - 64) return false;
-    return true;
+    for (int t = 0; t < 3; ++t) {
+        seg += kPage * L.k_words[t] * 4 / 16;
+        y.seg_end[t] = seg;
+    }
+    seg += kPage * L.k_width[3] * 2 / 16;
+    y.seg_end[3] = seg;
+    seg += kPage * 2 / 16;
+    y.seg_end[4] = seg;
+    seg += kPage * 2 / 16;
+    y.seg_end[5] = seg;
+    y.n_chunks = seg;
+    if (y.n_chunks > kMaxDma * 4 * 64) return false;
+    y.n_kslots = 2 * y.nb_int * 8;
+    if (y.n_kslots > kMaxKsDma * 4 * 64) return false;
+    // raw buffer: 16-byte chunks (each wave instruction fills 1 KB), Value codes, Key scales
+    int rb = ((y.n_chunks + 63) / 64) * 1024;
+    y.raw_vc = rb;
+    rb += 4096;
+    y.raw_ks = rb;
+    rb += ((y.n_kslots + 63) / 64) * 256;
+    y.raw_bytes = round_up(rb, 16);
+    int off = 0;
+    y.off_qperm = off;
+    off += y.nb * 64 * 4;
+    y.off_qs = off;
+    off += y.nb * 16 * 16;
+    y.off_tt = off;
+    off += round_up(2 * (L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3]), 16);
+    y.off_small = off;
+    off += (32 + 32 + 96) * 4;
+    off = round_up(off, 16);
+    y.off_ck = off;
+    int ck = 0;
+    y.ck_vt = ck;
+    ck += 32 * 36 * 4;
+    y.ck_v16 = ck;
+    ck += kPage * y.w16p * 2;
+    ck = round_up(ck, 16);
+    y.ck_vsc = ck;
+    ck += kPage * 4;
+    y.ck_vmid = ck;
+    ck += kPage * 4;
+    off += round_up(ck, 16);
+    for (int i = 0; i < kNBuf; ++i) {
+        y.off_raw[i] = off;
+        off += y.raw_bytes;
+    }
+    // q [8][128], wave outputs [4][8][128] and residual probabilities [4][32][8] alias the raw buffers
+    const int alias_bytes = (8 + 32) * kD * 4 + 4 * 32 * 8 * 4;
+    if (kNBuf * y.raw_bytes < alias_bytes) off += alias_bytes - kNBuf * y.raw_bytes;
+    y.lds_bytes = off;
+    return y.lds_bytes <= 160 * 1024 - 64;
 }
 
 }  // namespace
@@ -708,7 +832,7 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
         return LF_OK;
     }
     *handled = true;
-    // Raise the dynamic-LDS limit to what this launch needs (static LDS counts against the same budget).
+    // Raise the dynamic-LDS limit to what this launch needs.
     static int lds_limit = 64 * 1024;
     if (mp.y.lds_bytes > lds_limit) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_kernel),
@@ -717,7 +841,14 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
         lds_limit = mp.y.lds_bytes;
     }
     hipLaunchKernelGGL(decode_mfma_kernel, dim3(p.A.n_work, p.L.n_kv), dim3(kThreads), mp.y.lds_bytes, stream, mp);
-    const hipError_t err = hipGetLastError();
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return static_cast<int>(err);
+    // A sequence has at most n_work - batch + 1 items; weights for 2 * items * g floats when they fit.
+    const int64_t want = 2ll * (p.A.n_work - p.L.batch + 1) * p.g;
+    const int lds_floats = static_cast<int>(want < 8192 ? want : 8192);
+    hipLaunchKernelGGL(decode_reduce_kernel, dim3(p.L.batch * p.L.n_kv), dim3(256), lds_floats * sizeof(float), stream,
+                       p, lds_floats);
+    err = hipGetLastError();
     return err == hipSuccess ? LF_OK : static_cast<int>(err);
 }
 

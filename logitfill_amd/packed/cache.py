@@ -148,7 +148,10 @@ class _LayerStore:
         old, old_cap = self._s, self._cap
         B, H, D, dev = self.batch, self.n_kv, self.head_dim, self.device
         W, WD = self.widths, self.words
+        # Key-group capacity rounded up to even: the decode kernel fetches the fp16 scale/min of
+        # two consecutive pages as one aligned 4-byte word.
         groups = cap // self.k_group_size
+        groups += groups & 1
         s = {
             "k_code": [torch.zeros(B, H, cap, WD[t], dtype=torch.int32, device=dev) for t in range(3)],
             "k_scale": [torch.ones(B, H, W[t], groups, dtype=torch.float16, device=dev) for t in range(3)],
@@ -163,7 +166,7 @@ class _LayerStore:
             s["v_scale"] = torch.zeros(B, H, cap, vg, dtype=torch.float16, device=dev)
             s["v_min"] = torch.zeros(B, H, cap, vg, dtype=torch.float16, device=dev)
         if old is not None and old_cap:
-            og = old_cap // self.k_group_size
+            og = old["k_scale"][0].shape[-1]
             for t in range(3):
                 s["k_code"][t][:, :, :old_cap].copy_(old["k_code"][t])
                 s["k_scale"][t][..., :og].copy_(old["k_scale"][t])
@@ -186,7 +189,7 @@ class _LayerStore:
             s = self._s
             self._struct = make_layer_struct(
                 self.table, self._tables_dev, batch=self.batch, n_kv=self.n_kv, head_dim=self.head_dim,
-                cap_tokens=self._cap, cap_kgroups=self._cap // self.k_group_size, page_size=self.page_size,
+                cap_tokens=self._cap, cap_kgroups=int(s["k_scale"][0].shape[-1]), page_size=self.page_size,
                 k_group=self.k_group_size, v_group=self.v_group_size, bit_v=self.bit_v,
                 k_code=s["k_code"], k_scale=s["k_scale"], k_min=s["k_min"], k_value16=s["k_value16"],
                 v_code=s.get("v_code"), v_scale=s.get("v_scale"), v_min=s.get("v_min"),
