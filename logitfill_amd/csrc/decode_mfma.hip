@@ -27,9 +27,10 @@
 //
 // Values.  The S^T accumulator layout (lane: head n = lane%16, tokens 4*kb+r
 // of the wave's two 16-token tiles, kb = lane/16) is the A-operand layout of
-// O = P' . (code_V - 1.5), so probabilities feed the second MFMA in place.
-// P' = p * vscale is split hi/lo across rows 0..7 / 8..15; the Value midpoint
-// vmin + 1.5 * vscale enters through sum_t p_t * mid_t.  Value codes are
+// O = P' . (4 + code_V), so probabilities feed the second MFMA in place (4 + c
+// from the same exponent-field unpack).  P' = p * vscale is split hi/lo across
+// rows 0..7 / 8..15; the constant vmin - 4 * vscale enters through
+// sum_t p_t * mid_t.  Value codes are
 // regrouped per page (one dword = one byte column of 4 consecutive tokens) so
 // each lane's 8 codes are two LDS dwords.
 #include "decode_common.hpp"
@@ -66,7 +67,7 @@ struct MfmaLayout {
     int ck_vt;           // cooked: [32 groups][36] u32 byte columns (4 per 8-word row) + 4 pad
     int ck_v16;          // cooked: [128][w16p] fp16 Key fp16 tier, zero padded
     int ck_vsc;          // cooked: [128] fp32 Value scale
-    int ck_vmid;         // cooked: [128] fp32 Value midpoint min + 1.5 * scale
+    int ck_vmid;         // cooked: [128] fp32 vmin - 4 * vscale
     int off_qperm;       // [nb][8 heads][8] fp32: q * scaling*log2e per slot (0 for padding)
     int off_qs;          // [nb][16][8] fp16: Qs hi (rows 0..7) / lo (rows 8..15)
     int off_tt;          // int16 tier table of this kv head (ranks -> channel ids), tiers back to back
@@ -88,12 +89,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// s_waitcnt vmcnt(n) lgkmcnt(0); s_barrier, for a run-time n (n >= 16 waits for everything).
+// s_waitcnt vmcnt(n) lgkmcnt(0); s_barrier, for a run-time n (n >= 32 waits for everything).
 __device__ __forceinline__ void dma_barrier(int n) {
 #define LF_W(N) case N: asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
     switch (n) {
         LF_W(0) LF_W(1) LF_W(2) LF_W(3) LF_W(4) LF_W(5) LF_W(6) LF_W(7)
         LF_W(8) LF_W(9) LF_W(10) LF_W(11) LF_W(12) LF_W(13) LF_W(14) LF_W(15)
+        LF_W(16) LF_W(17) LF_W(18) LF_W(19) LF_W(20) LF_W(21) LF_W(22) LF_W(23)
+        LF_W(24) LF_W(25) LF_W(26) LF_W(27) LF_W(28) LF_W(29) LF_W(30) LF_W(31)
         default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
     }
 #undef LF_W
@@ -130,11 +133,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t b
     return r;
 }
 
-__device__ __forceinline__ uint32_t pk_add_h(uint32_t x, uint32_t c) {
-    const half2v r = __builtin_bit_cast(half2v, x) + __builtin_bit_cast(half2v, c);
-    return __builtin_bit_cast(uint32_t, r);
-}
-
 // Tier-local rank of position ``pos`` (0..7) of local block ``lb``.  Register r of a
 // block (positions 2r, 2r+1) holds the code pair the unpack helpers below produce.
 __device__ __forceinline__ int block_slot(int tier, int lb, int pos) {
@@ -154,13 +152,6 @@ __device__ __forceinline__ bool block_live(const lf_packed_layer& L, int tier, i
     if (tier == 1) return lb < L.k_words[1];
     if (tier == 2) return 2 * lb < L.k_words[2];
     return 8 * lb < L.k_width[3];
-}
-
-// Offset beta of position ``pos`` of an integer-tier block (the unpacked value is beta + code).
-__device__ __forceinline__ float slot_beta(int tier, int pos) {
-    if (tier == 0) return (pos & 2) ? 4.f : 16.f;
-    if (tier == 1) return (pos & 2) ? 16.f : 256.f;
-    return 1024.f;
 }
 
 // int2, half H of word w: registers r = (code 4H+r, code 4H+r+8); even r: bits to mantissa
@@ -200,6 +191,65 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a0, uint32_t a1, uint32
     o[1] = __builtin_amdgcn_perm(t23_lo, t01_lo, 0x07060302u);
     o[2] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x05040100u);
     o[3] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);
+}
+
+// fp16 value of one page of a (page & ~1, page | 1) pair word, as float.
+template <bool Odd>
+__device__ __forceinline__ float pair_half(uint32_t w) {
+    return f16_to_f32(static_cast<uint16_t>(Odd ? (w >> 16) : (w & 0xffffu)));
+}
+
+// Qs rows of block ``gb`` for head ``n`` -- hi in row n, lo (the fp16 residual) in row n + 8 --
+// and the block's share of the bias sum_slot q * (min - beta * scale).  Padding slots have
+// q == 0; their scale/min words hold a real slot's (finite) values.
+template <bool Odd>
+__device__ __forceinline__ float qs_block(const float* qperm, const uint32_t* ksr, half8* qs, const MfmaLayout& y,
+                                          int gb, int n) {
+    const float* qrow = qperm + (gb * 8 + n) * 8;
+    const float4 q0 = *reinterpret_cast<const float4*>(qrow);
+    const float4 q1 = *reinterpret_cast<const float4*>(qrow + 4);
+    const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    half8 hi, lo;
+    float bsum = 0.f;
+    if (gb < y.nb_int) {
+        const uint4 s0 = *reinterpret_cast<const uint4*>(ksr + gb * 8);
+        const uint4 s1 = *reinterpret_cast<const uint4*>(ksr + gb * 8 + 4);
+        const uint4 m0 = *reinterpret_cast<const uint4*>(ksr + y.n_kslots / 2 + gb * 8);
+        const uint4 m1 = *reinterpret_cast<const uint4*>(ksr + y.n_kslots / 2 + gb * 8 + 4);
+        const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+        const int tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
+        const float beta_lo = tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f;  // positions with (pos & 2) == 0
+        const float beta_hi = tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float sc = pair_half<Odd>(sw[k]), mn = pair_half<Odd>(mw[k]);
+            const _Float16 h = static_cast<_Float16>(qv[k] * sc);
+            hi[k] = h;
+            lo[k] = static_cast<_Float16>(fmaf(qv[k], sc, -static_cast<float>(h)));
+            bsum = fmaf(qv[k], fmaf(-((k & 2) ? beta_hi : beta_lo), sc, mn), bsum);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const _Float16 h = static_cast<_Float16>(qv[k]);
+            hi[k] = h;
+            lo[k] = static_cast<_Float16>(qv[k] - static_cast<float>(h));
+        }
+    }
+    qs[gb * 16 + n] = hi;
+    qs[gb * 16 + 8 + n] = lo;
+    return bsum;
+}
+
+// Sum of x over each half wave, left in lanes 31 and 63 (DPP row shifts, then row_bcast:15).
+__device__ __forceinline__ float half_wave_sum(float x) {
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x111, 0xf, 0xf, true));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x112, 0xf, 0xf, true));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x114, 0xf, 0xf, true));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x118, 0xf, 0xf, true));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xa, 0xf, false));
+    return x;
 }
 
 // Per-lane DMA sources of the next page to fetch; dma_page advances them one page.
@@ -381,10 +431,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             }
             qperm[e] = v;
         }
-        // Qs rows of heads >= g are never rewritten: zero them once; fp16-tier padding columns too.
+        // Qs rows of heads >= g are never rewritten: zero them once.
         for (int e = tid; e < y.nb * 16; e += kThreads)
             if ((e & 7) >= g) qs[e] = half8{};
-        for (int e = tid; e < kPage * y.w16p / 2; e += kThreads) reinterpret_cast<uint32_t*>(ck + y.ck_v16)[e] = 0u;
         __syncthreads();  // qlin (raw buffer 0) is dead from here on
 
         DmaSrc ds;
@@ -415,69 +464,41 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = o[k];
             }
             if (tid < kPage) {
+                // Value scale and the per-token constant vmin - 4 * vscale (4: the offset of
+                // the Value-code unpack below)
                 const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + 16 * y.seg_end[3]);
                 const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + 16 * y.seg_end[4]);
                 const float s = f16_to_f32(vs[tid]);
                 reinterpret_cast<float*>(ck + y.ck_vsc)[tid] = s;
-                reinterpret_cast<float*>(ck + y.ck_vmid)[tid] = fmaf(1.5f, s, f16_to_f32(vm[tid]));
-            }
-            if (w16 > 0) {
-                const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw + 16 * y.seg_end[2]);
-                uint16_t* dst = reinterpret_cast<uint16_t*>(ck + y.ck_v16);
-                for (int e = tid; e < kPage * w16; e += kThreads) {
-                    const int tok = w16 == 1 ? e : static_cast<int>(__umulhi(static_cast<uint32_t>(e), y.w16_magic));
-                    dst[tok * y.w16p + (e - tok * w16)] = f16[e];
-                }
-            }
-            const int par = 16 * (page & 1);
-            const uint32_t* ksr = reinterpret_cast<const uint32_t*>(raw + y.raw_ks);
-            for (int e = tid; e < y.nb * 16; e += kThreads) {
-                const int gb = e >> 4, row = e & 15, n = row & 7;
-                if (n >= g) continue;
-                const float* qrow = qperm + (gb * 8 + n) * 8;
-                const float4 q0 = *reinterpret_cast<const float4*>(qrow);
-                const float4 q1 = *reinterpret_cast<const float4*>(qrow + 4);
-                float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-                if (gb < y.nb_int) {
-                    const uint4 s0 = *reinterpret_cast<const uint4*>(ksr + gb * 8);
-                    const uint4 s1 = *reinterpret_cast<const uint4*>(ksr + gb * 8 + 4);
-                    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+                reinterpret_cast<float*>(ck + y.ck_vmid)[tid] = fmaf(-4.f, s, f16_to_f32(vm[tid]));
+                // fp16-tier row of token tid, zero padded to w16p columns
+                const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw + 16 * y.seg_end[2]) + tid * w16;
+                uint4* dst = reinterpret_cast<uint4*>(ck + y.ck_v16 + 2 * tid * y.w16p);
+                for (int c0 = 0; c0 < w16; c0 += 8) {
+                    uint32_t v[8];
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const float sc = f16_to_f32(static_cast<uint16_t>(sw[k] >> par));
-                        qv[k] = qv[k] != 0.f ? qv[k] * sc : 0.f;  // padding slots stay exactly 0
-                    }
+                    for (int k = 0; k < 8; ++k) v[k] = c0 + k < w16 ? f16[c0 + k] : 0u;
+                    dst[c0 >> 3] = uint4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
                 }
-                half8 hv;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const _Float16 hi = static_cast<_Float16>(qv[k]);
-                    hv[k] = row < 8 ? hi : static_cast<_Float16>(qv[k] - static_cast<float>(hi));
-                }
-                qs[e] = hv;
             }
+            // Qs and the bias: thread (head tid / 32, blocks tid % 32 + 32 i); each head's bias
+            // is summed over its half wave
             {
-                // bias[n] = sum over integer-tier slots of q * (min - beta * scale)
-                const int n = tid & 7, part = tid >> 3;  // 32 parts
-                float acc = 0.f;
-                for (int gb = part; gb < y.nb_int; gb += 32) {
-                    const int tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
-                    const float* qrow = qperm + (gb * 8 + n) * 8;
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const float sc = f16_to_f32(static_cast<uint16_t>(ksr[gb * 8 + k] >> par));
-                        const float mn = f16_to_f32(static_cast<uint16_t>(ksr[y.n_kslots / 2 + gb * 8 + k] >> par));
-                        const float term = qrow[k] * fmaf(-slot_beta(tier, k), sc, mn);
-                        acc += qrow[k] != 0.f ? term : 0.f;
+                const uint32_t* ksr = reinterpret_cast<const uint32_t*>(raw + y.raw_ks);
+                const int n = tid >> 5;
+                float bsum = 0.f;
+                if (n < g) {
+                    if (page & 1) {
+                        for (int gb = tid & 31; gb < y.nb; gb += 32) bsum += qs_block<true>(qperm, ksr, qs, y, gb, n);
+                    } else {
+                        for (int gb = tid & 31; gb < y.nb; gb += 32) bsum += qs_block<false>(qperm, ksr, qs, y, gb, n);
                     }
                 }
-                acc += __shfl_xor(acc, 8, kWave);
-                acc += __shfl_xor(acc, 16, kWave);
-                acc += __shfl_xor(acc, 32, kWave);
-                if (lane < 8) bpart[wave * 8 + lane] = acc;
+                bsum = half_wave_sum(bsum);
+                if ((lane & 31) == 31) bpart[n] = bsum;
             }
             lds_barrier();
-            const float bias = (n16 < 8) ? bpart[n16] + bpart[8 + n16] + bpart[16 + n16] + bpart[24 + n16] : 0.f;
+            const float bias = (n16 < 8) ? bpart[n16] : 0.f;
 
             // ---- scores of this wave's 32 tokens ----
             // Integer tiers read up to 7 dwords past their segment (still inside the raw
@@ -523,15 +544,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ub), bq, acc1, 0, 0, 0);
                 }
             }
-            // hi + lo columns (row_shl:8, zero outside the row), + bias.  The accumulator
-            // elements are copied to scalars before the DPP move: applied to vector elements
-            // directly, this compiler emits one move for all of them.
+            // hi + lo columns (row_shl:8, zero outside the row).  The accumulator elements are
+            // copied to scalars before the DPP move: applied to vector elements directly, this
+            // compiler emits one move for all of them.  The page's bias enters through the max.
             float sv[8];
             const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 const int xi = __builtin_bit_cast(int, accs[r]);
-                sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true)) + bias;
+                sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
             }
             // ---- online softmax (log2 domain) ----
             float mx = sv[0];
@@ -539,8 +560,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
             mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
             mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-            const float m_new = fmaxf(m_run, mx);
+            const float m_new = fmaxf(m_run, mx + bias);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            const float m_off = m_new - bias;  // p = 2^(sv + bias - m_new)
             m_run = m_new;
             const float* vsc = reinterpret_cast<const float*>(ck + y.ck_vsc);
             const float* vmd = reinterpret_cast<const float*>(ck + y.ck_vmid);
@@ -554,7 +576,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             float psum = 0.f, pmid = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float pi = __builtin_amdgcn_exp2f(sv[i] - m_new);
+                const float pi = __builtin_amdgcn_exp2f(sv[i] - m_off);
                 psum += pi;
                 pmid = fmaf(pi, vd[i], pmid);
                 pp[i] = pi * vs[i];
@@ -581,11 +603,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             au.z = __builtin_amdgcn_update_dpp(ahi[2], alo[2], 0x118, 0xf, 0xc, false);
             au.w = __builtin_amdgcn_update_dpp(ahi[3], alo[3], 0x118, 0xf, 0xc, false);
             const half8 ap = __builtin_bit_cast(half8, au);
-            // alpha of the 4 output rows this lane holds (rows 4*kb + r, head (4*kb + r) % 8);
-            // a same-wave LDS write then read is ordered by the LDS queue
-            if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = alpha;
-            __builtin_amdgcn_wave_barrier();
-            const float4 arow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * (kb & 1));
+            // Rescale O when some head's max moved: alpha of the 4 output rows this lane holds
+            // (rows 4*kb + r, head (4*kb + r) % 8); a same-wave LDS write then read is ordered
+            // by the LDS queue.
+            if (__builtin_amdgcn_ballot_w64(n16 < 8 && alpha != 1.f)) {
+                if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = alpha;
+                __builtin_amdgcn_wave_barrier();
+                const float4 arow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * (kb & 1));
+#pragma unroll
+                for (int nt = 0; nt < 8; ++nt) {
+                    O[nt][0] *= arow.x;
+                    O[nt][1] *= arow.y;
+                    O[nt][2] *= arow.z;
+                    O[nt][3] *= arow.w;
+                }
+            }
             // ---- value product ----
             const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + y.ck_vt);
             const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
@@ -596,15 +628,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             const uint32_t dhi[8] = {d1a.x, d1a.y, d1a.z, d1a.w, d1b.x, d1b.y, d1b.z, d1b.w};
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
-                // tokens (0, 2): code bits to mantissa 6..7 (16 + c), minus 17.5;
-                // tokens (1, 3): bits 8..9 (4 + c), minus 5.5  ->  c - 1.5
+                // code bits to mantissa 8..9 under exponent 4: value 4 + c (the offset is folded
+                // into the per-token constant); tokens (0, 2) sit at byte bits sh, (1, 3) at 8 + sh
                 uint4 bu;
-                bu.x = pk_add_h(and_or(dlo[nt] << (6 - sh), 0x00C000C0u, 0x4C004C00u), 0xCC60CC60u);
-                bu.y = pk_add_h(and_or(dlo[nt] >> sh, 0x03000300u, 0x44004400u), 0xC580C580u);
-                bu.z = pk_add_h(and_or(dhi[nt] << (6 - sh), 0x00C000C0u, 0x4C004C00u), 0xCC60CC60u);
-                bu.w = pk_add_h(and_or(dhi[nt] >> sh, 0x03000300u, 0x44004400u), 0xC580C580u);
+                bu.x = and_or(dlo[nt] << (8 - sh), 0x03000300u, 0x44004400u);
+                bu.y = and_or(dlo[nt] >> sh, 0x03000300u, 0x44004400u);
+                bu.z = and_or(dhi[nt] << (8 - sh), 0x03000300u, 0x44004400u);
+                bu.w = and_or(dhi[nt] >> sh, 0x03000300u, 0x44004400u);
                 const half8 bv = __builtin_bit_cast(half8, bu);
-                float4v o4 = {O[nt][0] * arow.x, O[nt][1] * arow.y, O[nt][2] * arow.z, O[nt][3] * arow.w};
+                float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
                 o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, bv, o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }

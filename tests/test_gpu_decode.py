@@ -67,9 +67,10 @@ def test_split_count_invariance(gpu, kernel):
     mgr, lens = build(d, [20, 13], [9, 77], 14, 2, 128, gpu)
     outs = [run(mgr, d, gpu, 0.09, KERNELS[kernel], pages_per_split=s, out_dtype=torch.float32)
             for s in (1, 3, 64)]
-    # the VALU path is fp32 throughout; the MFMA path rounds hi/lo fp16 operands (~22 bits),
-    # so its result moves by ~1e-6 relative with the split pattern (a merge error is >> 1e-3)
-    rel_bar = 2e-6 if kernel == "valu" else 2e-5
+    # the VALU path is fp32 throughout; the MFMA path rounds hi/lo fp16 operands (~22 bits) and
+    # accumulates Value codes as 4 + c (the offset cancels against the per-token constant), so
+    # its result moves by a few 1e-5 relative with the split pattern (a merge error is >> 1e-3)
+    rel_bar = 2e-6 if kernel == "valu" else 1e-4
     for o in outs[1:]:
         rel = float((o - outs[0]).norm() / outs[0].norm())
         assert rel <= rel_bar, f"split-count change moved the output by {rel:.3g} (bar {rel_bar})"
