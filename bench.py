@@ -40,7 +40,43 @@ def parse_args():
     p.add_argument("--pages-per-split", type=int, default=None)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                   help="only run a plain device-to-device copy of BYTES (3 times) and exit: the reference "
+                        "kernel that scales the PMC byte counters (FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
+
+
+PMC_SUMMARY = ROOT / "profiles" / "decode_mfma_c2_pmc.txt"
+
+
+def measured_traffic(config: str):
+    """HBM bytes per decode-kernel dispatch from the committed PMC summary (FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by the same counter's reading for a copy of known
+    size), or None when there is no summary for this workload."""
+    if config != "c2" or not PMC_SUMMARY.exists():
+        return None
+    vals = {}
+    for line in PMC_SUMMARY.read_text().splitlines():
+        if ":" in line and not line.lstrip().startswith("#"):
+            k, v = line.split(":", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        return int(float(vals["traffic_bytes_per_dispatch"]))
+    except (KeyError, ValueError):
+        return None
+
+
+def copy_calibration(nbytes: int) -> None:
+    import torch
+
+    n = nbytes // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n * 4, "launches": 3}), flush=True)
 
 
 def algorithmic_bytes(widths, words, n_kv, n_q, D, H, R1, k_group=128, v_group=128):
@@ -156,6 +192,9 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of this "
               "path is a design note, not a built component", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     import torch
 
     from logitfill_amd import _native, synth
@@ -205,7 +244,8 @@ def main():
         "bytes_per_layer_step": int(bytes_launch),
         "wall_ms_per_step": round(wall_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(args.config) if args.layers in (None, cfg["layers"]) else None},
     }
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 1
+#define LF_ABI_VERSION 2
 
 /* Element types of query / residual / output tensors. */
 enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
@@ -128,19 +128,14 @@ typedef struct lf_decode_args {
     float scaling;                            /* softmax scale (reference: attn.scaling) */
     const int32_t* work;  int32_t n_work;     /* device, from lf_plan_decode            */
     const int32_t* seq_work;                  /* device, from lf_plan_decode            */
-    void* workspace; int64_t workspace_bytes; /* >= lf_decode_workspace_bytes(); its
-                                                 counter area must be zero before the
-                                                 first call (calls leave it zero)       */
+    void* workspace; int64_t workspace_bytes; /* >= lf_decode_workspace_bytes(); needs
+                                                 no initialisation                      */
     int32_t kernel;                           /* 0 auto, 1 VALU, 2 MFMA                 */
 } lf_decode_args;
 
-/* Workspace bytes for lf_decode_attention with ``n_work`` items. */
-int64_t lf_decode_workspace_bytes(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim,
-                                  int32_t n_work);
-/* Byte offset, inside the workspace, of the int32 counters [batch][n_kv] that must
- * start zeroed (always 0: the counters come first, the partials follow). */
-int64_t lf_decode_counter_offset(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim,
-                                 int32_t n_work);
+/* Workspace bytes for lf_decode_attention with ``n_work`` items: the fp32
+ * partials [n_work][n_q][head_dim + 2] of the split-K items. */
+int64_t lf_decode_workspace_bytes(int32_t n_q, int32_t head_dim, int32_t n_work);
 
 /*
  * Decode attention for one new query token per sequence.  Replaces
@@ -150,8 +145,8 @@ int64_t lf_decode_counter_offset(int32_t batch, int32_t n_kv, int32_t n_q, int32
  *   out[b, i] = softmax(scaling * q[b,i] . K_b^T) V_b,
  *   K_b = [dequant(history_b) ; tail_k[b, :, :tail_len[b]] ; k_new[b]]  (V likewise),
  *
- * with q head i reading kv head i / (n_q / n_kv).  Split-K over packed pages
- * plus a fused cross-split softmax merge; accumulation in fp32; output
+ * with q head i reading kv head i / (n_q / n_kv).  Split-K over packed pages,
+ * then a second kernel merges the splits' softmax partials; accumulation in fp32; output
  * rounded to ``out_dtype``.  Requires bit_v == 2 (as the reference kernel,
  * reference.py:62) and n_q % n_kv == 0.
  */

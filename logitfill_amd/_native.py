@@ -86,8 +86,7 @@ _SIGNATURES = {
     "lf_pack_pages": (c_int32, [POINTER(PackedLayer), c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64,
                                 c_void_p, c_int32, c_void_p]),
     "lf_plan_decode": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
-    "lf_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
-    "lf_decode_counter_offset": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "lf_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "lf_decode_attention": (c_int32, [POINTER(PackedLayer), POINTER(DecodeArgs), c_void_p]),
     "lf_dequantize": (c_int32, [POINTER(PackedLayer), c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "lf_dense_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
@@ -96,7 +95,7 @@ _SIGNATURES = {
                                   c_void_p]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 _LIB = None
 
 

@@ -127,17 +127,9 @@ int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_p
     return n;
 }
 
-int64_t lf_decode_workspace_bytes(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim, int32_t n_work) {
-    return lf::decode_workspace_total(batch, n_kv, n_q, head_dim, n_work);
-}
-
-int64_t lf_decode_counter_offset(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim, int32_t n_work) {
-    (void)batch;
-    (void)n_kv;
-    (void)n_q;
-    (void)head_dim;
-    (void)n_work;
-    return 0;
+int64_t lf_decode_workspace_bytes(int32_t n_q, int32_t head_dim, int32_t n_work) {
+    if (n_q <= 0 || head_dim <= 0 || n_work < 0) return LF_E_SHAPE;
+    return lf::decode_workspace_total(n_q, head_dim, n_work);
 }
 
 int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* args, void* stream) {
@@ -158,7 +150,7 @@ int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* 
     if (layer->v_groups > 8) return LF_E_UNSUPPORTED;
     if (A.tail_cap < 0 || (A.tail_cap > 0 && (!A.tail_k || !A.tail_v))) return LF_E_NULL;
     if (A.n_work <= 0) return LF_E_SHAPE;
-    if (A.workspace_bytes < lf_decode_workspace_bytes(layer->batch, layer->n_kv, A.n_q, D, A.n_work))
+    if (A.workspace_bytes < lf_decode_workspace_bytes(A.n_q, D, A.n_work))
         return LF_E_WORKSPACE;
     if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
 
@@ -167,9 +159,7 @@ int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* 
     p.A = A;
     p.g = g;
     p.qscale = A.scaling * lf::kLog2e;
-    p.counters = static_cast<int*>(A.workspace);
-    p.part = reinterpret_cast<float*>(static_cast<char*>(A.workspace) +
-                                      lf::decode_part_offset_bytes(layer->batch, layer->n_kv));
+    p.part = static_cast<float*>(A.workspace);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (A.kernel != 1) {
         bool handled = false;

@@ -762,14 +762,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     }
 }
 
-// One workgroup per (sequence, kv head): merge the sequence's partials into the output.
-__global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p, int lds_floats) {
-    extern __shared__ float wsc[];
-    const int b = blockIdx.x / p.L.n_kv;
-    const int h = blockIdx.x % p.L.n_kv;
-    merge_partials(p, b, h, wsc, lds_floats);
-}
-
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
@@ -873,15 +865,9 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
         lds_limit = mp.y.lds_bytes;
     }
     hipLaunchKernelGGL(decode_mfma_kernel, dim3(p.A.n_work, p.L.n_kv), dim3(kThreads), mp.y.lds_bytes, stream, mp);
-    hipError_t err = hipGetLastError();
+    const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);
-    // A sequence has at most n_work - batch + 1 items; weights for 2 * items * g floats when they fit.
-    const int64_t want = 2ll * (p.A.n_work - p.L.batch + 1) * p.g;
-    const int lds_floats = static_cast<int>(want < 8192 ? want : 8192);
-    hipLaunchKernelGGL(decode_reduce_kernel, dim3(p.L.batch * p.L.n_kv), dim3(256), lds_floats * sizeof(float), stream,
-                       p, lds_floats);
-    err = hipGetLastError();
-    return err == hipSuccess ? LF_OK : static_cast<int>(err);
+    return launch_decode_reduce(p, stream);
 }
 
 }  // namespace lf

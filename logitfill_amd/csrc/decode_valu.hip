@@ -5,7 +5,7 @@
 // dense semantics of src/logitfill/packed/reference.py:30-56.  Differences in
 // structure: one wave serves all g query heads of a kv head so the packed
 // bytes are read once per kv head (the reference re-reads them per query head);
-// the history is split across workgroups (split-K) and merged by the last one.
+// the history is split across workgroups (split-K) and merged by decode_reduce_kernel.
 //
 // Per 64-token chunk a lane owns one token for the scores and one or more
 // channels for the value accumulation.  The Key scale is folded into the
@@ -27,7 +27,6 @@ struct ValuSmem {
     float vsc[64][8];            // V scale per token and channel group
     float vmn[64][8];            // V min
     uint32_t vcode[64][D / 16];  // V codes of the chunk
-    int flag;
 };
 
 __device__ __forceinline__ int slot_tier(const int* off, int slot) {
@@ -262,10 +261,6 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
             r[D + 1] = lt;
         }
     }
-    if (last_split_arrives(p, b, h, &sm.flag)) {
-        const int n_slots = off[3] + L.k_width[3];
-        merge_partials(p, b, h, qp, n_slots * kMaxG);
-    }
 }
 
 }  // namespace
@@ -280,7 +275,8 @@ int launch_decode_valu(const DecodeParams& p, hipStream_t stream) {
     else if (D == 256) hipLaunchKernelGGL(decode_valu_kernel<256>, grid, block, dyn, stream, p);
     else return LF_E_SHAPE;
     const hipError_t err = hipGetLastError();
-    return err == hipSuccess ? LF_OK : static_cast<int>(err);
+    if (err != hipSuccess) return static_cast<int>(err);
+    return launch_decode_reduce(p, stream);
 }
 
 }  // namespace lf

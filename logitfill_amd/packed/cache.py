@@ -419,9 +419,9 @@ class PackedKVManager:
             self.seq_len = self.layers[layer_idx].length
 
     def workspace(self, nbytes: int) -> torch.Tensor:
-        """Shared decode workspace (grown on demand; the counter area starts zeroed)."""
+        """Shared decode workspace: split-K partials (grown on demand, needs no clearing)."""
         if self._workspace is None or self._workspace.numel() < nbytes:
-            self._workspace = torch.zeros(int(nbytes), dtype=torch.uint8, device=self.device)
+            self._workspace = torch.empty(int(nbytes), dtype=torch.uint8, device=self.device)
         return self._workspace
 
 

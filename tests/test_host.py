@@ -62,7 +62,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
         assert name in _native._SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.lf_abi_version() == 1
+    assert lib.lf_abi_version() == 2
     assert b"gfx950" in lib.lf_build_info()
 
 
@@ -106,10 +106,11 @@ def test_plan_decode_known_answer():
 
 
 def test_workspace_layout():
+    """Workspace = fp32 partials (o[D], m, l) per item and q head; bad shapes are rejected."""
     lib = _native.load()
-    assert lib.lf_decode_counter_offset(16, 4, 28, 128, 100) == 0
-    assert lib.lf_decode_workspace_bytes(16, 4, 28, 128, 100) == 256 + 100 * 28 * 130 * 4
-    assert lib.lf_decode_workspace_bytes(100, 4, 28, 128, 1) == 1792 + 28 * 130 * 4
+    assert lib.lf_decode_workspace_bytes(28, 128, 100) == 100 * 28 * 130 * 4
+    assert lib.lf_decode_workspace_bytes(28, 128, 1) == 28 * 130 * 4
+    assert lib.lf_decode_workspace_bytes(0, 128, 1) == -2
 
 
 def test_argument_validation_rejects_before_launch():
