@@ -103,14 +103,14 @@ int32_t lf_pack_pages(const lf_packed_layer* layer,
                       const int32_t* jobs, int32_t n_jobs, void* stream);
 
 /*
- * Decode work plan (host function, no device access).  Splits each
- * sequence's ``hist_pages[b]`` packed pages into items of at most
- * ``pages_per_split`` pages, plus one residual item per sequence (tail page
- * + new token).  Writes ``work_out`` [n][4] = (b, page_begin, page_end, kind)
- * (kind 0 = packed pages, 1 = residual) and ``seq_work_out`` [batch][2] =
- * (first item, item count).  Returns the item count n, or a negative
- * LF_E_* when ``work_cap`` is too small.  Both arrays must be copied to the
- * device before lf_decode_attention.
+ * Decode work plan (host function, no device access).  Items 0..batch-1 are
+ * the residual items (b, 0, 0, 1) of sequence b (tail page + new token); then
+ * each sequence's ``hist_pages[b]`` packed pages follow as items of at most
+ * ``pages_per_split`` pages (b, page_begin, page_end, 0).  Writes
+ * ``work_out`` [n][4] and ``seq_work_out`` [batch][2] = (first page item,
+ * page item count) of each sequence.  Returns the item count n, or a
+ * negative LF_E_* when ``work_cap`` is too small.  Both arrays must be copied
+ * to the device before lf_decode_attention.
  */
 int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split,
                        int32_t* work_out, int32_t work_cap, int32_t* seq_work_out);

@@ -101,10 +101,19 @@ int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_p
                        int32_t* work_out, int32_t work_cap, int32_t* seq_work_out) {
     if (!hist_pages || !work_out || !seq_work_out) return LF_E_NULL;
     if (batch <= 0 || pages_per_split <= 0) return LF_E_SHAPE;
-    int32_t n = 0;
+    if (work_cap < batch) return LF_E_WORKSPACE;
+    // Residual items first (one per sequence): they are short but latency-bound, so they are
+    // dispatched before the page items rather than at the tail of the grid.
+    for (int32_t b = 0; b < batch; ++b) {
+        if (hist_pages[b] < 0) return LF_E_SHAPE;
+        work_out[4 * b + 0] = b;
+        work_out[4 * b + 1] = 0;
+        work_out[4 * b + 2] = 0;
+        work_out[4 * b + 3] = 1;
+    }
+    int32_t n = batch;
     for (int32_t b = 0; b < batch; ++b) {
         const int32_t pages = hist_pages[b];
-        if (pages < 0) return LF_E_SHAPE;
         const int32_t first = n;
         for (int32_t p0 = 0; p0 < pages; p0 += pages_per_split) {
             if (n >= work_cap) return LF_E_WORKSPACE;
@@ -115,12 +124,6 @@ int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_p
             work_out[4 * n + 3] = 0;
             ++n;
         }
-        if (n >= work_cap) return LF_E_WORKSPACE;
-        work_out[4 * n + 0] = b;
-        work_out[4 * n + 1] = 0;
-        work_out[4 * n + 2] = 0;
-        work_out[4 * n + 3] = 1;
-        ++n;
         seq_work_out[2 * b + 0] = first;
         seq_work_out[2 * b + 1] = n - first;
     }

@@ -6,8 +6,8 @@
 // page = Key group = 128 tokens, one Value group per token (v_group 128), int2
 // Values, 1 <= g = n_q/n_kv <= 8.  Anything else runs the VALU kernel.
 //
-// Work: one workgroup of 8 waves per (split item, kv head); wave w computes
-// tokens 16w..16w+15 of every page of the item.  Pages arrive by LDS-DMA
+// Work: one workgroup of 4 waves per (split item, kv head); wave w computes
+// tokens 32w..32w+31 (two 16-token tiles) of every page of the item.  Pages arrive by LDS-DMA
 // (global_load_lds) two pages ahead of the page being computed: Key codes into
 // a ring of three LDS buffers, everything else into a ring of two.  Each page
 // is "prepared" (the per-page operands below) into one of two prepared buffers
@@ -28,14 +28,13 @@
 // recombines them.
 //
 // Values.  The S^T accumulator layout (lane: head n = lane%16, tokens 4*kb+r
-// of the wave's 16-token tile, kb = lane/16) is the A-operand layout of
-// O = P' . (4 + code_V) (the K dimension's upper half is zero), so
-// probabilities feed the second MFMA in place (4 + c from the same
-// exponent-field unpack).  P' = p * vscale is split hi/lo across rows 0..7 /
-// 8..15; the constant vmin - 4 * vscale enters through sum_t p_t * mid_t.
-// Value codes are regrouped per page (one dword = one byte column of 4
-// consecutive tokens) so each lane's codes for one 16-channel tile are one
-// LDS dword.
+// of each of the wave's two 16-token tiles, kb = lane/16) is the A-operand
+// layout of O = P' . (4 + code_V) with k = those 8 tokens, so probabilities
+// feed the second MFMA in place (4 + c from the same exponent-field unpack).
+// P' = p * vscale is split hi/lo across rows 0..7 / 8..15; the constant
+// vmin - 4 * vscale enters through sum_t p_t * mid_t.  Value codes are
+// regrouped per page (one dword = one byte column of 4 consecutive tokens) so
+// each lane's 8 codes for one 16-channel tile are two LDS dwords.
 #include "decode_common.hpp"
 
 namespace lf {
@@ -47,13 +46,16 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kD = 128;
 constexpr int kPage = 128;
-constexpr int kMaxDma = 4;    // 16-byte DMA instructions per wave per page (<= 2048 chunks)
-constexpr int kMaxKsDma = 2;  // 4-byte Key scale/min DMA instructions per wave per page
-constexpr int kVcDma = 2;     // 4-byte Value-code DMA instructions per wave per page (1024 dwords)
+constexpr int kMaxDma = 8;    // 16-byte DMA instructions per wave per page (<= 2048 chunks)
+constexpr int kMaxKsDma = 4;  // 4-byte Key scale/min DMA instructions per wave per page
+constexpr int kRawbVs = 0;    // rest buffer: Value scale [128] fp16
+constexpr int kRawbVm = 256;  //              Value min [128] fp16
+constexpr int kRawbVc = 512;  //              Value codes [128][8] u32
+constexpr int kRawbF16 = 4608;  //            fp16-tier rows [128][width16]
 
 struct MfmaLayout {
     int kst[4];          // K-steps per tier (int2: even; K-step s takes half s&1 of 4 words)
@@ -61,15 +63,13 @@ struct MfmaLayout {
     int nb;              // padded blocks (4 per K-step)
     int nb_int;          // padded blocks of the integer tiers
     int w16p;            // fp16-tier row stride in the prepared buffer (multiple of 8)
-    int seg_end[6];      // cumulative 16-byte chunks of a page: K0, K1, K2, fp16 tier, v scale, v min
-    int n_chunks;        // = seg_end[5]
+    int seg_end[3];      // cumulative 16-byte chunks of the Key-code rows K0, K1, K2 (region A)
+    int n_chunks;        // region A + region B chunks
     int ja, jb;          // 64-chunk DMA blocks of the Key codes (chunks [0, seg_end[2])) and of the rest
     int n_kslots;        // 2 * nb_int * 8: Key scale slots, then Key min slots
     int rawa_bytes;      // Key-code buffer: K0, K1, K2 rows of the page
-    int rawb_vs;         // rest buffer: fp16 tier rows at 0, then v scale, v min
-    int rawb_vm;
-    int rawb_vc;         // rest buffer: [32 groups][8 words][4 tokens] u32 Value codes
-    int rawb_ks;         // rest buffer: [n_kslots] u32 fp16 pairs (page & ~1, page | 1) of Key scale / min
+    int rawb_ks;         // rest buffer (v scale at 0, v min at 256, [128][8] u32 Value codes at 512,
+                         // fp16-tier rows at 4608): [n_kslots] u32 Key scale / min page pairs
     int rawb_bytes;
     int ck_qs;           // prepared: [nb][16][8] fp16 Qs hi (rows 0..7) / lo (rows 8..15)
     int ck_vt;           // prepared: [32 groups][36] u32 byte columns (4 per 8-word row) + 4 pad
@@ -80,7 +80,7 @@ struct MfmaLayout {
     int ck_bytes;
     int off_qperm;       // [nb][8 heads][8] fp32: q * scaling*log2e per slot (0 for padding)
     int off_tt;          // int16 tier table of this kv head (ranks -> channel ids), tiers back to back
-    int off_small;       // alpha [8 waves][8], wave m/l/mid [8 waves][3][8]
+    int off_small;       // alpha [waves][8], wave m/l/mid [waves][3][8]
     int off_ck;          // two prepared buffers
     int off_rawa;        // three Key-code buffers
     int off_rawb;        // two rest buffers (prepared + Key-code + rest buffers form one alias region)
@@ -121,24 +121,35 @@ __device__ __forceinline__ T sel3(const T (&a)[3], int t) {
 __device__ __forceinline__ uint32_t lds_addr(unsigned char* p) {
     return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)p)));
 }
-__device__ __forceinline__ void dma16(const unsigned char* g, unsigned char* lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+__device__ __forceinline__ void dma16(const unsigned char* g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
-__device__ __forceinline__ void dma4(const unsigned char* g, unsigned char* lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+__device__ __forceinline__ void dma4(const unsigned char* g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
 
-// Bit patterns of the exponent-field code unpack.  They reach the kernel as arguments so the
-// compiler keeps (x & mask) | (bits & ~mask) as one v_bfi_b32 instead of folding the
-// constants into an AND + OR pair.  (The unpack must be compiler-visible code: results feed
-// MFMA operands, and only the compiler tracks the MFMA read hazards on those registers.)
+// Bit patterns of the exponent-field code unpack, held in VGPRs: with register operands the
+// compiler selects (x & mask) | bits as one v_and_or_b32 (VOP3 takes no literal), and the
+// unpack stays compiler-visible code, so the compiler also inserts the wait states an MFMA
+// needs after a VALU write of its operands.  ``as_vgpr`` hides the constant from folding.
 struct UnpackBits {
     uint32_t m2lo, m2hi;    // int2 code at mantissa bits 6..7 / 8..9 (both halves)
     uint32_t m4lo, m4hi;    // int4 code at mantissa bits 2..5 / 6..9
     uint32_t e16, e4, e256; // fp16 exponent fields of 16, 4, 256 (both halves)
 };
 
-__device__ __forceinline__ uint32_t bfi(uint32_t x, uint32_t mask, uint32_t bits) { return (x & mask) | (bits & ~mask); }
+__device__ __forceinline__ uint32_t as_vgpr(uint32_t s) {
+    uint32_t v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
+    return v;
+}
+
+__device__ __forceinline__ UnpackBits vgpr_bits(const UnpackBits& k) {
+    return UnpackBits{as_vgpr(k.m2lo), as_vgpr(k.m2hi), as_vgpr(k.m4lo), as_vgpr(k.m4hi),
+                      as_vgpr(k.e16),  as_vgpr(k.e4),   as_vgpr(k.e256)};
+}
+
+__device__ __forceinline__ uint32_t bfi(uint32_t x, uint32_t mask, uint32_t bits) { return (x & mask) | bits; }
 
 struct MfmaParams {
     DecodeParams p;
@@ -210,26 +221,30 @@ __device__ __forceinline__ float pair_half(uint32_t w) {
     return f16_to_f32(static_cast<uint16_t>(Odd ? (w >> 16) : (w & 0xffffu)));
 }
 
-// Qs of slots 4*half..4*half+3 of block ``gb`` for head ``n`` -- hi into row n, lo (the fp16
-// residual) into row n + 8 -- and their share of the bias sum_slot q * (min - beta * scale).
-// Padding slots have q == 0; their scale/min words hold a real slot's (finite) values.
+// Qs of block ``gb`` for head ``n`` -- hi into row n, lo (the fp16 residual) into row n + 8 --
+// and the block's share of the bias sum_slot q * (min - beta * scale).  Padding slots have
+// q == 0; their scale/min words hold a real slot's (finite) values.
 template <bool Odd>
-__device__ __forceinline__ float qs_quad(const float* qperm, const uint32_t* ksr, unsigned char* qs,
-                                         const MfmaLayout& y, int gb, int n, int half) {
-    const float4 q4 = *reinterpret_cast<const float4*>(qperm + (gb * 8 + n) * 8 + 4 * half);
-    const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
-    half4 hi, lo;
+__device__ __forceinline__ float qs_block(const float* qperm, const uint32_t* ksr, half8* qs, const MfmaLayout& y,
+                                          int gb, int n) {
+    const float* qrow = qperm + (gb * 8 + n) * 8;
+    const float4 q0 = *reinterpret_cast<const float4*>(qrow);
+    const float4 q1 = *reinterpret_cast<const float4*>(qrow + 4);
+    const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    half8 hi, lo;
     float bsum = 0.f;
     if (gb < y.nb_int) {
-        const uint4 s4 = *reinterpret_cast<const uint4*>(ksr + gb * 8 + 4 * half);
-        const uint4 m4 = *reinterpret_cast<const uint4*>(ksr + y.n_kslots / 2 + gb * 8 + 4 * half);
-        const uint32_t sw[4] = {s4.x, s4.y, s4.z, s4.w};
-        const uint32_t mw[4] = {m4.x, m4.y, m4.z, m4.w};
+        const uint4 s0 = *reinterpret_cast<const uint4*>(ksr + gb * 8);
+        const uint4 s1 = *reinterpret_cast<const uint4*>(ksr + gb * 8 + 4);
+        const uint4 m0 = *reinterpret_cast<const uint4*>(ksr + y.n_kslots / 2 + gb * 8);
+        const uint4 m1 = *reinterpret_cast<const uint4*>(ksr + y.n_kslots / 2 + gb * 8 + 4);
+        const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
         const int tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
         const float beta_lo = tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f;  // positions with (pos & 2) == 0
         const float beta_hi = tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < 8; ++k) {
             const float sc = pair_half<Odd>(sw[k]), mn = pair_half<Odd>(mw[k]);
             const _Float16 hk = static_cast<_Float16>(qv[k] * sc);
             hi[k] = hk;
@@ -238,88 +253,93 @@ __device__ __forceinline__ float qs_quad(const float* qperm, const uint32_t* ksr
         }
     } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < 8; ++k) {
             const _Float16 hk = static_cast<_Float16>(qv[k]);
             hi[k] = hk;
             lo[k] = static_cast<_Float16>(qv[k] - static_cast<float>(hk));
         }
     }
-    *reinterpret_cast<half4*>(qs + 2 * ((gb * 16 + n) * 8 + 4 * half)) = hi;
-    *reinterpret_cast<half4*>(qs + 2 * ((gb * 16 + 8 + n) * 8 + 4 * half)) = lo;
+    qs[gb * 16 + n] = hi;
+    qs[gb * 16 + 8 + n] = lo;
     return bsum;
 }
 
-// Sum of x over the wave, valid in lane 63 (DPP row shifts, row_bcast:15, row_bcast:31).
-__device__ __forceinline__ float wave_sum_to_63(float x) {
+// Sum of x over each half wave, left in lanes 31 and 63 (DPP row shifts, then row_bcast:15).
+__device__ __forceinline__ float half_wave_sum(float x) {
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x111, 0xf, 0xf, true));
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x112, 0xf, 0xf, true));
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x114, 0xf, 0xf, true));
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x118, 0xf, 0xf, true));
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xa, 0xf, false));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143, 0xc, 0xf, false));
     return x;
 }
 
-// Per-lane DMA sources of the next page to fetch; dma_page advances them one page.
+// Per-lane DMA state.  A page is fetched as 16-byte chunks in two regions -- region A: the
+// Key-code rows K0, K1, K2; region B: Value scale, Value min, Value codes, fp16-tier rows --
+// plus one dword per Key scale/min slot (the fp16 pair of pages (p & ~1, p | 1)).  Block j
+// (64 chunks) of region A lands in the Key-code buffer at 1024 j, block j of region B in the
+// rest buffer at 1024 j; slot dwords follow region B at y.rawb_ks.  Wave w issues blocks
+// w, w + 4, ...; lanes past a region's last chunk are masked off.
 struct DmaSrc {
     const unsigned char* chunk[kMaxDma];
     int chunk_stride[kMaxDma];  // bytes per page of the chunk's segment
     int chunk_live;             // bit i: this lane's chunk of instruction i exists
-    const unsigned char* vc[kVcDma];
     const unsigned char* ks[kMaxKsDma];
-    int n_chunk;   // 16-byte DMA instructions this wave issues per page
-    int n_ks;      // 4-byte scale DMA instructions this wave issues per page
-    int per_page;  // DMA instructions this wave issues per page
+    int ks_live;                // bit i: this lane's slot of instruction i exists
+    int n_chunk;                // 16-byte DMA instructions this wave issues per page
+    int n_ks;                   // 4-byte slot DMA instructions this wave issues per page
+    int per_page;               // DMA instructions this wave issues per page
 };
 
 __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout& y, int b, int h, int pbeg,
                           int wave, int lane) {
     const int64_t row0 = tok_row(L, b, h, static_cast<int64_t>(pbeg) * kPage);
+    const int na = y.seg_end[2];             // region A chunks
+    const int nb_chunks = y.n_chunks - na;   // region B chunks
     s.n_chunk = 0;
     s.chunk_live = 0;
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
-        // block j < ja: Key-code chunks 64 j + lane; block j >= ja: chunk seg_end[2] + 64 (j - ja) + lane
         const int j = kWaves * i + wave;
         if (j < y.ja + y.jb) s.n_chunk = i + 1;
-        int c = j < y.ja ? 64 * j + lane : y.seg_end[2] + 64 * (j - y.ja) + lane;
-        const bool live = j < y.ja ? c < y.seg_end[2] : (j < y.ja + y.jb && c < y.n_chunks);
+        const int c = j < y.ja ? 64 * j + lane : 64 * (j - y.ja) + lane;  // chunk within its region
+        const bool live = j < y.ja ? c < na : (j < y.ja + y.jb && c < nb_chunks);
         if (live) s.chunk_live |= 1 << i;
-        else c = 0;  // dead lanes are masked off at issue
-        const unsigned char* src;
-        int stride;
-        if (c < y.seg_end[0]) {
-            src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]) + 16 * c;
-            stride = kPage * L.k_words[0] * 4;
-        } else if (c < y.seg_end[1]) {
-            src = reinterpret_cast<const unsigned char*>(L.k_code[1] + row0 * L.k_words[1]) + 16 * (c - y.seg_end[0]);
-            stride = kPage * L.k_words[1] * 4;
-        } else if (c < y.seg_end[2]) {
-            src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]) + 16 * (c - y.seg_end[1]);
-            stride = kPage * L.k_words[2] * 4;
-        } else if (c < y.seg_end[3]) {
-            src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]) + 16 * (c - y.seg_end[2]);
-            stride = kPage * L.k_width[3] * 2;
-        } else if (c < y.seg_end[4]) {
-            src = reinterpret_cast<const unsigned char*>(L.v_scale + row0) + 16 * (c - y.seg_end[3]);
-            stride = kPage * 2;
-        } else {
-            src = reinterpret_cast<const unsigned char*>(L.v_min + row0) + 16 * (c - y.seg_end[4]);
-            stride = kPage * 2;
+        const unsigned char* src = reinterpret_cast<const unsigned char*>(L.k_code[0]);
+        int stride = 0;
+        if (live && j < y.ja) {
+            if (c < y.seg_end[0]) {
+                src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]) + 16 * c;
+                stride = kPage * L.k_words[0] * 4;
+            } else if (c < y.seg_end[1]) {
+                src = reinterpret_cast<const unsigned char*>(L.k_code[1] + row0 * L.k_words[1]) + 16 * (c - y.seg_end[0]);
+                stride = kPage * L.k_words[1] * 4;
+            } else {
+                src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]) + 16 * (c - y.seg_end[1]);
+                stride = kPage * L.k_words[2] * 4;
+            }
+        } else if (live) {
+            // region B: v scale (16 chunks), v min (16), v codes (256), fp16-tier rows
+            if (c < 16) {
+                src = reinterpret_cast<const unsigned char*>(L.v_scale + row0) + 16 * c;
+                stride = kPage * 2;
+            } else if (c < 32) {
+                src = reinterpret_cast<const unsigned char*>(L.v_min + row0) + 16 * (c - 16);
+                stride = kPage * 2;
+            } else if (c < 32 + 256) {
+                src = reinterpret_cast<const unsigned char*>(L.v_code + row0 * 8) + 16 * (c - 32);
+                stride = kPage * 32;
+            } else {
+                src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]) + 16 * (c - 288);
+                stride = kPage * L.k_width[3] * 2;
+            }
         }
         s.chunk[i] = src;
         s.chunk_stride[i] = stride;
     }
-    // Value codes: dword e of the regrouped page = word (e/4)%8 of token 4*(e/32) + e%4.
-#pragma unroll
-    for (int i = 0; i < kVcDma; ++i) {
-        const int e = (kWaves * i + wave) * 64 + lane;
-        const int tok = 4 * (e >> 5) + (e & 3), word = (e >> 2) & 7;
-        s.vc[i] = reinterpret_cast<const unsigned char*>(L.v_code + (row0 + tok) * 8 + word);
-    }
-    // Key scale/min slots: one dword = the fp16 pair of pages (p & ~1, p | 1) of one slot.
-    // Padding slots read slot 0 of the first integer tier (their q is zero).
+    // Key scale/min slots.  Padding slots read slot 0 of the first integer tier (their q is zero).
     s.n_ks = 0;
+    s.ks_live = 0;
     const int t0 = L.k_width[0] ? 0 : L.k_width[1] ? 1 : 2;
     const unsigned char* dummy = reinterpret_cast<const unsigned char*>(
         sel3(L.k_scale, t0) + kgrp_idx(L, b, h, sel4(L.k_width, t0), 0, pbeg & ~1));
@@ -330,6 +350,7 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
         const int e = e0 + lane;
         const unsigned char* src = dummy;
         if (e < y.n_kslots) {
+            s.ks_live |= 1 << i;
             const bool is_min = e >= y.n_kslots / 2;
             const int slot = is_min ? e - y.n_kslots / 2 : e;
             const int gb = slot >> 3, pos = slot & 7;
@@ -346,31 +367,34 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
         }
         s.ks[i] = src;
     }
-    s.per_page = s.n_chunk + kVcDma + s.n_ks;
+    s.per_page = s.n_chunk + s.n_ks;
 }
 
-// Issue the DMA of page ``page`` into Key-code buffer ``rawa`` and rest buffer ``rawb``,
-// and advance the sources one page.
-__device__ __forceinline__ void dma_page(DmaSrc& s, unsigned char* rawa, unsigned char* rawb, const MfmaLayout& y,
-                                         int page, int wave) {
+// Issue the DMA of page ``page``: region A into the Key-code buffer at LDS address ``rawa``,
+// region B and the slots into the rest buffer at ``rawb`` (32-bit LDS addresses); advance
+// the sources one page.
+__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t rawa, uint32_t rawb, const MfmaLayout& y, int page,
+                                         int wave) {
+    // The per-instruction conditions and addresses are cheap scalar work; passing their inputs
+    // through an empty asm keeps the compiler from hoisting one register per instruction out
+    // of the page loop (which would exhaust the scalar registers).
+    int n_chunk = s.n_chunk, n_ks = s.n_ks, ja = y.ja, jw = wave;
+    int chunk_live = s.chunk_live, ks_live = s.ks_live;
+    asm volatile("" : "+s"(n_chunk), "+s"(n_ks), "+s"(ja), "+s"(jw));
+    asm volatile("" : "+v"(chunk_live), "+v"(ks_live));
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
-        if (i < s.n_chunk) {
-            const int j = kWaves * i + wave;
-            unsigned char* dst = j < y.ja ? rawa + 1024 * j : rawb + 1024 * (j - y.ja);
-            if (s.chunk_live & (1 << i)) dma16(s.chunk[i], dst);
+        if (i < n_chunk) {
+            const int j = kWaves * i + jw;
+            const uint32_t dst = j < ja ? rawa + 1024 * j : rawb + 1024 * (j - ja);
+            if (chunk_live & (1 << i)) dma16(s.chunk[i], dst);
             s.chunk[i] += s.chunk_stride[i];
         }
     }
 #pragma unroll
-    for (int i = 0; i < kVcDma; ++i) {
-        dma4(s.vc[i], rawb + y.rawb_vc + (kWaves * i + wave) * 256);
-        s.vc[i] += kPage * 32;
-    }
-#pragma unroll
     for (int i = 0; i < kMaxKsDma; ++i) {
-        if (i < s.n_ks) {
-            dma4(s.ks[i], rawb + y.rawb_ks + (kWaves * i + wave) * 256);
+        if (i < n_ks) {
+            if (ks_live & (1 << i)) dma4(s.ks[i], rawb + y.rawb_ks + (kWaves * i + jw) * 256);
             if (page & 1) s.ks[i] += 4;
         }
     }
@@ -380,25 +404,26 @@ __device__ __forceinline__ void dma_page(DmaSrc& s, unsigned char* rawa, unsigne
 __device__ __forceinline__ void prepare_page(const MfmaLayout& y, const unsigned char* raw, unsigned char* ck,
                                              const float* qperm, int page, int g, int w16, int tid) {
     const int lane = tid & 63;
-    if (tid < 256) {
+    {
         // Value codes: dwords (group tg, word w, tokens 0..3) -> byte columns
         const int tg = tid >> 3, w = tid & 7;
-        const uint4 a = *reinterpret_cast<const uint4*>(raw + y.rawb_vc + 16 * (tg * 8 + w));
+        const uint32_t* vc = reinterpret_cast<const uint32_t*>(raw + kRawbVc) + 32 * tg + w;
         uint32_t o[4];
-        byte_transpose4(a.x, a.y, a.z, a.w, o);
+        byte_transpose4(vc[0], vc[8], vc[16], vc[24], o);
         uint32_t* vt = reinterpret_cast<uint32_t*>(ck + y.ck_vt);
 #pragma unroll
         for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = o[k];
-    } else if (tid < 256 + kPage) {
+    }
+    if (tid < kPage) {
         // Value scale, the per-token constant vmin - 4 * vscale (4: the offset of the Value-code
         // unpack), and the token's fp16-tier row zero padded to w16p columns
-        const int t = tid - 256;
-        const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + y.rawb_vs);
-        const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + y.rawb_vm);
+        const int t = tid;
+        const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + kRawbVs);
+        const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + kRawbVm);
         const float s = f16_to_f32(vs[t]);
         reinterpret_cast<float*>(ck + y.ck_vsc)[t] = s;
         reinterpret_cast<float*>(ck + y.ck_vmid)[t] = fmaf(-4.f, s, f16_to_f32(vm[t]));
-        const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw) + t * w16;
+        const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw + kRawbF16) + t * w16;
         uint4* dst = reinterpret_cast<uint4*>(ck + y.ck_v16 + 2 * t * y.w16p);
         for (int c0 = 0; c0 < w16; c0 += 8) {
             uint32_t v[8];
@@ -407,26 +432,27 @@ __device__ __forceinline__ void prepare_page(const MfmaLayout& y, const unsigned
             dst[c0 >> 3] = uint4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
         }
     }
-    // Qs and the bias: wave n takes head n; lane pair (2 gb', +1) takes block gb' + 32 i
-    const int n = tid >> 6;
+    // Qs and the bias: thread (head tid / 32, blocks tid % 32 + 32 i); each head's bias is
+    // summed over its half wave
+    const int n = tid >> 5;
     float bsum = 0.f;
     if (n < g) {
         const uint32_t* ksr = reinterpret_cast<const uint32_t*>(raw + y.rawb_ks);
-        const int half = lane & 1;
+        half8* qs = reinterpret_cast<half8*>(ck + y.ck_qs);
         if (page & 1) {
-            for (int gb = lane >> 1; gb < y.nb; gb += 32) bsum += qs_quad<true>(qperm, ksr, ck + y.ck_qs, y, gb, n, half);
+            for (int gb = tid & 31; gb < y.nb; gb += 32) bsum += qs_block<true>(qperm, ksr, qs, y, gb, n);
         } else {
-            for (int gb = lane >> 1; gb < y.nb; gb += 32) bsum += qs_quad<false>(qperm, ksr, ck + y.ck_qs, y, gb, n, half);
+            for (int gb = tid & 31; gb < y.nb; gb += 32) bsum += qs_block<false>(qperm, ksr, qs, y, gb, n);
         }
     }
-    bsum = wave_sum_to_63(bsum);
-    if (lane == 63) reinterpret_cast<float*>(ck + y.ck_bias)[n] = bsum;
+    bsum = half_wave_sum(bsum);
+    if ((lane & 31) == 31) reinterpret_cast<float*>(ck + y.ck_bias)[n] = bsum;
 }
 
-__global__ __launch_bounds__(kThreads, 4) void decode_mfma_kernel(MfmaParams mp) {
+__global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
     const DecodeParams& p = mp.p;
     const MfmaLayout& y = mp.y;
-    const UnpackBits& kbits = mp.k;
+    const UnpackBits kv = vgpr_bits(mp.k);
     const lf_packed_layer& L = p.L;
     const lf_decode_args& A = p.A;
     const int item = blockIdx.x;
@@ -445,10 +471,10 @@ __global__ __launch_bounds__(kThreads, 4) void decode_mfma_kernel(MfmaParams mp)
     extern __shared__ __align__(16) unsigned char smem[];
     float* qperm = reinterpret_cast<float*>(smem + y.off_qperm);
     float* small = reinterpret_cast<float*>(smem + y.off_small);
-    float* alpha_lds = small;      // [8 waves][8]: softmax rescale per head
-    float* wstat = small + 64;     // [8 waves][3][8]: m, l, mid per head
+    float* alpha_lds = small;              // [waves][8]: softmax rescale per head
+    float* wstat = small + kWaves * 8;     // [waves][3][8]: m, l, mid per head
     // Aliases of the prepared + raw buffers (free outside the page loop): q [8][128], wave
-    // outputs [8][8][128], residual probabilities [8][16][8].
+    // outputs [waves][8][128], residual probabilities [waves][32][8].
     float* qlin = reinterpret_cast<float*>(smem + y.off_ck);
     float* red = qlin + 8 * kD;
     float* pbuf = red + kWaves * 8 * kD;
@@ -507,22 +533,25 @@ __global__ __launch_bounds__(kThreads, 4) void decode_mfma_kernel(MfmaParams mp)
         unsigned char* rawa0 = smem + y.off_rawa;
         unsigned char* rawb0 = smem + y.off_rawb;
         unsigned char* ck0 = smem + y.off_ck;
+        const uint32_t lds0 = lds_addr(smem);  // LDS address of smem
+        const uint32_t rawa_lds = lds0 + y.off_rawa, rawb_lds = lds0 + y.off_rawb;
         const int w16 = L.k_width[3];
-        dma_page(ds, rawa0, rawb0, y, pbeg, wave);
-        if (pbeg + 1 < pend) dma_page(ds, rawa0 + y.rawa_bytes, rawb0 + y.rawb_bytes, y, pbeg + 1, wave);
+        dma_page(ds, rawa_lds, rawb_lds, y, pbeg, wave);
+        if (pbeg + 1 < pend) dma_page(ds, rawa_lds + y.rawa_bytes, rawb_lds + y.rawb_bytes, y, pbeg + 1, wave);
         dma_barrier(pbeg + 1 < pend ? ds.per_page : 0);  // page pbeg landed (every wave's share)
         prepare_page(y, rawb0, ck0, qperm, pbeg, g, w16, tid);
 
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
         const int sh = 2 * (n16 & 3);
-        const int tok = 16 * wave + n16;
+        const int tok0 = 32 * wave + n16, tok1 = tok0 + 16;
         for (int page = pbeg; page < pend; ++page) {
             const int rel = page - pbeg;
             // Page + 1 landed; page prepared; page - 1 computed, so its Key-code buffer and
             // prepared buffer are free, and page's rest buffer was consumed by its preparation.
             dma_barrier(0);
             if (page + 2 < pend)
-                dma_page(ds, rawa0 + ((rel + 2) % 3) * y.rawa_bytes, rawb0 + (rel & 1) * y.rawb_bytes, y, page + 2, wave);
+                dma_page(ds, rawa_lds + ((rel + 2) % 3) * y.rawa_bytes, rawb_lds + (rel & 1) * y.rawb_bytes, y, page + 2,
+                         wave);
             if (page + 1 < pend)
                 prepare_page(y, rawb0 + ((rel + 1) & 1) * y.rawb_bytes, ck0 + ((rel + 1) & 1) * y.ck_bytes, qperm,
                              page + 1, g, w16, tid);
@@ -533,78 +562,104 @@ __global__ __launch_bounds__(kThreads, 4) void decode_mfma_kernel(MfmaParams mp)
             const half8* qs = reinterpret_cast<const half8*>(ck + y.ck_qs);
             // Integer tiers read up to 7 dwords past their segment (inside the LDS allocation):
             // those blocks have Qs == 0 and unpack to finite values.
-            float4v acc = {0.f, 0.f, 0.f, 0.f};
+            float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
             {
                 const uint32_t* k0 = reinterpret_cast<const uint32_t*>(raw);
                 for (int s2 = 0; s2 < y.kst[0] / 2; ++s2) {
-                    const uint32_t wa = k0[tok * kw0 + 4 * s2 + kb];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wa, kbits), qs[(8 * s2 + kb) * 16 + n16], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wa, kbits), qs[(8 * s2 + 4 + kb) * 16 + n16], acc, 0,
-                                                                 0, 0);
+                    const uint32_t wa = k0[tok0 * kw0 + 4 * s2 + kb];
+                    const uint32_t wb = k0[tok1 * kw0 + 4 * s2 + kb];
+                    const half8 bq0 = qs[(8 * s2 + kb) * 16 + n16];
+                    const half8 bq1 = qs[(8 * s2 + 4 + kb) * 16 + n16];
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wa, kv), bq0, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wb, kv), bq0, acc1, 0, 0, 0);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wa, kv), bq1, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wb, kv), bq1, acc1, 0, 0, 0);
                 }
                 const uint32_t* k1 = reinterpret_cast<const uint32_t*>(raw + 16 * y.seg_end[0]);
                 for (int s = 0; s < y.kst[1]; ++s) {
                     const half8 bq = qs[(4 * (y.kfirst[1] + s) + kb) * 16 + n16];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok * kw1 + 4 * s + kb], kbits), bq, acc, 0, 0, 0);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok0 * kw1 + 4 * s + kb], kv), bq, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok1 * kw1 + 4 * s + kb], kv), bq, acc1, 0, 0, 0);
                 }
                 const uint32_t* k2 = reinterpret_cast<const uint32_t*>(raw + 16 * y.seg_end[1]);
                 for (int s = 0; s < y.kst[2]; ++s) {
                     const int w0 = 2 * (4 * s + kb);
                     const half8 bq = qs[(4 * (y.kfirst[2] + s) + kb) * 16 + n16];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok * kw2 + w0], k2[tok * kw2 + w0 + 1]), bq,
-                                                                 acc, 0, 0, 0);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok0 * kw2 + w0], k2[tok0 * kw2 + w0 + 1]), bq,
+                                                                  acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok1 * kw2 + w0], k2[tok1 * kw2 + w0 + 1]), bq,
+                                                                  acc1, 0, 0, 0);
                 }
                 const unsigned char* v16 = ck + y.ck_v16;
                 for (int s = 0; s < y.kst[3]; ++s) {
                     const int col = 8 * (4 * s + kb);
-                    const uint4 ua =
-                        col < y.w16p ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok * y.w16p + col)) : uint4{0, 0, 0, 0};
+                    const bool ok = col < y.w16p;
+                    const uint4 ua = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok0 * y.w16p + col)) : uint4{0, 0, 0, 0};
+                    const uint4 ub = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok1 * y.w16p + col)) : uint4{0, 0, 0, 0};
                     const half8 bq = qs[(4 * (y.kfirst[3] + s) + kb) * 16 + n16];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ua), bq, acc, 0, 0, 0);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ua), bq, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ub), bq, acc1, 0, 0, 0);
                 }
             }
             // hi + lo columns (row_shl:8, zero outside the row).  The accumulator elements are
             // copied to scalars before the DPP move: applied to vector elements directly, this
             // compiler emits one move for all of them.  The page's bias enters through the max.
-            float sv[4];
-            const float accs[4] = {acc[0], acc[1], acc[2], acc[3]};
+            float sv[8];
+            const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < 8; ++r) {
                 const int xi = __builtin_bit_cast(int, accs[r]);
                 sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
             }
             // ---- online softmax (log2 domain) ----
             const float bias = (n16 < 8) ? reinterpret_cast<const float*>(ck + y.ck_bias)[n16] : 0.f;
-            float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            float mx = sv[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
             mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
             mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
             const float m_new = fmaxf(m_run, mx + bias);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             const float m_off = m_new - bias;  // p = 2^(sv + bias - m_new)
             m_run = m_new;
-            const float4 vs = *reinterpret_cast<const float4*>(ck + y.ck_vsc + 4 * (16 * wave + 4 * kb));
-            const float4 vd = *reinterpret_cast<const float4*>(ck + y.ck_vmid + 4 * (16 * wave + 4 * kb));
-            const float p0 = __builtin_amdgcn_exp2f(sv[0] - m_off), p1 = __builtin_amdgcn_exp2f(sv[1] - m_off);
-            const float p2 = __builtin_amdgcn_exp2f(sv[2] - m_off), p3 = __builtin_amdgcn_exp2f(sv[3] - m_off);
-            l_run = l_run * alpha + ((p0 + p1) + (p2 + p3));
-            mid_run = mid_run * alpha + fmaf(p0, vd.x, fmaf(p1, vd.y, fmaf(p2, vd.z, p3 * vd.w)));
-            // A operand of the value product: k = 8*kb + j holds token 4*kb + (0, 2, 1, 3)[j] for
-            // j < 4 and zero above; hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8.
-            const float x0 = p0 * vs.x, x1 = p1 * vs.y, x2 = p2 * vs.z, x3 = p3 * vs.w;
-            const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
-            const _Float16 h2 = static_cast<_Float16>(x2), h3 = static_cast<_Float16>(x3);
-            const half2v hv02 = {h0, h2}, hv13 = {h1, h3};
-            const half2v lv02 = {static_cast<_Float16>(x0 - static_cast<float>(h0)),
-                                 static_cast<_Float16>(x2 - static_cast<float>(h2))};
-            const half2v lv13 = {static_cast<_Float16>(x1 - static_cast<float>(h1)),
-                                 static_cast<_Float16>(x3 - static_cast<float>(h3))};
+            const float* vsc = reinterpret_cast<const float*>(ck + y.ck_vsc);
+            const float* vmd = reinterpret_cast<const float*>(ck + y.ck_vmid);
+            const float4 s_lo = *reinterpret_cast<const float4*>(vsc + 32 * wave + 4 * kb);
+            const float4 s_hi = *reinterpret_cast<const float4*>(vsc + 32 * wave + 16 + 4 * kb);
+            const float4 d_lo = *reinterpret_cast<const float4*>(vmd + 32 * wave + 4 * kb);
+            const float4 d_hi = *reinterpret_cast<const float4*>(vmd + 32 * wave + 16 + 4 * kb);
+            const float vs[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
+            const float vd[8] = {d_lo.x, d_lo.y, d_lo.z, d_lo.w, d_hi.x, d_hi.y, d_hi.z, d_hi.w};
+            float pp[8];
+            float psum = 0.f, pmid = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float pi = __builtin_amdgcn_exp2f(sv[i] - m_off);
+                psum += pi;
+                pmid = fmaf(pi, vd[i], pmid);
+                pp[i] = pi * vs[i];
+            }
+            l_run = l_run * alpha + psum;
+            mid_run = mid_run * alpha + pmid;
+            // A operand of the value product: k order (t0,t2),(t1,t3),(t4,t6),(t5,t7) of the
+            // lane's tokens; hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8.
+            uint32_t ahi[4], alo[4];
+            const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float x0 = pp[order[2 * j]], x1 = pp[order[2 * j + 1]];
+                const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
+                const half2v hv = {h0, h1};
+                const half2v lv = {static_cast<_Float16>(x0 - static_cast<float>(h0)),
+                                   static_cast<_Float16>(x1 - static_cast<float>(h1))};
+                ahi[j] = __builtin_bit_cast(uint32_t, hv);
+                alo[j] = __builtin_bit_cast(uint32_t, lv);
+            }
             uint4 au;
-            au.x = __builtin_amdgcn_update_dpp(__builtin_bit_cast(uint32_t, hv02), __builtin_bit_cast(uint32_t, lv02), 0x118,
-                                               0xf, 0xc, false);
-            au.y = __builtin_amdgcn_update_dpp(__builtin_bit_cast(uint32_t, hv13), __builtin_bit_cast(uint32_t, lv13), 0x118,
-                                               0xf, 0xc, false);
-            au.z = 0u;
-            au.w = 0u;
+            au.x = __builtin_amdgcn_update_dpp(ahi[0], alo[0], 0x118, 0xf, 0xc, false);
+            au.y = __builtin_amdgcn_update_dpp(ahi[1], alo[1], 0x118, 0xf, 0xc, false);
+            au.z = __builtin_amdgcn_update_dpp(ahi[2], alo[2], 0x118, 0xf, 0xc, false);
+            au.w = __builtin_amdgcn_update_dpp(ahi[3], alo[3], 0x118, 0xf, 0xc, false);
             const half8 ap = __builtin_bit_cast(half8, au);
             // Rescale O when some head's max moved: alpha of the 4 output rows this lane holds
             // (rows 4*kb + r, head (4*kb + r) % 8); a same-wave LDS write then read is ordered
@@ -621,20 +676,23 @@ __global__ __launch_bounds__(kThreads, 4) void decode_mfma_kernel(MfmaParams mp)
                     O[nt][3] *= arow.w;
                 }
             }
-            // ---- value product: codes of tokens 4*kb..4*kb+3, channel 16*nt + n16 ----
-            const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + y.ck_vt) + (4 * wave + kb) * 36 + (n16 >> 2) * 8;
-            const uint4 da = *reinterpret_cast<const uint4*>(vt);
-            const uint4 db = *reinterpret_cast<const uint4*>(vt + 4);
-            const uint32_t d[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+            // ---- value product: codes of the lane's 8 tokens, channel 16*nt + n16 ----
+            const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + y.ck_vt);
+            const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
+            const uint4 d0b = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8 + 4);
+            const uint4 d1a = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8);
+            const uint4 d1b = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8 + 4);
+            const uint32_t dlo[8] = {d0a.x, d0a.y, d0a.z, d0a.w, d0b.x, d0b.y, d0b.z, d0b.w};
+            const uint32_t dhi[8] = {d1a.x, d1a.y, d1a.z, d1a.w, d1b.x, d1b.y, d1b.z, d1b.w};
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
                 // code bits to mantissa 8..9 under exponent 4: value 4 + c (the offset is folded
                 // into the per-token constant); tokens (0, 2) sit at byte bits sh, (1, 3) at 8 + sh
                 uint4 bu;
-                bu.x = bfi(d[nt] << (8 - sh), kbits.m2hi, kbits.e4);
-                bu.y = bfi(d[nt] >> sh, kbits.m2hi, kbits.e4);
-                bu.z = 0u;
-                bu.w = 0u;
+                bu.x = bfi(dlo[nt] << (8 - sh), kv.m2hi, kv.e4);
+                bu.y = bfi(dlo[nt] >> sh, kv.m2hi, kv.e4);
+                bu.z = bfi(dhi[nt] << (8 - sh), kv.m2hi, kv.e4);
+                bu.w = bfi(dhi[nt] >> sh, kv.m2hi, kv.e4);
                 float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
                 o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
@@ -665,69 +723,134 @@ __global__ __launch_bounds__(kThreads, 4) void decode_mfma_kernel(MfmaParams mp)
         __syncthreads();
     } else {
         // ---- residual item: the tail page and the new token (at most page_size tokens) ----
-        // VALU: wave w scores tokens 16w..16w+15 (lane = token), then accumulates them into
-        // channels 2*lane, 2*lane+1.  One pass, so each wave's max is final.
+        // VALU: wave w scores tokens 32w..32w+31 (lane % 32 = token, lane / 32 = channel half;
+        // q read as float4 from LDS), then accumulates them into channels 2*lane, 2*lane+1.
+        // One pass, so each wave's max is final.  Every global load of a phase is issued
+        // before its first use.
         const int tl = A.tail_len[b];
         const int n_res = tl + (A.k_new != nullptr ? 1 : 0);
-        const int t = 16 * wave + lane;
-        const bool act = lane < 16 && t < n_res;
+        const int t = 32 * wave + (lane & 31);
+        const int ch0 = 64 * (lane >> 5);
+        const bool act = t < n_res;
         float s[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) s[i] = 0.f;
         if (act) {
             const void* kp = t < tl ? A.tail_k : A.k_new;
             const int kdt = t < tl ? A.tail_dtype : A.new_dtype;
-            const int64_t kbase = t < tl ? ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + t) * kD
-                                         : (static_cast<int64_t>(b) * L.n_kv + h) * kD;
-            for (int c0 = 0; c0 < kD; c0 += 32) {
-                float kv[4][8];
+            const int64_t kbase = (t < tl ? ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + t) * kD
+                                          : (static_cast<int64_t>(b) * L.n_kv + h) * kD) + ch0;
+            float kv[64];
+            if (kdt != LF_FP32) {
+                uint4 raw[8];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) load8_as_f32(kp, kbase + c0 + 8 * u, kdt, kv[u]);
+                for (int u = 0; u < 8; ++u) raw[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(kp) + kbase + 8 * u);
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
 #pragma unroll
-                    for (int k = 0; k < 8; ++k)
+                    for (int k = 0; k < 8; ++k) {
+                        const uint16_t x = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+                        kv[8 * u + k] = kdt == LF_BF16 ? bf16_to_f32(x) : f16_to_f32(x);
+                    }
+                }
+            } else {
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) s[i] = fmaf(qlin[i * kD + c0 + 8 * u + k], kv[u][k], s[i]);
+                for (int u = 0; u < 8; ++u) load8_as_f32(kp, kbase + 8 * u, kdt, kv + 8 * u);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4* q4 = reinterpret_cast<const float4*>(qlin + i * kD + ch0);
+#pragma unroll
+                for (int c4 = 0; c4 < 16; ++c4) {
+                    const float4 q = q4[c4];
+                    s[i] = fmaf(q.x, kv[4 * c4], fmaf(q.y, kv[4 * c4 + 1], fmaf(q.z, kv[4 * c4 + 2], fmaf(q.w, kv[4 * c4 + 3], s[i]))));
+                }
             }
         }
-        float* pw = pbuf + wave * 16 * 8;  // [16][8]
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[i] += __shfl_xor(s[i], 32, kWave);
+        float* pw = pbuf + wave * 32 * 8;  // [32][8]
+        float mx[8], pv[8], lt[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx[i] = act ? s[i] : -__builtin_inff();
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], off, kWave));
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float x = act ? s[i] : -__builtin_inff();
-            const float mx = wave_max(x);
-            const float pi = act ? __builtin_amdgcn_exp2f(x - mx) : 0.f;
-            const float lt = wave_sum(pi);
-            if (lane < 16) pw[lane * 8 + i] = pi;
-            if (lane == 0) {
-                wstat[(wave * 3 + 0) * 8 + i] = mx;
-                wstat[(wave * 3 + 1) * 8 + i] = lt;
+            pv[i] = act ? __builtin_amdgcn_exp2f(s[i] - mx[i]) : 0.f;
+            lt[i] = pv[i];
+        }
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lt[i] += __shfl_xor(lt[i], off, kWave);
+        if (lane < 32) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pw[lane * 8 + i] = pv[i];
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                wstat[(wave * 3 + 0) * 8 + i] = mx[i];
+                wstat[(wave * 3 + 1) * 8 + i] = lt[i];
                 wstat[(wave * 3 + 2) * 8 + i] = 0.f;
             }
         }
         __builtin_amdgcn_wave_barrier();
-        const int cnt = max(0, min(16, n_res - 16 * wave));
+        const int cnt = max(0, min(32, n_res - 32 * wave));
+        const int64_t vrow0 = ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap) * kD;
+        const int64_t vnew = (static_cast<int64_t>(b) * L.n_kv + h) * kD;
+        float v0[32], v1[32];
+        if (A.tail_dtype != LF_FP32 && (A.v_new == nullptr || A.new_dtype != LF_FP32)) {
+            // 2-byte Values: one dword (channels 2*lane, 2*lane+1) per token, addresses chosen
+            // without branches so all 32 loads are in flight together
+            uint32_t raw[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const int tk = 32 * wave + k;
+                const bool in_tail = tk < tl;
+                const uint16_t* base = static_cast<const uint16_t*>(in_tail ? A.tail_v : A.v_new);
+                const int64_t idx = (in_tail ? vrow0 + static_cast<int64_t>(tk) * kD : vnew) + 2 * lane;
+                raw[k] = k < cnt ? *reinterpret_cast<const uint32_t*>(base + idx) : 0u;
+            }
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const int dt = 32 * wave + k < tl ? A.tail_dtype : A.new_dtype;
+                const uint16_t lo = static_cast<uint16_t>(raw[k] & 0xffffu), hi = static_cast<uint16_t>(raw[k] >> 16);
+                v0[k] = dt == LF_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+                v1[k] = dt == LF_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const int tk = 32 * wave + k;
+                v0[k] = 0.f;
+                v1[k] = 0.f;
+                if (k < cnt) {
+                    if (tk < tl) {
+                        v0[k] = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tk) * kD + 2 * lane, A.tail_dtype);
+                        v1[k] = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tk) * kD + 2 * lane + 1, A.tail_dtype);
+                    } else {
+                        v0[k] = load_as_f32(A.v_new, vnew + 2 * lane, A.new_dtype);
+                        v1[k] = load_as_f32(A.v_new, vnew + 2 * lane + 1, A.new_dtype);
+                    }
+                }
+            }
+        }
         float acc[2][8];
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[cc][i] = 0.f;
-        const int64_t vrow0 = ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap) * kD;
-        const int64_t vnew = (static_cast<int64_t>(b) * L.n_kv + h) * kD;
-        for (int k = 0; k < cnt; ++k) {
-            const int tk = 16 * wave + k;
-            float v0, v1;
-            if (tk < tl) {
-                v0 = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tk) * kD + 2 * lane, A.tail_dtype);
-                v1 = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tk) * kD + 2 * lane + 1, A.tail_dtype);
-            } else {
-                v0 = load_as_f32(A.v_new, vnew + 2 * lane, A.new_dtype);
-                v1 = load_as_f32(A.v_new, vnew + 2 * lane + 1, A.new_dtype);
-            }
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                acc[0][i] = fmaf(pw[k * 8 + i], v0, acc[0][i]);
-                acc[1][i] = fmaf(pw[k * 8 + i], v1, acc[1][i]);
+                acc[0][i] = fmaf(pw[k * 8 + i], v0[k], acc[0][i]);
+                acc[1][i] = fmaf(pw[k * 8 + i], v1[k], acc[1][i]);
             }
         }
 #pragma unroll
@@ -793,13 +916,8 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
         seg += kPage * L.k_words[t] * 4 / 16;
         y.seg_end[t] = seg;
     }
-    seg += kPage * L.k_width[3] * 2 / 16;
-    y.seg_end[3] = seg;
-    seg += kPage * 2 / 16;
-    y.seg_end[4] = seg;
-    seg += kPage * 2 / 16;
-    y.seg_end[5] = seg;
-    y.n_chunks = seg;
+    // region B (DMA order): v scale, v min, v codes (256 chunks), fp16-tier rows
+    y.n_chunks = y.seg_end[2] + 16 + 16 + 256 + kPage * L.k_width[3] * 2 / 16;
     y.ja = (y.seg_end[2] + 63) / 64;
     y.jb = (y.n_chunks - y.seg_end[2] + 63) / 64;
     if (y.ja + y.jb > kMaxDma * kWaves) return false;
@@ -808,15 +926,9 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     // Key-code buffer: the K0, K1, K2 rows; rest buffer: fp16 tier, v scale, v min, Value codes,
     // Key scale/min (DMA lanes past the last chunk of a region do not write)
     y.rawa_bytes = round_up(16 * y.seg_end[2], 16);
-    int rb = 16 * (y.seg_end[3] - y.seg_end[2]);
-    y.rawb_vs = rb;
-    rb += 2 * kPage;
-    y.rawb_vm = rb;
-    rb += 2 * kPage;
-    y.rawb_vc = rb;
-    rb += 4096;
-    y.rawb_ks = rb;
-    rb += ((y.n_kslots + 63) / 64) * 256;
+    int rb = kRawbF16 + kPage * L.k_width[3] * 2;
+    y.rawb_ks = round_up(rb, 16);
+    rb = y.rawb_ks + ((y.n_kslots + 63) / 64) * 256;
     y.rawb_bytes = round_up(rb, 16);
     int ck = 0;
     y.ck_qs = ck;
@@ -839,7 +951,7 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     y.off_tt = off;
     off += round_up(2 * (L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3]), 16);
     y.off_small = off;
-    off += (64 + kWaves * 24) * 4;
+    off += kWaves * 32 * 4;
     off = round_up(off, 16);
     y.off_ck = off;
     off += 2 * y.ck_bytes;
@@ -847,9 +959,9 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     off += 3 * y.rawa_bytes;
     y.off_rawb = off;
     off += 2 * y.rawb_bytes;
-    // q [8][128], wave outputs [8][8][128] and residual probabilities [8][16][8] alias the
-    // prepared, Key-code and rest buffers
-    const int alias_bytes = (8 + kWaves * 8) * kD * 4 + kWaves * 16 * 8 * 4;
+    // q [8][128], wave outputs [waves][8][128] and residual probabilities [waves][32][8] alias
+    // the prepared, Key-code and rest buffers
+    const int alias_bytes = (8 + kWaves * 8) * kD * 4 + kWaves * 32 * 8 * 4;
     if (off - y.off_ck < alias_bytes) off = y.off_ck + alias_bytes;
     y.lds_bytes = off;
     return y.lds_bytes <= 160 * 1024 - 64;

@@ -84,14 +84,27 @@ def reference_attention(manager, layer_idx: int, query: torch.Tensor, key_new: t
     return torch.stack(outs).to(dtype=query.dtype)
 
 
-def choose_pages_per_split(total_page_heads: int, kernel: int) -> int:
-    """Pages per split-K item: about four workgroups per CU of the 256 (measured on the 7B
-    shape at 32K context: 16 pages per item beats 8 and 32 on the MFMA kernel)."""
+_CU_COUNT: dict = {}
+
+
+def _cu_count(device) -> int:
+    key = str(device)
+    if key not in _CU_COUNT:
+        _CU_COUNT[key] = int(torch.cuda.get_device_properties(device).multi_processor_count)
+    return _CU_COUNT[key]
+
+
+def choose_pages_per_split(total_page_heads: int, kernel: int, residual_items: int = 0, device=None) -> int:
+    """Pages per split-K item.  The decode kernel holds two workgroups per CU; splitting the
+    pages so that page items plus residual items fill those slots exactly once runs the
+    launch in a single round (measured on the 7B shape at 32K context: the single-round split
+    beats 16 and 32 pages per item)."""
     forced = env_int("LOGITFILL_AMD_PAGES_PER_SPLIT", 0)
     if forced > 0:
         return forced
-    target = 1024
-    return max(1, min(64, math.ceil(total_page_heads / target)))
+    slots = 2 * (_cu_count(device) if device is not None else 256)
+    page_slots = max(slots - residual_items, slots // 2)
+    return max(1, math.ceil(total_page_heads / page_slots))
 
 
 class DecodePlan:
@@ -147,7 +160,7 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     P = layer.page_size
     hist_pages = [h // P for h in layer.hist_lens]
     if pages_per_split is None:
-        pages_per_split = choose_pages_per_split(sum(hist_pages) * layer.n_kv, kernel)
+        pages_per_split = choose_pages_per_split(sum(hist_pages) * layer.n_kv, kernel, B * layer.n_kv, layer.device)
     plan = layer.decode_plan
     if plan is None or plan.key != (tuple(hist_pages), pages_per_split):
         plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device)

@@ -97,10 +97,10 @@ def test_plan_decode_known_answer():
     n = lib.lf_plan_decode(hp, 3, 2, work, 10, seq)
     assert n == 7
     items = np.array(list(work)[:28]).reshape(7, 4).tolist()
-    assert items == [[0, 0, 2, 0], [0, 2, 4, 0], [0, 4, 5, 0], [0, 0, 0, 1],
-                     [1, 0, 0, 1],
-                     [2, 0, 2, 0], [2, 0, 0, 1]]
-    assert list(seq) == [0, 4, 4, 1, 5, 2]
+    assert items == [[0, 0, 0, 1], [1, 0, 0, 1], [2, 0, 0, 1],          # residual items first
+                     [0, 0, 2, 0], [0, 2, 4, 0], [0, 4, 5, 0],
+                     [2, 0, 2, 0]]
+    assert list(seq) == [3, 3, 6, 0, 6, 1]
     assert lib.lf_plan_decode(hp, 3, 2, work, 6, seq) == -4          # LF_E_WORKSPACE
     assert lib.lf_plan_decode(hp, 3, 0, work, 10, seq) == -2         # LF_E_SHAPE
 
