@@ -56,6 +56,12 @@ constexpr int kRawbVs = 0;    // rest buffer: Value scale [128] fp16
 constexpr int kRawbVm = 256;  //              Value min [128] fp16
 constexpr int kRawbVc = 512;  //              Value codes [128][8] u32
 constexpr int kRawbF16 = 4608;  //            fp16-tier rows [128][width16]
+// Prepared buffer: fixed offsets first (they become immediate offsets of the LDS accesses).
+constexpr int kCkVsc = 0;       // [128] fp32 Value scale
+constexpr int kCkVmid = 512;    // [128] fp32 vmin - 4 * vscale
+constexpr int kCkBias = 1024;   // [8] fp32 page bias per head
+constexpr int kCkVt = 1056;     // [32 groups][36] u32 Value-code byte columns (4 per 8-word row) + 4 pad
+constexpr int kCkQs = kCkVt + 32 * 36 * 4;  // [nb][16][8] fp16 Qs hi (rows 0..7) / lo (rows 8..15)
 
 struct MfmaLayout {
     int kst[4];          // K-steps per tier (int2: even; K-step s takes half s&1 of 4 words)
@@ -67,16 +73,12 @@ struct MfmaLayout {
     int n_chunks;        // region A + region B chunks
     int ja, jb;          // 64-chunk DMA blocks of the Key codes (chunks [0, seg_end[2])) and of the rest
     int n_kslots;        // 2 * nb_int * 8: Key scale slots, then Key min slots
-    int rawa_bytes;      // Key-code buffer: K0, K1, K2 rows of the page
+    int rawa_bytes;      // Key-code buffer: K0, K1, K2 rows of the page, padded to whole DMA blocks
     int rawb_ks;         // rest buffer (v scale at 0, v min at 256, [128][8] u32 Value codes at 512,
-                         // fp16-tier rows at 4608): [n_kslots] u32 Key scale / min page pairs
+                         // fp16-tier rows at 4608, padded to whole DMA blocks):
+                         // [n_kslots] u32 Key scale / min page pairs
     int rawb_bytes;
-    int ck_qs;           // prepared: [nb][16][8] fp16 Qs hi (rows 0..7) / lo (rows 8..15)
-    int ck_vt;           // prepared: [32 groups][36] u32 byte columns (4 per 8-word row) + 4 pad
-    int ck_v16;          // prepared: [128][w16p] fp16 Key fp16 tier, zero padded
-    int ck_vsc;          // prepared: [128] fp32 Value scale
-    int ck_vmid;         // prepared: [128] fp32 vmin - 4 * vscale
-    int ck_bias;         // prepared: [8] fp32 page bias per head
+    int ck_v16;          // prepared: [128][w16p] fp16 Key fp16 tier, zero padded (after Qs)
     int ck_bytes;
     int off_qperm;       // [nb][8 heads][8] fp32: q * scaling*log2e per slot (0 for padding)
     int off_tt;          // int16 tier table of this kv head (ranks -> channel ids), tiers back to back
@@ -215,52 +217,56 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a0, uint32_t a1, uint32
     o[3] = __builtin_amdgcn_perm(t23_hi, t01_hi, 0x07060302u);
 }
 
-// fp16 value of one page of a (page & ~1, page | 1) pair word, as float.
-template <bool Odd>
-__device__ __forceinline__ float pair_half(uint32_t w) {
-    return f16_to_f32(static_cast<uint16_t>(Odd ? (w >> 16) : (w & 0xffffu)));
+// Loop-invariant layout values, each in a scalar register of its own.  Read straight from the
+// kernel argument, the compiler keeps 16 consecutive argument dwords as one register tuple and
+// spills and reloads the tuple whole inside the page loop.
+struct LoopY {
+    int kst0, kst1, kst2, kst3, kf1, kf2, kf3, nb, nb_int, w16p;
+    int seg0, seg1, ja, rawa_bytes, rawb_ks, rawb_bytes, ck_v16, ck_bytes, n_kslots;
+};
+
+__device__ __forceinline__ LoopY loop_y(const MfmaLayout& y) {
+    LoopY z{y.kst[0], y.kst[1], y.kst[2], y.kst[3], y.kfirst[1], y.kfirst[2], y.kfirst[3], y.nb, y.nb_int, y.w16p,
+            y.seg_end[0], y.seg_end[1], y.ja, y.rawa_bytes, y.rawb_ks, y.rawb_bytes, y.ck_v16, y.ck_bytes, y.n_kslots};
+    asm volatile("" : "+s"(z.kst0), "+s"(z.kst1), "+s"(z.kst2), "+s"(z.kst3), "+s"(z.kf1), "+s"(z.kf2), "+s"(z.kf3),
+                      "+s"(z.nb), "+s"(z.nb_int), "+s"(z.w16p));
+    asm volatile("" : "+s"(z.seg0), "+s"(z.seg1), "+s"(z.ja), "+s"(z.rawa_bytes), "+s"(z.rawb_ks),
+                      "+s"(z.rawb_bytes), "+s"(z.ck_v16), "+s"(z.ck_bytes), "+s"(z.n_kslots));
+    return z;
 }
 
-// Qs of block ``gb`` for head ``n`` -- hi into row n, lo (the fp16 residual) into row n + 8 --
-// and the block's share of the bias sum_slot q * (min - beta * scale).  Padding slots have
-// q == 0; their scale/min words hold a real slot's (finite) values.
+// Qs of integer-tier block ``gb`` for head ``n`` -- hi into row n, lo (the fp16 residual) into
+// row n + 8 -- and the block's share of the bias sum_slot q * (min - beta * scale).  ``ksc`` /
+// ``kmn``: the block's Key scale / min pair words (page Odd in the high halves).  Padding
+// slots have q == 0; their scale/min words hold a real slot's (finite) values.  Written so
+// the compiler uses mixed-precision FMAs on the fp16 halves directly.
 template <bool Odd>
-__device__ __forceinline__ float qs_block(const float* qperm, const uint32_t* ksr, half8* qs, const MfmaLayout& y,
-                                          int gb, int n) {
-    const float* qrow = qperm + (gb * 8 + n) * 8;
+__device__ __forceinline__ float qs_block(const float* qrow, const uint32_t* ksc, const uint32_t* kmn, half8* qs_hi,
+                                          half8* qs_lo, float beta_lo, float beta_hi) {
     const float4 q0 = *reinterpret_cast<const float4*>(qrow);
     const float4 q1 = *reinterpret_cast<const float4*>(qrow + 4);
     const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const uint4 s0 = *reinterpret_cast<const uint4*>(ksc);
+    const uint4 s1 = *reinterpret_cast<const uint4*>(ksc + 4);
+    const uint4 m0 = *reinterpret_cast<const uint4*>(kmn);
+    const uint4 m1 = *reinterpret_cast<const uint4*>(kmn + 4);
+    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
     half8 hi, lo;
     float bsum = 0.f;
-    if (gb < y.nb_int) {
-        const uint4 s0 = *reinterpret_cast<const uint4*>(ksr + gb * 8);
-        const uint4 s1 = *reinterpret_cast<const uint4*>(ksr + gb * 8 + 4);
-        const uint4 m0 = *reinterpret_cast<const uint4*>(ksr + y.n_kslots / 2 + gb * 8);
-        const uint4 m1 = *reinterpret_cast<const uint4*>(ksr + y.n_kslots / 2 + gb * 8 + 4);
-        const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-        const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-        const int tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
-        const float beta_lo = tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f;  // positions with (pos & 2) == 0
-        const float beta_hi = tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float sc = pair_half<Odd>(sw[k]), mn = pair_half<Odd>(mw[k]);
-            const _Float16 hk = static_cast<_Float16>(qv[k] * sc);
-            hi[k] = hk;
-            lo[k] = static_cast<_Float16>(fmaf(qv[k], sc, -static_cast<float>(hk)));
-            bsum = fmaf(qv[k], fmaf(-((k & 2) ? beta_hi : beta_lo), sc, mn), bsum);
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const _Float16 hk = static_cast<_Float16>(qv[k]);
-            hi[k] = hk;
-            lo[k] = static_cast<_Float16>(qv[k] - static_cast<float>(hk));
-        }
+    for (int k = 0; k < 8; ++k) {
+        const _Float16 sc = __builtin_bit_cast(half2v, sw[k])[Odd ? 1 : 0];
+        const _Float16 mn = __builtin_bit_cast(half2v, mw[k])[Odd ? 1 : 0];
+        const _Float16 hk = static_cast<_Float16>(fmaf(qv[k], static_cast<float>(sc), 0.f));
+        hi[k] = hk;
+        lo[k] = static_cast<_Float16>(fmaf(qv[k], static_cast<float>(sc), -static_cast<float>(hk)));
+        // positions with (k & 2) == 0 unpack under beta_lo, the others under beta_hi
+        const float mp = fmaf((k & 2) ? -beta_hi : -beta_lo, static_cast<float>(sc), static_cast<float>(mn));
+        bsum = fmaf(qv[k], mp, bsum);
     }
-    qs[gb * 16 + n] = hi;
-    qs[gb * 16 + 8 + n] = lo;
+    *qs_hi = hi;
+    *qs_lo = lo;
     return bsum;
 }
 
@@ -274,18 +280,49 @@ __device__ __forceinline__ float half_wave_sum(float x) {
     return x;
 }
 
+// Max / sum of x over the four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48), in every lane:
+// v_permlane16_swap pairs rows (0, 1), (2, 3); v_permlane32_swap pairs the wave halves.  Both
+// swapped registers pass through an empty asm: this compiler otherwise takes the two results
+// of a swap to be equal and drops the second.
+template <bool Half32>
+__device__ __forceinline__ void swap_rows(float x, float& a, float& b) {
+    const int xi = __builtin_bit_cast(int, x);
+    const auto r = Half32 ? __builtin_amdgcn_permlane32_swap(xi, xi, false, false)
+                          : __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+    int r0 = r[0], r1 = r[1];
+    asm volatile("" : "+v"(r0), "+v"(r1));
+    a = __builtin_bit_cast(float, r0);
+    b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    float a, b;
+    swap_rows<true>(x, a, b);
+    return a + b;
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    float a, b;
+    swap_rows<false>(x, a, b);
+    return halves_sum(a + b);
+}
+__device__ __forceinline__ float rows_max(float x) {
+    float a, b;
+    swap_rows<false>(x, a, b);
+    swap_rows<true>(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+
 // Per-lane DMA state.  A page is fetched as 16-byte chunks in two regions -- region A: the
 // Key-code rows K0, K1, K2; region B: Value scale, Value min, Value codes, fp16-tier rows --
 // plus one dword per Key scale/min slot (the fp16 pair of pages (p & ~1, p | 1)).  Block j
 // (64 chunks) of region A lands in the Key-code buffer at 1024 j, block j of region B in the
-// rest buffer at 1024 j; slot dwords follow region B at y.rawb_ks.  Wave w issues blocks
-// w, w + 4, ...; lanes past a region's last chunk are masked off.
+// rest buffer at 1024 j; slot dwords follow region B at rawb_ks.  Wave w issues blocks
+// w, w + 4, ...  Every lane of an issued instruction loads: lanes past a region's last chunk
+// re-read that chunk into the block padding of their buffer, lanes past the last slot re-read
+// a real slot into the slot area's padding.
 struct DmaSrc {
     const unsigned char* chunk[kMaxDma];
-    int chunk_stride[kMaxDma];  // bytes per page of the chunk's segment
-    int chunk_live;             // bit i: this lane's chunk of instruction i exists
+    uint32_t chunk_stride[kMaxDma];  // bytes per page of the chunk's segment
     const unsigned char* ks[kMaxKsDma];
-    int ks_live;                // bit i: this lane's slot of instruction i exists
     int n_chunk;                // 16-byte DMA instructions this wave issues per page
     int n_ks;                   // 4-byte slot DMA instructions this wave issues per page
     int per_page;               // DMA instructions this wave issues per page
@@ -297,17 +334,14 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
     const int na = y.seg_end[2];             // region A chunks
     const int nb_chunks = y.n_chunks - na;   // region B chunks
     s.n_chunk = 0;
-    s.chunk_live = 0;
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
         const int j = kWaves * i + wave;
         if (j < y.ja + y.jb) s.n_chunk = i + 1;
-        const int c = j < y.ja ? 64 * j + lane : 64 * (j - y.ja) + lane;  // chunk within its region
-        const bool live = j < y.ja ? c < na : (j < y.ja + y.jb && c < nb_chunks);
-        if (live) s.chunk_live |= 1 << i;
         const unsigned char* src = reinterpret_cast<const unsigned char*>(L.k_code[0]);
-        int stride = 0;
-        if (live && j < y.ja) {
+        uint32_t stride = 0;
+        if (j < y.ja) {
+            const int c = min(64 * j + lane, na - 1);
             if (c < y.seg_end[0]) {
                 src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]) + 16 * c;
                 stride = kPage * L.k_words[0] * 4;
@@ -318,8 +352,9 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
                 src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]) + 16 * (c - y.seg_end[1]);
                 stride = kPage * L.k_words[2] * 4;
             }
-        } else if (live) {
+        } else if (j < y.ja + y.jb) {
             // region B: v scale (16 chunks), v min (16), v codes (256), fp16-tier rows
+            const int c = min(64 * (j - y.ja) + lane, nb_chunks - 1);
             if (c < 16) {
                 src = reinterpret_cast<const unsigned char*>(L.v_scale + row0) + 16 * c;
                 stride = kPage * 2;
@@ -337,9 +372,9 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
         s.chunk[i] = src;
         s.chunk_stride[i] = stride;
     }
-    // Key scale/min slots.  Padding slots read slot 0 of the first integer tier (their q is zero).
+    // Key scale/min slots.  Padding slots, and lanes past the last slot, read slot 0 of the
+    // first integer tier (the padding slots' q is zero).
     s.n_ks = 0;
-    s.ks_live = 0;
     const int t0 = L.k_width[0] ? 0 : L.k_width[1] ? 1 : 2;
     const unsigned char* dummy = reinterpret_cast<const unsigned char*>(
         sel3(L.k_scale, t0) + kgrp_idx(L, b, h, sel4(L.k_width, t0), 0, pbeg & ~1));
@@ -350,7 +385,6 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
         const int e = e0 + lane;
         const unsigned char* src = dummy;
         if (e < y.n_kslots) {
-            s.ks_live |= 1 << i;
             const bool is_min = e >= y.n_kslots / 2;
             const int slot = is_min ? e - y.n_kslots / 2 : e;
             const int gb = slot >> 3, pos = slot & 7;
@@ -373,35 +407,34 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
 // Issue the DMA of page ``page``: region A into the Key-code buffer at LDS address ``rawa``,
 // region B and the slots into the rest buffer at ``rawb`` (32-bit LDS addresses); advance
 // the sources one page.
-__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t rawa, uint32_t rawb, const MfmaLayout& y, int page,
+__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t rawa, uint32_t rawb, const LoopY& z, int page,
                                          int wave) {
     // The per-instruction conditions and addresses are cheap scalar work; passing their inputs
     // through an empty asm keeps the compiler from hoisting one register per instruction out
     // of the page loop (which would exhaust the scalar registers).
-    int n_chunk = s.n_chunk, n_ks = s.n_ks, ja = y.ja, jw = wave;
-    int chunk_live = s.chunk_live, ks_live = s.ks_live;
+    int n_chunk = s.n_chunk, n_ks = s.n_ks, ja = z.ja, jw = wave;
     asm volatile("" : "+s"(n_chunk), "+s"(n_ks), "+s"(ja), "+s"(jw));
-    asm volatile("" : "+v"(chunk_live), "+v"(ks_live));
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
         if (i < n_chunk) {
             const int j = kWaves * i + jw;
             const uint32_t dst = j < ja ? rawa + 1024 * j : rawb + 1024 * (j - ja);
-            if (chunk_live & (1 << i)) dma16(s.chunk[i], dst);
+            dma16(s.chunk[i], dst);
             s.chunk[i] += s.chunk_stride[i];
         }
     }
+    const uint32_t ksd = rawb + z.rawb_ks + jw * 256;
 #pragma unroll
     for (int i = 0; i < kMaxKsDma; ++i) {
         if (i < n_ks) {
-            if (ks_live & (1 << i)) dma4(s.ks[i], rawb + y.rawb_ks + (kWaves * i + jw) * 256);
+            dma4(s.ks[i], ksd + kWaves * 256 * i);
             if (page & 1) s.ks[i] += 4;
         }
     }
 }
 
 // Prepare page ``page`` from rest buffer ``raw`` into prepared buffer ``ck`` (all threads).
-__device__ __forceinline__ void prepare_page(const MfmaLayout& y, const unsigned char* raw, unsigned char* ck,
+__device__ __forceinline__ void prepare_page(const LoopY& z, const unsigned char* raw, unsigned char* ck,
                                              const float* qperm, int page, int g, int w16, int tid) {
     const int lane = tid & 63;
     {
@@ -410,7 +443,7 @@ __device__ __forceinline__ void prepare_page(const MfmaLayout& y, const unsigned
         const uint32_t* vc = reinterpret_cast<const uint32_t*>(raw + kRawbVc) + 32 * tg + w;
         uint32_t o[4];
         byte_transpose4(vc[0], vc[8], vc[16], vc[24], o);
-        uint32_t* vt = reinterpret_cast<uint32_t*>(ck + y.ck_vt);
+        uint32_t* vt = reinterpret_cast<uint32_t*>(ck + kCkVt);
 #pragma unroll
         for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = o[k];
     }
@@ -421,10 +454,10 @@ __device__ __forceinline__ void prepare_page(const MfmaLayout& y, const unsigned
         const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + kRawbVs);
         const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + kRawbVm);
         const float s = f16_to_f32(vs[t]);
-        reinterpret_cast<float*>(ck + y.ck_vsc)[t] = s;
-        reinterpret_cast<float*>(ck + y.ck_vmid)[t] = fmaf(-4.f, s, f16_to_f32(vm[t]));
+        reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
+        reinterpret_cast<float*>(ck + kCkVmid)[t] = fmaf(-4.f, s, f16_to_f32(vm[t]));
         const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw + kRawbF16) + t * w16;
-        uint4* dst = reinterpret_cast<uint4*>(ck + y.ck_v16 + 2 * t * y.w16p);
+        uint4* dst = reinterpret_cast<uint4*>(ck + z.ck_v16 + 2 * t * z.w16p);
         for (int c0 = 0; c0 < w16; c0 += 8) {
             uint32_t v[8];
 #pragma unroll
@@ -432,21 +465,40 @@ __device__ __forceinline__ void prepare_page(const MfmaLayout& y, const unsigned
             dst[c0 >> 3] = uint4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
         }
     }
-    // Qs and the bias: thread (head tid / 32, blocks tid % 32 + 32 i); each head's bias is
-    // summed over its half wave
+    // Qs of the integer tiers and the bias: thread (head tid / 32, blocks tid % 32 + 32 i); each
+    // head's bias is summed over its half wave.  The fp16 tier's Qs (plain q) is set once.
     const int n = tid >> 5;
     float bsum = 0.f;
     if (n < g) {
-        const uint32_t* ksr = reinterpret_cast<const uint32_t*>(raw + y.rawb_ks);
-        half8* qs = reinterpret_cast<half8*>(ck + y.ck_qs);
-        if (page & 1) {
-            for (int gb = tid & 31; gb < y.nb; gb += 32) bsum += qs_block<true>(qperm, ksr, qs, y, gb, n);
-        } else {
-            for (int gb = tid & 31; gb < y.nb; gb += 32) bsum += qs_block<false>(qperm, ksr, qs, y, gb, n);
+        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
+        const uint32_t* kmn = ksc + z.n_kslots / 2;
+        half8* qs = reinterpret_cast<half8*>(ck + kCkQs);
+        for (int gb = tid & 31; gb < z.nb_int; gb += 32) {
+            const int tier = gb >= 4 * z.kf2 ? 2 : gb >= 4 * z.kf1 ? 1 : 0;
+            const float beta_lo = tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f;
+            const float beta_hi = tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f;
+            const float* qrow = qperm + (gb * 8 + n) * 8;
+            if (page & 1)
+                bsum += qs_block<true>(qrow, ksc + gb * 8, kmn + gb * 8, qs + gb * 16 + n, qs + gb * 16 + 8 + n,
+                                       beta_lo, beta_hi);
+            else
+                bsum += qs_block<false>(qrow, ksc + gb * 8, kmn + gb * 8, qs + gb * 16 + n, qs + gb * 16 + 8 + n,
+                                        beta_lo, beta_hi);
         }
     }
     bsum = half_wave_sum(bsum);
-    if ((lane & 31) == 31) reinterpret_cast<float*>(ck + y.ck_bias)[n] = bsum;
+    if ((lane & 31) == 31) reinterpret_cast<float*>(ck + kCkBias)[n] = bsum;
+}
+
+// q of the workgroup's heads, scaled into the log2 domain, into qlin [8][128] (0 for heads >= g).
+__device__ __forceinline__ void load_q(const DecodeParams& p, int b, int h, float* qlin, int tid) {
+    const lf_decode_args& A = p.A;
+    for (int e = tid; e < 8 * kD; e += kThreads) {
+        const int n = e / kD, c = e % kD;
+        qlin[e] = n < p.g ? load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * p.g + n) * kD + c, A.q_dtype) *
+                                p.qscale
+                          : 0.f;
+    }
 }
 
 __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
@@ -473,30 +525,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     float* small = reinterpret_cast<float*>(smem + y.off_small);
     float* alpha_lds = small;              // [waves][8]: softmax rescale per head
     float* wstat = small + kWaves * 8;     // [waves][3][8]: m, l, mid per head
-    // Aliases of the prepared + raw buffers (free outside the page loop): q [8][128], wave
-    // outputs [waves][8][128], residual probabilities [waves][32][8].
+    // Aliases of the prepared + raw buffers (free outside the page loop): q [8][128] (the first
+    // 4 KB of prepared buffer 0, below its Qs rows), wave outputs [waves][8][128], residual
+    // probabilities [waves][32][8].
     float* qlin = reinterpret_cast<float*>(smem + y.off_ck);
     float* red = qlin + 8 * kD;
     float* pbuf = red + kWaves * 8 * kD;
-
-    // ---- q (scaled into the log2 domain) and this head's tier table ----
-    int16_t* tt = reinterpret_cast<int16_t*>(smem + y.off_tt);
-    int tt_off[4];
-    tt_off[0] = 0;
-    for (int t = 1; t < 4; ++t) tt_off[t] = tt_off[t - 1] + L.k_width[t - 1];
-    for (int e = tid; e < 8 * kD; e += kThreads) {
-        const int n = e / kD, c = e % kD;
-        qlin[e] = n < g ? load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD + c, A.q_dtype) *
-                              p.qscale
-                        : 0.f;
-    }
-    for (int e = tid; e < tt_off[3] + L.k_width[3]; e += kThreads) {
-        const int t = e >= tt_off[3] ? 3 : e >= tt_off[2] ? 2 : e >= tt_off[1] ? 1 : 0;
-        const int j = e - sel4(tt_off, t);
-        tt[e] = j < sel4(L.tier_count, t)[h] ? static_cast<int16_t>(sel4(L.tier_index, t)[h * sel4(L.k_width, t) + j])
-                                             : int16_t(-1);
-    }
-    __syncthreads();
 
     float O[8][4];
 #pragma unroll
@@ -506,7 +540,35 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     float m_run = -__builtin_inff(), l_run = 0.f, mid_run = 0.f;
 
     if (kind == 0) {
-        // q permuted into slot order (0 for padding slots and heads >= g)
+        // The first two pages' DMA goes out first; q, the tier table and the permuted q are
+        // built while it is in flight (the DMA targets do not overlap q).
+        const LoopY z = loop_y(y);
+        DmaSrc ds;
+        dma_setup(ds, L, y, b, h, pbeg, wave, lane);
+        unsigned char* rawa0 = smem + y.off_rawa;
+        unsigned char* rawb0 = smem + y.off_rawb;
+        unsigned char* ck0 = smem + y.off_ck;
+        const uint32_t lds0 = lds_addr(smem);  // LDS address of smem
+        const uint32_t rawa_lds = lds0 + y.off_rawa, rawb_lds = lds0 + y.off_rawb;
+        dma_page(ds, rawa_lds, rawb_lds, z, pbeg, wave);
+        if (pbeg + 1 < pend) dma_page(ds, rawa_lds + z.rawa_bytes, rawb_lds + z.rawb_bytes, z, pbeg + 1, wave);
+
+        // ---- q (scaled into the log2 domain) and this head's tier table ----
+        int16_t* tt = reinterpret_cast<int16_t*>(smem + y.off_tt);
+        int tt_off[4];
+        tt_off[0] = 0;
+        for (int t = 1; t < 4; ++t) tt_off[t] = tt_off[t - 1] + L.k_width[t - 1];
+        load_q(p, b, h, qlin, tid);
+        for (int e = tid; e < tt_off[3] + L.k_width[3]; e += kThreads) {
+            const int t = e >= tt_off[3] ? 3 : e >= tt_off[2] ? 2 : e >= tt_off[1] ? 1 : 0;
+            const int j = e - sel4(tt_off, t);
+            tt[e] = j < sel4(L.tier_count, t)[h] ? static_cast<int16_t>(sel4(L.tier_index, t)[h * sel4(L.k_width, t) + j])
+                                                 : int16_t(-1);
+        }
+        __syncthreads();
+        // q permuted into slot order (0 for padding slots and heads >= g).  The fp16 tier's Qs
+        // is this q (hi / lo) on every page: set once in both prepared buffers, as are the zero
+        // Qs rows of heads >= g in the integer tiers.
         for (int e = tid; e < y.nb * 64; e += kThreads) {
             const int gb = e >> 6, n = (e >> 3) & 7, pos = e & 7;
             const int tier = gb >= 4 * y.kfirst[3] ? 3 : gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
@@ -520,26 +582,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 }
             }
             qperm[e] = v;
+            if (gb >= y.nb_int || n >= g) {
+                const _Float16 hv = static_cast<_Float16>(v);
+                const _Float16 lv = static_cast<_Float16>(v - static_cast<float>(hv));
+#pragma unroll
+                for (int buf = 0; buf < 2; ++buf) {
+                    _Float16* qs = reinterpret_cast<_Float16*>(ck0 + buf * y.ck_bytes + kCkQs);
+                    qs[(gb * 16 + n) * 8 + pos] = hv;
+                    qs[(gb * 16 + 8 + n) * 8 + pos] = lv;
+                }
+            }
         }
-        __syncthreads();  // qlin (aliased by the buffers) is dead from here on
-        // Qs rows of heads >= g are never written by the preparation: zero them in both buffers.
-        for (int e = tid; e < 2 * y.nb * 16; e += kThreads) {
-            const int buf = e / (y.nb * 16), r = e % (y.nb * 16);
-            if ((r & 7) >= g) reinterpret_cast<half8*>(smem + y.off_ck + buf * y.ck_bytes + y.ck_qs)[r] = half8{};
-        }
-
-        DmaSrc ds;
-        dma_setup(ds, L, y, b, h, pbeg, wave, lane);
-        unsigned char* rawa0 = smem + y.off_rawa;
-        unsigned char* rawb0 = smem + y.off_rawb;
-        unsigned char* ck0 = smem + y.off_ck;
-        const uint32_t lds0 = lds_addr(smem);  // LDS address of smem
-        const uint32_t rawa_lds = lds0 + y.off_rawa, rawb_lds = lds0 + y.off_rawb;
+        __syncthreads();  // qlin (aliased by prepared buffer 0) is dead from here on
         const int w16 = L.k_width[3];
-        dma_page(ds, rawa_lds, rawb_lds, y, pbeg, wave);
-        if (pbeg + 1 < pend) dma_page(ds, rawa_lds + y.rawa_bytes, rawb_lds + y.rawb_bytes, y, pbeg + 1, wave);
         dma_barrier(pbeg + 1 < pend ? ds.per_page : 0);  // page pbeg landed (every wave's share)
-        prepare_page(y, rawb0, ck0, qperm, pbeg, g, w16, tid);
+        prepare_page(z, rawb0, ck0, qperm, pbeg, g, w16, tid);
 
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
         const int sh = 2 * (n16 & 3);
@@ -550,22 +607,22 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             // prepared buffer are free, and page's rest buffer was consumed by its preparation.
             dma_barrier(0);
             if (page + 2 < pend)
-                dma_page(ds, rawa_lds + ((rel + 2) % 3) * y.rawa_bytes, rawb_lds + (rel & 1) * y.rawb_bytes, y, page + 2,
+                dma_page(ds, rawa_lds + ((rel + 2) % 3) * z.rawa_bytes, rawb_lds + (rel & 1) * z.rawb_bytes, z, page + 2,
                          wave);
             if (page + 1 < pend)
-                prepare_page(y, rawb0 + ((rel + 1) & 1) * y.rawb_bytes, ck0 + ((rel + 1) & 1) * y.ck_bytes, qperm,
+                prepare_page(z, rawb0 + ((rel + 1) & 1) * z.rawb_bytes, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm,
                              page + 1, g, w16, tid);
 
             // ---- compute page ``page`` from its prepared buffer and Key codes ----
-            const unsigned char* raw = rawa0 + (rel % 3) * y.rawa_bytes;
-            const unsigned char* ck = ck0 + (rel & 1) * y.ck_bytes;
-            const half8* qs = reinterpret_cast<const half8*>(ck + y.ck_qs);
+            const unsigned char* raw = rawa0 + (rel % 3) * z.rawa_bytes;
+            const unsigned char* ck = ck0 + (rel & 1) * z.ck_bytes;
+            const half8* qs = reinterpret_cast<const half8*>(ck + kCkQs);
             // Integer tiers read up to 7 dwords past their segment (inside the LDS allocation):
             // those blocks have Qs == 0 and unpack to finite values.
             float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
             {
                 const uint32_t* k0 = reinterpret_cast<const uint32_t*>(raw);
-                for (int s2 = 0; s2 < y.kst[0] / 2; ++s2) {
+                for (int s2 = 0; s2 < z.kst0 / 2; ++s2) {
                     const uint32_t wa = k0[tok0 * kw0 + 4 * s2 + kb];
                     const uint32_t wb = k0[tok1 * kw0 + 4 * s2 + kb];
                     const half8 bq0 = qs[(8 * s2 + kb) * 16 + n16];
@@ -575,28 +632,28 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wa, kv), bq1, acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wb, kv), bq1, acc1, 0, 0, 0);
                 }
-                const uint32_t* k1 = reinterpret_cast<const uint32_t*>(raw + 16 * y.seg_end[0]);
-                for (int s = 0; s < y.kst[1]; ++s) {
-                    const half8 bq = qs[(4 * (y.kfirst[1] + s) + kb) * 16 + n16];
+                const uint32_t* k1 = reinterpret_cast<const uint32_t*>(raw + 16 * z.seg0);
+                for (int s = 0; s < z.kst1; ++s) {
+                    const half8 bq = qs[(4 * (z.kst0 + s) + kb) * 16 + n16];
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok0 * kw1 + 4 * s + kb], kv), bq, acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok1 * kw1 + 4 * s + kb], kv), bq, acc1, 0, 0, 0);
                 }
-                const uint32_t* k2 = reinterpret_cast<const uint32_t*>(raw + 16 * y.seg_end[1]);
-                for (int s = 0; s < y.kst[2]; ++s) {
+                const uint32_t* k2 = reinterpret_cast<const uint32_t*>(raw + 16 * z.seg1);
+                for (int s = 0; s < z.kst2; ++s) {
                     const int w0 = 2 * (4 * s + kb);
-                    const half8 bq = qs[(4 * (y.kfirst[2] + s) + kb) * 16 + n16];
+                    const half8 bq = qs[(4 * (z.kf2 + s) + kb) * 16 + n16];
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok0 * kw2 + w0], k2[tok0 * kw2 + w0 + 1]), bq,
                                                                   acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok1 * kw2 + w0], k2[tok1 * kw2 + w0 + 1]), bq,
                                                                   acc1, 0, 0, 0);
                 }
-                const unsigned char* v16 = ck + y.ck_v16;
-                for (int s = 0; s < y.kst[3]; ++s) {
+                const unsigned char* v16 = ck + z.ck_v16;
+                for (int s = 0; s < z.kst3; ++s) {
                     const int col = 8 * (4 * s + kb);
-                    const bool ok = col < y.w16p;
-                    const uint4 ua = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok0 * y.w16p + col)) : uint4{0, 0, 0, 0};
-                    const uint4 ub = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok1 * y.w16p + col)) : uint4{0, 0, 0, 0};
-                    const half8 bq = qs[(4 * (y.kfirst[3] + s) + kb) * 16 + n16];
+                    const bool ok = col < z.w16p;
+                    const uint4 ua = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok0 * z.w16p + col)) : uint4{0, 0, 0, 0};
+                    const uint4 ub = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok1 * z.w16p + col)) : uint4{0, 0, 0, 0};
+                    const half8 bq = qs[(4 * (z.kf3 + s) + kb) * 16 + n16];
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ua), bq, acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ub), bq, acc1, 0, 0, 0);
                 }
@@ -612,18 +669,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
             }
             // ---- online softmax (log2 domain) ----
-            const float bias = (n16 < 8) ? reinterpret_cast<const float*>(ck + y.ck_bias)[n16] : 0.f;
+            const float bias = (n16 < 8) ? reinterpret_cast<const float*>(ck + kCkBias)[n16] : 0.f;
             float mx = sv[0];
 #pragma unroll
             for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            mx = rows_max(mx);
             const float m_new = fmaxf(m_run, mx + bias);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             const float m_off = m_new - bias;  // p = 2^(sv + bias - m_new)
             m_run = m_new;
-            const float* vsc = reinterpret_cast<const float*>(ck + y.ck_vsc);
-            const float* vmd = reinterpret_cast<const float*>(ck + y.ck_vmid);
+            const float* vsc = reinterpret_cast<const float*>(ck + kCkVsc);
+            const float* vmd = reinterpret_cast<const float*>(ck + kCkVmid);
             const float4 s_lo = *reinterpret_cast<const float4*>(vsc + 32 * wave + 4 * kb);
             const float4 s_hi = *reinterpret_cast<const float4*>(vsc + 32 * wave + 16 + 4 * kb);
             const float4 d_lo = *reinterpret_cast<const float4*>(vmd + 32 * wave + 4 * kb);
@@ -677,7 +733,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 }
             }
             // ---- value product: codes of the lane's 8 tokens, channel 16*nt + n16 ----
-            const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + y.ck_vt);
+            const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + kCkVt);
             const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
             const uint4 d0b = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8 + 4);
             const uint4 d1a = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8);
@@ -699,15 +755,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             }
         }
         // Reduce l and the midpoint term over the 4 lane groups of each head.
-        l_run += __shfl_xor(l_run, 16, kWave);
-        l_run += __shfl_xor(l_run, 32, kWave);
-        mid_run += __shfl_xor(mid_run, 16, kWave);
-        mid_run += __shfl_xor(mid_run, 32, kWave);
+        l_run = rows_sum(l_run);
+        mid_run = rows_sum(mid_run);
         // Rows r (hi, lanes kb 0..1) + rows r+8 (lo, lanes kb 2..3).
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) O[nt][r] += __shfl_xor(O[nt][r], 32, kWave);
+            for (int r = 0; r < 4; ++r) O[nt][r] = halves_sum(O[nt][r]);
         __syncthreads();  // every wave is done with the buffers that ``red`` aliases
         if (kb < 2) {
 #pragma unroll
@@ -727,6 +781,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         // q read as float4 from LDS), then accumulates them into channels 2*lane, 2*lane+1.
         // One pass, so each wave's max is final.  Every global load of a phase is issued
         // before its first use.
+        load_q(p, b, h, qlin, tid);
+        __syncthreads();
         const int tl = A.tail_len[b];
         const int n_res = tl + (A.k_new != nullptr ? 1 : 0);
         const int t = 32 * wave + (lane & 31);
@@ -923,28 +979,15 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     if (y.ja + y.jb > kMaxDma * kWaves) return false;
     y.n_kslots = 2 * y.nb_int * 8;
     if (y.n_kslots > kMaxKsDma * kWaves * 64) return false;
-    // Key-code buffer: the K0, K1, K2 rows; rest buffer: fp16 tier, v scale, v min, Value codes,
-    // Key scale/min (DMA lanes past the last chunk of a region do not write)
-    y.rawa_bytes = round_up(16 * y.seg_end[2], 16);
-    int rb = kRawbF16 + kPage * L.k_width[3] * 2;
-    y.rawb_ks = round_up(rb, 16);
-    rb = y.rawb_ks + ((y.n_kslots + 63) / 64) * 256;
-    y.rawb_bytes = round_up(rb, 16);
-    int ck = 0;
-    y.ck_qs = ck;
-    ck += y.nb * 16 * 16;
-    y.ck_vt = ck;
-    ck += 32 * 36 * 4;
-    y.ck_v16 = ck;
-    ck += kPage * y.w16p * 2;
-    ck = round_up(ck, 16);
-    y.ck_vsc = ck;
-    ck += kPage * 4;
-    y.ck_vmid = ck;
-    ck += kPage * 4;
-    y.ck_bias = ck;
-    ck += 8 * 4;
-    y.ck_bytes = round_up(ck, 16);
+    // Key-code buffer: the K0, K1, K2 rows; rest buffer: v scale, v min, Value codes, fp16 tier,
+    // then the Key scale/min slots.  Every lane of a DMA instruction writes, so both regions are
+    // padded to whole 64-chunk blocks (1024 bytes) and the slot area to whole 64-slot blocks.
+    y.rawa_bytes = 1024 * y.ja;
+    y.rawb_ks = 1024 * y.jb;
+    y.rawb_bytes = y.rawb_ks + ((y.n_kslots + 63) / 64) * 256;
+    // prepared buffer: fixed-offset parts, Qs [nb][16][8] fp16 at kCkQs, fp16-tier rows after it
+    y.ck_v16 = kCkQs + y.nb * 16 * 16;
+    y.ck_bytes = round_up(y.ck_v16 + kPage * y.w16p * 2, 16);
     int off = 0;
     y.off_qperm = off;
     off += y.nb * 64 * 4;
