@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 2
+#define LF_ABI_VERSION 3
 
 /* Element types of query / residual / output tensors. */
 enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
@@ -103,16 +103,19 @@ int32_t lf_pack_pages(const lf_packed_layer* layer,
                       const int32_t* jobs, int32_t n_jobs, void* stream);
 
 /*
- * Decode work plan (host function, no device access).  Items 0..batch-1 are
- * the residual items (b, 0, 0, 1) of sequence b (tail page + new token); then
- * each sequence's ``hist_pages[b]`` packed pages follow as items of at most
- * ``pages_per_split`` pages (b, page_begin, page_end, 0).  Writes
- * ``work_out`` [n][4] and ``seq_work_out`` [batch][2] = (first page item,
- * page item count) of each sequence.  Returns the item count n, or a
+ * Decode work plan (host function, no device access).  Sequence b's work is
+ * its residual -- the BF16 tail page plus the new token, costed as
+ * ``residual_pages`` pages -- and its ``hist_pages[b]`` packed pages.  It is
+ * cut into ceil((hist_pages[b] + residual_pages) / pages_per_split) items of
+ * equal work, (b, page_begin, page_end, kind): the first item (kind 2, or 1
+ * when it holds no page) covers the residual and the pages left in its share,
+ * the others (kind 0) pages only.  Writes ``work_out`` [n][4] and
+ * ``seq_work_out`` [batch][2] = (first item, item count) of each sequence;
+ * a sequence's items are consecutive.  Returns the item count n, or a
  * negative LF_E_* when ``work_cap`` is too small.  Both arrays must be copied
  * to the device before lf_decode_attention.
  */
-int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split,
+int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split, int32_t residual_pages,
                        int32_t* work_out, int32_t work_cap, int32_t* seq_work_out);
 
 /* Decode-attention call arguments (see lf_decode_attention). */

@@ -85,7 +85,7 @@ _SIGNATURES = {
     "lf_status_string": (c_char_p, [c_int32]),
     "lf_pack_pages": (c_int32, [POINTER(PackedLayer), c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64,
                                 c_void_p, c_int32, c_void_p]),
-    "lf_plan_decode": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
+    "lf_plan_decode": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "lf_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "lf_decode_attention": (c_int32, [POINTER(PackedLayer), POINTER(DecodeArgs), c_void_p]),
     "lf_dequantize": (c_int32, [POINTER(PackedLayer), c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
@@ -95,7 +95,7 @@ _SIGNATURES = {
                                   c_void_p]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _LIB = None
 
 

@@ -97,31 +97,30 @@ int32_t lf_pack_pages(const lf_packed_layer* layer, const void* k_src, const voi
                                  jobs, n_jobs, static_cast<hipStream_t>(stream));
 }
 
-int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split,
+int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split, int32_t residual_pages,
                        int32_t* work_out, int32_t work_cap, int32_t* seq_work_out) {
     if (!hist_pages || !work_out || !seq_work_out) return LF_E_NULL;
-    if (batch <= 0 || pages_per_split <= 0) return LF_E_SHAPE;
-    if (work_cap < batch) return LF_E_WORKSPACE;
-    // Residual items first (one per sequence): they are short but latency-bound, so they are
-    // dispatched before the page items rather than at the tail of the grid.
-    for (int32_t b = 0; b < batch; ++b) {
-        if (hist_pages[b] < 0) return LF_E_SHAPE;
-        work_out[4 * b + 0] = b;
-        work_out[4 * b + 1] = 0;
-        work_out[4 * b + 2] = 0;
-        work_out[4 * b + 3] = 1;
-    }
-    int32_t n = batch;
+    if (batch <= 0 || pages_per_split <= 0 || residual_pages < 0) return LF_E_SHAPE;
+    // Sequence b's work is its residual (tail page + new token), costed as ``residual_pages``
+    // pages, followed by its packed pages.  It is cut into ceil(work / pages_per_split) items
+    // of equal work; the first item takes the residual and the pages left in its share.
+    int32_t n = 0;
     for (int32_t b = 0; b < batch; ++b) {
         const int32_t pages = hist_pages[b];
+        if (pages < 0) return LF_E_SHAPE;
         const int32_t first = n;
-        for (int32_t p0 = 0; p0 < pages; p0 += pages_per_split) {
+        const int64_t work = static_cast<int64_t>(pages) + residual_pages;
+        const int64_t items = pages == 0 ? 1 : (work + pages_per_split - 1) / pages_per_split;
+        for (int64_t k = 0; k < items; ++k) {
+            const int64_t w0 = k * work / items, w1 = (k + 1) * work / items;
+            const int32_t p0 = static_cast<int32_t>(w0 > residual_pages ? w0 - residual_pages : 0);
+            const int32_t p1 = static_cast<int32_t>(w1 > residual_pages ? w1 - residual_pages : 0);
+            if (k > 0 && p1 == p0) continue;
             if (n >= work_cap) return LF_E_WORKSPACE;
-            const int32_t p1 = p0 + pages_per_split < pages ? p0 + pages_per_split : pages;
             work_out[4 * n + 0] = b;
             work_out[4 * n + 1] = p0;
             work_out[4 * n + 2] = p1;
-            work_out[4 * n + 3] = 0;
+            work_out[4 * n + 3] = k > 0 ? 0 : p1 > p0 ? 2 : 1;
             ++n;
         }
         seq_work_out[2 * b + 0] = first;

@@ -52,6 +52,7 @@ constexpr int kD = 128;
 constexpr int kPage = 128;
 constexpr int kMaxDma = 8;    // 16-byte DMA instructions per wave per page (<= 2048 chunks)
 constexpr int kMaxKsDma = 4;  // 4-byte Key scale/min DMA instructions per wave per page
+constexpr float kLazyRescale = 8.f;  // log2-domain headroom before the running max moves
 constexpr int kRawbVs = 0;    // rest buffer: Value scale [128] fp16
 constexpr int kRawbVm = 256;  //              Value min [128] fp16
 constexpr int kRawbVc = 512;  //              Value codes [128][8] u32
@@ -524,13 +525,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     float* qperm = reinterpret_cast<float*>(smem + y.off_qperm);
     float* small = reinterpret_cast<float*>(smem + y.off_small);
     float* alpha_lds = small;              // [waves][8]: softmax rescale per head
-    float* wstat = small + kWaves * 8;     // [waves][3][8]: m, l, mid per head
+    // Wave partials: slots 0..3 the pages (waves 0..3), slots 4..7 the residual of an item that
+    // has both (kind 2; a residual-only item uses slots 0..3).
+    float* wstat = small + kWaves * 8;     // [2 * waves][3][8]: m, l, mid per head
     // Aliases of the prepared + raw buffers (free outside the page loop): q [8][128] (the first
-    // 4 KB of prepared buffer 0, below its Qs rows), wave outputs [waves][8][128], residual
-    // probabilities [waves][32][8].
+    // 4 KB of prepared buffer 0, below its Qs rows), wave partial outputs [2 * waves][8][128],
+    // residual probabilities [waves][32][8].
     float* qlin = reinterpret_cast<float*>(smem + y.off_ck);
     float* red = qlin + 8 * kD;
-    float* pbuf = red + kWaves * 8 * kD;
+    float* pbuf = red + 2 * kWaves * 8 * kD;
 
     float O[8][4];
 #pragma unroll
@@ -539,7 +542,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         for (int r = 0; r < 4; ++r) O[nt][r] = 0.f;
     float m_run = -__builtin_inff(), l_run = 0.f, mid_run = 0.f;
 
-    if (kind == 0) {
+    if (kind != 1) {
+        // ---- pages (kind 0, 2) ----
         // The first two pages' DMA goes out first; q, the tier table and the permuted q are
         // built while it is in flight (the DMA targets do not overlap q).
         const LoopY z = loop_y(y);
@@ -674,10 +678,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
 #pragma unroll
             for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
             mx = rows_max(mx);
-            const float m_new = fmaxf(m_run, mx + bias);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            // The reference point m_run moves only when the page's max exceeds it by more than
+            // kLazyRescale (probabilities stay below 2^kLazyRescale), so most pages skip the
+            // rescale of O and l.
+            const float m_cand = mx + bias;
+            const bool grow = m_cand > m_run + kLazyRescale;
+            const float m_new = grow ? m_cand : m_run;
             const float m_off = m_new - bias;  // p = 2^(sv + bias - m_new)
-            m_run = m_new;
             const float* vsc = reinterpret_cast<const float*>(ck + kCkVsc);
             const float* vmd = reinterpret_cast<const float*>(ck + kCkVmid);
             const float4 s_lo = *reinterpret_cast<const float4*>(vsc + 32 * wave + 4 * kb);
@@ -695,8 +702,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 pmid = fmaf(pi, vd[i], pmid);
                 pp[i] = pi * vs[i];
             }
-            l_run = l_run * alpha + psum;
-            mid_run = mid_run * alpha + pmid;
             // A operand of the value product: k order (t0,t2),(t1,t3),(t4,t6),(t5,t7) of the
             // lane's tokens; hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8.
             uint32_t ahi[4], alo[4];
@@ -720,7 +725,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             // Rescale O when some head's max moved: alpha of the 4 output rows this lane holds
             // (rows 4*kb + r, head (4*kb + r) % 8); a same-wave LDS write then read is ordered
             // by the LDS queue.
-            if (__builtin_amdgcn_ballot_w64(n16 < 8 && alpha != 1.f)) {
+            if (__builtin_amdgcn_ballot_w64(n16 < 8 && grow)) {
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
+                mid_run *= alpha;
                 if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = alpha;
                 __builtin_amdgcn_wave_barrier();
                 const float4 arow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * (kb & 1));
@@ -732,6 +740,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     O[nt][3] *= arow.w;
                 }
             }
+            m_run = m_new;
+            l_run += psum;
+            mid_run += pmid;
             // ---- value product: codes of the lane's 8 tokens, channel 16*nt + n16 ----
             const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + kCkVt);
             const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
@@ -775,12 +786,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             wstat[(wave * 3 + 2) * 8 + n16] = mid_run;
         }
         __syncthreads();
-    } else {
-        // ---- residual item: the tail page and the new token (at most page_size tokens) ----
+    }
+    if (kind != 0) {
+        // ---- residual (kind 1, 2): the tail page and the new token (at most page_size tokens) ----
         // VALU: wave w scores tokens 32w..32w+31 (lane % 32 = token, lane / 32 = channel half;
         // q read as float4 from LDS), then accumulates them into channels 2*lane, 2*lane+1.
         // One pass, so each wave's max is final.  Every global load of a phase is issued
         // before its first use.
+        const int rw = kind == 2 ? wave + kWaves : wave;  // partial slot
         load_q(p, b, h, qlin, tid);
         __syncthreads();
         const int tl = A.tail_len[b];
@@ -850,9 +863,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         if (lane == 0) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                wstat[(wave * 3 + 0) * 8 + i] = mx[i];
-                wstat[(wave * 3 + 1) * 8 + i] = lt[i];
-                wstat[(wave * 3 + 2) * 8 + i] = 0.f;
+                wstat[(rw * 3 + 0) * 8 + i] = mx[i];
+                wstat[(rw * 3 + 1) * 8 + i] = lt[i];
+                wstat[(rw * 3 + 2) * 8 + i] = 0.f;
             }
         }
         __builtin_amdgcn_wave_barrier();
@@ -912,18 +925,19 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) red[(wave * 8 + i) * kD + 2 * lane + cc] = acc[cc][i];
+            for (int i = 0; i < 8; ++i) red[(rw * 8 + i) * kD + 2 * lane + cc] = acc[cc][i];
         __syncthreads();
     }
 
-    // ---- merge the waves and store this item's partial ----
+    // ---- merge the wave partials and store this item's partial ----
+    const int n_part = kind == 2 ? 2 * kWaves : kWaves;
     for (int e = tid; e < g * kD; e += kThreads) {
         const int i = e / kD, c = e % kD;
         float M = -__builtin_inff();
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wstat[(w * 3 + 0) * 8 + i]);
+        for (int w = 0; w < n_part; ++w) M = fmaxf(M, wstat[(w * 3 + 0) * 8 + i]);
         float o = 0.f, l = 0.f;
         if (M != -__builtin_inff()) {
-            for (int w = 0; w < kWaves; ++w) {
+            for (int w = 0; w < n_part; ++w) {
                 const float mw = wstat[(w * 3 + 0) * 8 + i];
                 const float sc = __builtin_amdgcn_exp2f(mw - M);
                 o += sc * (red[(w * 8 + i) * kD + c] + wstat[(w * 3 + 2) * 8 + i]);
@@ -994,7 +1008,7 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     y.off_tt = off;
     off += round_up(2 * (L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3]), 16);
     y.off_small = off;
-    off += kWaves * 32 * 4;
+    off += (kWaves * 8 + 2 * kWaves * 3 * 8) * 4;  // alpha, wave partial statistics
     off = round_up(off, 16);
     y.off_ck = off;
     off += 2 * y.ck_bytes;
@@ -1002,9 +1016,9 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     off += 3 * y.rawa_bytes;
     y.off_rawb = off;
     off += 2 * y.rawb_bytes;
-    // q [8][128], wave outputs [waves][8][128] and residual probabilities [waves][32][8] alias
-    // the prepared, Key-code and rest buffers
-    const int alias_bytes = (8 + kWaves * 8) * kD * 4 + kWaves * 32 * 8 * 4;
+    // q [8][128], wave partial outputs [2 * waves][8][128] and residual probabilities
+    // [waves][32][8] alias the prepared, Key-code and rest buffers
+    const int alias_bytes = (8 + 2 * kWaves * 8) * kD * 4 + kWaves * 32 * 8 * 4;
     if (off - y.off_ck < alias_bytes) off = y.off_ck + alias_bytes;
     y.lds_bytes = off;
     return y.lds_bytes <= 160 * 1024 - 64;

@@ -1,8 +1,8 @@
 // Cross-split softmax merge (flash-decoding reduce) of the decode partials.
 //
 // One workgroup per (sequence b, kv head h, local q head i), one thread per
-// channel.  The sequence's items are its residual item b and its page items
-// seq_work[b] = (first, count).  With M = max_k m_k over them and w_k = 2^(m_k - M):
+// channel.  The sequence's items are seq_work[b] = (first, count) (the first one also
+// covers the tail page and the new token).  With M = max_k m_k over them and w_k = 2^(m_k - M):
 //     out[b][h*g + i][c] = sum_k w_k o_k[c] / sum_k w_k l_k,
 // the merge of reference.py:44-56's single softmax over all tokens.  Items with
 // no tokens carry m = -inf and weigh nothing.
@@ -21,14 +21,14 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     const int i = blockIdx.x % g;
     const int h = (blockIdx.x / g) % p.L.n_kv;
     const int b = blockIdx.x / (g * p.L.n_kv);
-    const int first = p.A.seq_work[2 * b] - 1;  // item k > 0 is first + k; item 0 is the residual b
-    const int count = p.A.seq_work[2 * b + 1] + 1;
+    const int first = p.A.seq_work[2 * b];
+    const int count = p.A.seq_work[2 * b + 1];
     const int tid = threadIdx.x;
     const int nw = blockDim.x / kWave;
 
     // M = max over items
     float M = -__builtin_inff();
-    for (int k = tid; k < count; k += blockDim.x) M = fmaxf(M, part_rec(p, k ? first + k : b, h, i)[D]);
+    for (int k = tid; k < count; k += blockDim.x) M = fmaxf(M, part_rec(p, first + k, h, i)[D]);
     M = wave_max(M);
     if ((tid & (kWave - 1)) == 0) red[tid / kWave] = M;
     __syncthreads();
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     // weights (kept in LDS when they fit) and l = sum w_k l_k
     float l = 0.f;
     for (int k = tid; k < count; k += blockDim.x) {
-        const float* r = part_rec(p, k ? first + k : b, h, i);
+        const float* r = part_rec(p, first + k, h, i);
         const float wk = M == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(r[D] - M);
         if (k < kReduceLds) w[k] = wk;
         l += wk * r[D + 1];
@@ -52,9 +52,9 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     for (int c = tid; c < D; c += blockDim.x) {
         float o = 0.f;
 #pragma unroll 8
-        for (int k = 0; k < n_lds; ++k) o = fmaf(w[k], part_rec(p, k ? first + k : b, h, i)[c], o);
+        for (int k = 0; k < n_lds; ++k) o = fmaf(w[k], part_rec(p, first + k, h, i)[c], o);
         for (int k = n_lds; k < count; ++k) {
-            const float* r = part_rec(p, k ? first + k : b, h, i);
+            const float* r = part_rec(p, first + k, h, i);
             o = fmaf(__builtin_amdgcn_exp2f(r[D] - M), r[c], o);
         }
         const float val = l > 0.f ? o / l : 0.f;

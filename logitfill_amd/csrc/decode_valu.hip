@@ -91,7 +91,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
         }
     };
 
-    if (kind == 0) {
+    if (kind != 1) {  // pages (kind 0, 2)
         const int kg = L.k_group;
         const int chunk = kg < 64 ? kg : 64;
         const int vgs = L.v_groups;
@@ -193,8 +193,9 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
                 }
             }
         }
-    } else {
-        // Residual: the BF16 tail page then the new token (reference.py:35-44).
+    }
+    if (kind != 0) {
+        // Residual (kind 1, 2): the BF16 tail page then the new token (reference.py:35-44).
         const int tl = A.tail_len[b];
         const int has_new = A.k_new != nullptr;
         const int n_res = tl + has_new;

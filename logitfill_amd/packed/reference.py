@@ -94,33 +94,40 @@ def _cu_count(device) -> int:
     return _CU_COUNT[key]
 
 
-def choose_pages_per_split(total_page_heads: int, kernel: int, residual_items: int = 0, device=None) -> int:
-    """Pages per split-K item.  The decode kernel holds two workgroups per CU; splitting the
-    pages so that page items plus residual items fill those slots exactly once runs the
-    launch in a single round (measured on the 7B shape at 32K context: the single-round split
-    beats 16 and 32 pages per item)."""
+# Decode time of one sequence's residual (the BF16 tail page and the new token) in units of
+# packed pages, used to balance the split-K items (measured on the 7B shape: about 14 us
+# against 2.6 us per packed page and workgroup).
+RESIDUAL_PAGES = 5
+
+
+def choose_pages_per_split(hist_pages: list[int], n_kv: int, residual_pages: int = RESIDUAL_PAGES,
+                           device=None) -> int:
+    """Work per split-K item, in pages.  The decode kernel holds two workgroups per CU; items
+    of ``total work / slots`` pages (each sequence's work being its pages plus its residual)
+    fill those slots once, so the launch runs in a single round."""
     forced = env_int("LOGITFILL_AMD_PAGES_PER_SPLIT", 0)
     if forced > 0:
         return forced
     slots = 2 * (_cu_count(device) if device is not None else 256)
-    page_slots = max(slots - residual_items, slots // 2)
-    return max(1, math.ceil(total_page_heads / page_slots))
+    total = n_kv * sum(p + residual_pages for p in hist_pages)
+    return max(1, math.ceil(total / slots))
 
 
 class DecodePlan:
     """Device work list for one layer's current history lengths (rebuilt when they change)."""
 
-    def __init__(self, hist_pages: list[int], n_kv: int, pages_per_split: int, device):
+    def __init__(self, hist_pages: list[int], n_kv: int, pages_per_split: int, device,
+                 residual_pages: int = RESIDUAL_PAGES):
         lib = _native.load()
         batch = len(hist_pages)
-        cap = sum(-(-p // pages_per_split) for p in hist_pages) + batch
+        cap = sum(-(-(p + residual_pages) // pages_per_split) for p in hist_pages) + batch
         hp = (ctypes.c_int32 * batch)(*hist_pages)
         work = (ctypes.c_int32 * (4 * cap))()
         seq = (ctypes.c_int32 * (2 * batch))()
-        n = lib.lf_plan_decode(hp, batch, pages_per_split, work, cap, seq)
+        n = lib.lf_plan_decode(hp, batch, pages_per_split, residual_pages, work, cap, seq)
         if n < 0:
             _native.check(n, "lf_plan_decode")
-        self.key = (tuple(hist_pages), pages_per_split)
+        self.key = (tuple(hist_pages), pages_per_split, residual_pages)
         self.n_work = int(n)
         self.work = torch.tensor(list(work)[: 4 * n], dtype=torch.int32).to(device)
         self.seq_work = torch.tensor(list(seq), dtype=torch.int32).to(device)
@@ -160,10 +167,10 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     P = layer.page_size
     hist_pages = [h // P for h in layer.hist_lens]
     if pages_per_split is None:
-        pages_per_split = choose_pages_per_split(sum(hist_pages) * layer.n_kv, kernel, B * layer.n_kv, layer.device)
+        pages_per_split = choose_pages_per_split(hist_pages, layer.n_kv, RESIDUAL_PAGES, layer.device)
     plan = layer.decode_plan
-    if plan is None or plan.key != (tuple(hist_pages), pages_per_split):
-        plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device)
+    if plan is None or plan.key != (tuple(hist_pages), pages_per_split, RESIDUAL_PAGES):
+        plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device, RESIDUAL_PAGES)
         layer.decode_plan = plan
     lib = _native.load()
     nbytes = lib.lf_decode_workspace_bytes(manager.n_q, layer.head_dim, plan.n_work)

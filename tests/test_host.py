@@ -62,7 +62,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
         assert name in _native._SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.lf_abi_version() == 2
+    assert lib.lf_abi_version() == 3
     assert b"gfx950" in lib.lf_build_info()
 
 
@@ -90,19 +90,56 @@ def test_struct_layouts_match_c(tmp_path):
 
 
 def test_plan_decode_known_answer():
+    """Hand-derived plans: each sequence's work (residual + pages) cut into equal items, the
+    residual in the first item (kind 2, or 1 when that item holds no page)."""
     lib = _native.load()
     hp = (ctypes.c_int32 * 3)(5, 0, 2)
     work = (ctypes.c_int32 * 40)()
     seq = (ctypes.c_int32 * 6)()
-    n = lib.lf_plan_decode(hp, 3, 2, work, 10, seq)
-    assert n == 7
-    items = np.array(list(work)[:28]).reshape(7, 4).tolist()
-    assert items == [[0, 0, 0, 1], [1, 0, 0, 1], [2, 0, 0, 1],          # residual items first
-                     [0, 0, 2, 0], [0, 2, 4, 0], [0, 4, 5, 0],
-                     [2, 0, 2, 0]]
-    assert list(seq) == [3, 3, 6, 0, 6, 1]
-    assert lib.lf_plan_decode(hp, 3, 2, work, 6, seq) == -4          # LF_E_WORKSPACE
-    assert lib.lf_plan_decode(hp, 3, 0, work, 10, seq) == -2         # LF_E_SHAPE
+    n = lib.lf_plan_decode(hp, 3, 2, 1, work, 10, seq)
+    assert n == 6
+    items = np.array(list(work)[:24]).reshape(6, 4).tolist()
+    assert items == [[0, 0, 1, 2], [0, 1, 3, 0], [0, 3, 5, 0],   # work 6 -> 3 items of 2
+                     [1, 0, 0, 1],                               # no pages: residual only
+                     [2, 0, 0, 1], [2, 0, 2, 0]]                 # work 3 -> items of 1 and 2
+    assert list(seq) == [0, 3, 3, 1, 4, 2]
+    n = lib.lf_plan_decode(hp, 3, 2, 0, work, 10, seq)
+    assert n == 5
+    assert np.array(list(work)[:20]).reshape(5, 4).tolist() == [
+        [0, 0, 1, 2], [0, 1, 3, 0], [0, 3, 5, 0], [1, 0, 0, 1], [2, 0, 2, 2]]
+    assert list(seq) == [0, 3, 3, 1, 4, 1]
+    assert lib.lf_plan_decode(hp, 3, 2, 1, work, 5, seq) == -4       # LF_E_WORKSPACE
+    assert lib.lf_plan_decode(hp, 3, 0, 1, work, 10, seq) == -2      # LF_E_SHAPE
+    assert lib.lf_plan_decode(hp, 3, 2, -1, work, 10, seq) == -2     # LF_E_SHAPE
+
+
+@pytest.mark.parametrize("pps,res", [(1, 0), (3, 5), (7, 2), (32, 5), (33, 5)])
+def test_plan_decode_covers_pages(pps, res):
+    """Every page of every sequence lies in exactly one item, in order; items of a sequence
+    are consecutive; exactly its first item carries the residual; item work is balanced
+    to within one page."""
+    lib = _native.load()
+    pages = [0, 1, 7, 64, 256, 257, 3]
+    B = len(pages)
+    hp = (ctypes.c_int32 * B)(*pages)
+    cap = 4 * B + sum(pages)
+    work = (ctypes.c_int32 * (4 * cap))()
+    seq = (ctypes.c_int32 * (2 * B))()
+    n = lib.lf_plan_decode(hp, B, pps, res, work, cap, seq)
+    assert n > 0
+    items = np.array(list(work)[: 4 * n]).reshape(n, 4)
+    for b in range(B):
+        first, count = seq[2 * b], seq[2 * b + 1]
+        it = items[first:first + count]
+        assert (it[:, 0] == b).all()
+        assert it[0, 3] in (1, 2) and (it[1:, 3] == 0).all()
+        covered = np.concatenate([np.arange(p0, p1) for _, p0, p1, _ in it])
+        assert covered.tolist() == list(range(pages[b]))
+        if pages[b]:
+            assert count == -(-(pages[b] + res) // pps) or (it[:, 2] > it[:, 1]).sum() < count
+            w = (it[:, 2] - it[:, 1]) + np.where(it[:, 3] > 0, res, 0)
+            assert w.max() - w.min() <= 1 or res > w.min()
+    assert sum(seq[2 * b + 1] for b in range(B)) == n
 
 
 def test_workspace_layout():
