@@ -60,8 +60,8 @@ constexpr int kRawbF16 = 4608;  //            fp16-tier rows [128][width16]
 // Prepared buffer: fixed offsets first (they become immediate offsets of the LDS accesses).
 constexpr int kCkVsc = 0;       // [128] fp32 Value scale
 constexpr int kCkVmid = 512;    // [128] fp32 vmin - 4 * vscale
-constexpr int kCkBias = 1024;   // [8] fp32 page bias per head
-constexpr int kCkVt = 1056;     // [32 groups][36] u32 Value-code byte columns (4 per 8-word row) + 4 pad
+constexpr int kCkBias = 1024;   // [8 heads][4 waves] fp32 page bias partials
+constexpr int kCkVt = 1152;     // [32 groups][36] u32 Value-code byte columns (4 per 8-word row) + 4 pad
 constexpr int kCkQs = kCkVt + 32 * 36 * 4;  // [nb][16][8] fp16 Qs hi (rows 0..7) / lo (rows 8..15)
 
 struct MfmaLayout {
@@ -236,23 +236,31 @@ __device__ __forceinline__ LoopY loop_y(const MfmaLayout& y) {
     return z;
 }
 
-// Qs of integer-tier block ``gb`` for head ``n`` -- hi into row n, lo (the fp16 residual) into
-// row n + 8 -- and the block's share of the bias sum_slot q * (min - beta * scale).  ``ksc`` /
-// ``kmn``: the block's Key scale / min pair words (page Odd in the high halves).  Padding
-// slots have q == 0; their scale/min words hold a real slot's (finite) values.  Written so
-// the compiler uses mixed-precision FMAs on the fp16 halves directly.
+// Operands of one Qs block: q of (block, head) and the block's Key scale / min pair words.
+struct QsRegs {
+    float4 q0, q1;
+    uint4 s0, s1, m0, m1;
+};
+
+__device__ __forceinline__ void qs_fetch(const float* qrow, const uint32_t* ksc, const uint32_t* kmn, QsRegs& r) {
+    r.q0 = *reinterpret_cast<const float4*>(qrow);
+    r.q1 = *reinterpret_cast<const float4*>(qrow + 4);
+    r.s0 = *reinterpret_cast<const uint4*>(ksc);
+    r.s1 = *reinterpret_cast<const uint4*>(ksc + 4);
+    r.m0 = *reinterpret_cast<const uint4*>(kmn);
+    r.m1 = *reinterpret_cast<const uint4*>(kmn + 4);
+}
+
+// Qs of an integer-tier block for one head -- hi into ``qs_hi``, lo (the fp16 residual) into
+// ``qs_lo`` -- and the block's share of the bias sum_slot q * (min - beta * scale); page Odd
+// takes the high halves of the pair words.  Padding slots have q == 0; their scale/min words
+// hold a real slot's (finite) values.  Written so the compiler uses mixed-precision FMAs on
+// the fp16 halves directly.
 template <bool Odd>
-__device__ __forceinline__ float qs_block(const float* qrow, const uint32_t* ksc, const uint32_t* kmn, half8* qs_hi,
-                                          half8* qs_lo, float beta_lo, float beta_hi) {
-    const float4 q0 = *reinterpret_cast<const float4*>(qrow);
-    const float4 q1 = *reinterpret_cast<const float4*>(qrow + 4);
-    const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    const uint4 s0 = *reinterpret_cast<const uint4*>(ksc);
-    const uint4 s1 = *reinterpret_cast<const uint4*>(ksc + 4);
-    const uint4 m0 = *reinterpret_cast<const uint4*>(kmn);
-    const uint4 m1 = *reinterpret_cast<const uint4*>(kmn + 4);
-    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+__device__ __forceinline__ float qs_math(const QsRegs& r, half8* qs_hi, half8* qs_lo, float beta_lo, float beta_hi) {
+    const float qv[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t sw[8] = {r.s0.x, r.s0.y, r.s0.z, r.s0.w, r.s1.x, r.s1.y, r.s1.z, r.s1.w};
+    const uint32_t mw[8] = {r.m0.x, r.m0.y, r.m0.z, r.m0.w, r.m1.x, r.m1.y, r.m1.z, r.m1.w};
     half8 hi, lo;
     float bsum = 0.f;
 #pragma unroll
@@ -269,16 +277,6 @@ __device__ __forceinline__ float qs_block(const float* qrow, const uint32_t* ksc
     *qs_hi = hi;
     *qs_lo = lo;
     return bsum;
-}
-
-// Sum of x over each half wave, left in lanes 31 and 63 (DPP row shifts, then row_bcast:15).
-__device__ __forceinline__ float half_wave_sum(float x) {
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x111, 0xf, 0xf, true));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x112, 0xf, 0xf, true));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x114, 0xf, 0xf, true));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x118, 0xf, 0xf, true));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xa, 0xf, false));
-    return x;
 }
 
 // Max / sum of x over the four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48), in every lane:
@@ -434,29 +432,78 @@ __device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t rawa, uint32_t rawb
     }
 }
 
-// Prepare page ``page`` from rest buffer ``raw`` into prepared buffer ``ck`` (all threads).
-__device__ __forceinline__ void prepare_page(const LoopY& z, const unsigned char* raw, unsigned char* ck,
-                                             const float* qperm, int page, int g, int w16, int tid) {
-    const int lane = tid & 63;
-    {
-        // Value codes: dwords (group tg, word w, tokens 0..3) -> byte columns
-        const int tg = tid >> 3, w = tid & 7;
-        const uint32_t* vc = reinterpret_cast<const uint32_t*>(raw + kRawbVc) + 32 * tg + w;
-        uint32_t o[4];
-        byte_transpose4(vc[0], vc[8], vc[16], vc[24], o);
-        uint32_t* vt = reinterpret_cast<uint32_t*>(ck + kCkVt);
+// Page preparation, in two halves: prep_load issues the LDS reads of a page's rest buffer
+// into registers -- before the previous page's compute, so their latency hides behind it --
+// and prep_store converts them into the page's prepared buffer after that compute.
+//
+// Qs work: wave w takes blocks [w * nbw, (w + 1) * nbw) of the integer tiers (nbw = nb_int / 4
+// rounded up), lane = 8 * (block - w * nbw) + head, so a wave's q, scale/min reads and Qs
+// writes are consecutive in LDS (no bank conflicts).  Value scale/min: even threads, fp16-tier
+// rows: odd threads (token tid / 2).
+struct PrepRegs {
+    uint32_t vc[4];  // Value-code dwords: word tid % 8 of tokens 4 * (tid / 8) + (k + tid / 8) % 4
+    uint32_t vsm;    // Value scale (low half) and min (high half) of token tid / 2 (even tid)
+    QsRegs qs;       // Qs operands of the lane's first block
+};
+
+__device__ __forceinline__ float beta_lo_of(int tier) { return tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f; }
+__device__ __forceinline__ float beta_hi_of(int tier) { return tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f; }
+
+__device__ __forceinline__ void prep_load(const LoopY& z, const unsigned char* raw, const float* qperm, int g, int tid,
+                                          int wave, PrepRegs& r) {
+    // read k of thread (tg, w) takes token 4 tg + (k + tg) % 4: the 32 lanes of a half wave then
+    // hit 32 different banks
+    const int tg = tid >> 3, w = tid & 7;
+    const uint32_t* vc = reinterpret_cast<const uint32_t*>(raw + kRawbVc) + 32 * tg + w;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = o[k];
-    }
-    if (tid < kPage) {
-        // Value scale, the per-token constant vmin - 4 * vscale (4: the offset of the Value-code
-        // unpack), and the token's fp16-tier row zero padded to w16p columns
-        const int t = tid;
+    for (int k = 0; k < 4; ++k) r.vc[k] = vc[8 * ((k + tg) & 3)];
+    if ((tid & 1) == 0) {
         const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + kRawbVs);
         const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + kRawbVm);
-        const float s = f16_to_f32(vs[t]);
+        r.vsm = static_cast<uint32_t>(vs[tid >> 1]) | (static_cast<uint32_t>(vm[tid >> 1]) << 16);
+    }
+    const int lane = tid & 63, n = lane & 7, j = lane >> 3;
+    const int nbw = (z.nb_int + 3) >> 2, gb = wave * nbw + j;
+    if (n < g && j < nbw && gb < z.nb_int) {
+        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
+        qs_fetch(qperm + (gb * 8 + n) * 8, ksc + gb * 8, ksc + z.n_kslots / 2 + gb * 8, r.qs);
+    }
+}
+
+// Integer-tier Qs and bias of head n for block gb from fetched operands.
+__device__ __forceinline__ float qs_block(const LoopY& z, const QsRegs& r, half8* qs, int page, int gb, int n) {
+    const int tier = gb >= 4 * z.kf2 ? 2 : gb >= 4 * z.kf1 ? 1 : 0;
+    half8* hi = qs + gb * 16 + n;
+    half8* lo = qs + gb * 16 + 8 + n;
+    return (page & 1) ? qs_math<true>(r, hi, lo, beta_lo_of(tier), beta_hi_of(tier))
+                      : qs_math<false>(r, hi, lo, beta_lo_of(tier), beta_hi_of(tier));
+}
+
+// Finish page ``page``: fetched registers ``r`` (and, for what they do not hold, rest buffer
+// ``raw``) into prepared buffer ``ck`` (all threads).
+__device__ __forceinline__ void prep_store(const LoopY& z, const PrepRegs& r, const unsigned char* raw, unsigned char* ck,
+                                           const float* qperm, int page, int g, int w16, int tid, int wave) {
+    const int lane = tid & 63;
+    {
+        // Value codes: dwords (group tg, word w, tokens 0..3) -> byte columns.  The reads came
+        // in token order rotated by tg % 4, so each column comes out rotated by as many bytes.
+        const int tg = tid >> 3, w = tid & 7;
+        const uint32_t rot = (32 - 8 * (tg & 3)) & 31;
+        uint32_t o[4];
+        byte_transpose4(r.vc[0], r.vc[1], r.vc[2], r.vc[3], o);
+        uint32_t* vt = reinterpret_cast<uint32_t*>(ck + kCkVt);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = __builtin_amdgcn_alignbit(o[k], o[k], rot);
+    }
+    const int t = tid >> 1;
+    if ((tid & 1) == 0) {
+        // Value scale and the per-token constant vmin - 4 * vscale (4: the offset of the
+        // Value-code unpack)
+        const float s = f16_to_f32(static_cast<uint16_t>(r.vsm & 0xffffu));
         reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
-        reinterpret_cast<float*>(ck + kCkVmid)[t] = fmaf(-4.f, s, f16_to_f32(vm[t]));
+        reinterpret_cast<float*>(ck + kCkVmid)[t] = fmaf(-4.f, s, f16_to_f32(static_cast<uint16_t>(r.vsm >> 16)));
+    } else {
+        // the token's fp16-tier row, zero padded to w16p columns
         const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw + kRawbF16) + t * w16;
         uint4* dst = reinterpret_cast<uint4*>(ck + z.ck_v16 + 2 * t * z.w16p);
         for (int c0 = 0; c0 < w16; c0 += 8) {
@@ -466,29 +513,36 @@ __device__ __forceinline__ void prepare_page(const LoopY& z, const unsigned char
             dst[c0 >> 3] = uint4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
         }
     }
-    // Qs of the integer tiers and the bias: thread (head tid / 32, blocks tid % 32 + 32 i); each
-    // head's bias is summed over its half wave.  The fp16 tier's Qs (plain q) is set once.
-    const int n = tid >> 5;
+    // Qs of the integer tiers and this wave's share of the bias.  The fp16 tier's Qs (plain q)
+    // is set once.
+    const int n = lane & 7, j = lane >> 3;
+    const int nbw = (z.nb_int + 3) >> 2;
     float bsum = 0.f;
     if (n < g) {
-        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
-        const uint32_t* kmn = ksc + z.n_kslots / 2;
         half8* qs = reinterpret_cast<half8*>(ck + kCkQs);
-        for (int gb = tid & 31; gb < z.nb_int; gb += 32) {
-            const int tier = gb >= 4 * z.kf2 ? 2 : gb >= 4 * z.kf1 ? 1 : 0;
-            const float beta_lo = tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f;
-            const float beta_hi = tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f;
-            const float* qrow = qperm + (gb * 8 + n) * 8;
-            if (page & 1)
-                bsum += qs_block<true>(qrow, ksc + gb * 8, kmn + gb * 8, qs + gb * 16 + n, qs + gb * 16 + 8 + n,
-                                       beta_lo, beta_hi);
-            else
-                bsum += qs_block<false>(qrow, ksc + gb * 8, kmn + gb * 8, qs + gb * 16 + n, qs + gb * 16 + 8 + n,
-                                        beta_lo, beta_hi);
+        const int gb = wave * nbw + j;
+        if (j < nbw && gb < z.nb_int) bsum = qs_block(z, r.qs, qs, page, gb, n);
+        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
+        for (int jj = j + 8; jj < nbw; jj += 8) {
+            const int gb2 = wave * nbw + jj;
+            if (gb2 < z.nb_int) {
+                QsRegs q2;
+                qs_fetch(qperm + (gb2 * 8 + n) * 8, ksc + gb2 * 8, ksc + z.n_kslots / 2 + gb2 * 8, q2);
+                bsum += qs_block(z, q2, qs, page, gb2, n);
+            }
         }
     }
-    bsum = half_wave_sum(bsum);
-    if ((lane & 31) == 31) reinterpret_cast<float*>(ck + kCkBias)[n] = bsum;
+    // sum over the wave's lanes of head n (lanes n + 8 i): row_ror:8, then across the 4 rows
+    bsum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, bsum), 0x128, 0xf, 0xf, false));
+    bsum = rows_sum(bsum);
+    if (lane < 8) reinterpret_cast<float*>(ck + kCkBias)[4 * lane + wave] = bsum;
+}
+
+__device__ __forceinline__ void prepare_page(const LoopY& z, const unsigned char* raw, unsigned char* ck,
+                                             const float* qperm, int page, int g, int w16, int tid, int wave) {
+    PrepRegs r;
+    prep_load(z, raw, qperm, g, tid, wave, r);
+    prep_store(z, r, raw, ck, qperm, page, g, w16, tid, wave);
 }
 
 // q of the workgroup's heads, scaled into the log2 domain, into qlin [8][128] (0 for heads >= g).
@@ -600,7 +654,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         __syncthreads();  // qlin (aliased by prepared buffer 0) is dead from here on
         const int w16 = L.k_width[3];
         dma_barrier(pbeg + 1 < pend ? ds.per_page : 0);  // page pbeg landed (every wave's share)
-        prepare_page(z, rawb0, ck0, qperm, pbeg, g, w16, tid);
+        prepare_page(z, rawb0, ck0, qperm, pbeg, g, w16, tid, wave);
 
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
         const int sh = 2 * (n16 & 3);
@@ -613,9 +667,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             if (page + 2 < pend)
                 dma_page(ds, rawa_lds + ((rel + 2) % 3) * z.rawa_bytes, rawb_lds + (rel & 1) * z.rawb_bytes, z, page + 2,
                          wave);
-            if (page + 1 < pend)
-                prepare_page(z, rawb0 + ((rel + 1) & 1) * z.rawb_bytes, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm,
-                             page + 1, g, w16, tid);
+            // page + 1: its rest buffer is read now, its prepared buffer written after this
+            // page's compute
+            const bool prep_next = page + 1 < pend;
+            const unsigned char* raw_next = rawb0 + ((rel + 1) & 1) * z.rawb_bytes;
+            PrepRegs pr;
+            if (prep_next) prep_load(z, raw_next, qperm, g, tid, wave, pr);
 
             // ---- compute page ``page`` from its prepared buffer and Key codes ----
             const unsigned char* raw = rawa0 + (rel % 3) * z.rawa_bytes;
@@ -673,7 +730,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
             }
             // ---- online softmax (log2 domain) ----
-            const float bias = (n16 < 8) ? reinterpret_cast<const float*>(ck + kCkBias)[n16] : 0.f;
+            float bias = 0.f;
+            if (n16 < 8) {
+                const float4 bp = reinterpret_cast<const float4*>(ck + kCkBias)[n16];
+                bias = (bp.x + bp.y) + (bp.z + bp.w);
+            }
             float mx = sv[0];
 #pragma unroll
             for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
@@ -764,6 +825,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }
+            if (prep_next)
+                prep_store(z, pr, raw_next, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm, page + 1, g, w16, tid, wave);
         }
         // Reduce l and the midpoint term over the 4 lane groups of each head.
         l_run = rows_sum(l_run);
