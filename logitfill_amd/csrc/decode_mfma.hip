@@ -443,14 +443,40 @@ __device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t rawa, uint32_t rawb
 struct PrepRegs {
     uint32_t vc[4];  // Value-code dwords: word tid % 8 of tokens 4 * (tid / 8) + (k + tid / 8) % 4
     uint32_t vsm;    // Value scale (low half) and min (high half) of token tid / 2 (even tid)
+    uint32_t f16[2]; // fp16-tier dwords of the repack (see F16Map)
     QsRegs qs;       // Qs operands of the lane's first block
 };
+
+// The fp16-tier rows ([128][w16] halves in the rest buffer) are repacked into [128][w16p]
+// (zero padded to whole 8-half blocks): thread tid builds output dwords tid and tid + 256 from
+// two halves each.  Offsets are fixed per layer, so they are computed once.
+struct F16Map {
+    int src[2];      // byte offset of the dword's first half in the rest buffer (0 when unused)
+    int dst[2];      // byte offset of the dword in the prepared buffer, -1 past the end
+    uint32_t keep[2];  // 0xffff for each half that exists, else 0
+};
+
+__device__ __forceinline__ F16Map f16_map(const LoopY& z, int w16, int tid) {
+    F16Map m;
+    const int hw = z.w16p >> 1;  // output dwords per token
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int d = tid + 256 * i;
+        const int t = hw ? d / hw : 0, c = hw ? d - t * hw : 0;
+        const bool live = hw && t < kPage;
+        const bool lo = live && 2 * c < w16, hi = live && 2 * c + 1 < w16;
+        m.src[i] = lo ? kRawbF16 + 2 * (t * w16 + 2 * c) : 0;
+        m.dst[i] = live ? z.ck_v16 + 4 * d : -1;
+        m.keep[i] = (lo ? 0xffffu : 0u) | (hi ? 0xffff0000u : 0u);
+    }
+    return m;
+}
 
 __device__ __forceinline__ float beta_lo_of(int tier) { return tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f; }
 __device__ __forceinline__ float beta_hi_of(int tier) { return tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f; }
 
-__device__ __forceinline__ void prep_load(const LoopY& z, const unsigned char* raw, const float* qperm, int g, int tid,
-                                          int wave, PrepRegs& r) {
+__device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, const unsigned char* raw, const float* qperm,
+                                          int g, int tid, int wave, PrepRegs& r) {
     // read k of thread (tg, w) takes token 4 tg + (k + tg) % 4: the 32 lanes of a half wave then
     // hit 32 different banks
     const int tg = tid >> 3, w = tid & 7;
@@ -461,6 +487,13 @@ __device__ __forceinline__ void prep_load(const LoopY& z, const unsigned char* r
         const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + kRawbVs);
         const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + kRawbVm);
         r.vsm = static_cast<uint32_t>(vs[tid >> 1]) | (static_cast<uint32_t>(vm[tid >> 1]) << 16);
+    }
+    // both halves of each repack dword: two 2-byte reads (rows of odd width are 2-byte aligned);
+    // the high half of the last column reads the next row or padding and is masked off
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(raw + fm.src[i]);
+        r.f16[i] = (static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16)) & fm.keep[i];
     }
     const int lane = tid & 63, n = lane & 7, j = lane >> 3;
     const int nbw = (z.nb_int + 3) >> 2, gb = wave * nbw + j;
@@ -481,8 +514,9 @@ __device__ __forceinline__ float qs_block(const LoopY& z, const QsRegs& r, half8
 
 // Finish page ``page``: fetched registers ``r`` (and, for what they do not hold, rest buffer
 // ``raw``) into prepared buffer ``ck`` (all threads).
-__device__ __forceinline__ void prep_store(const LoopY& z, const PrepRegs& r, const unsigned char* raw, unsigned char* ck,
-                                           const float* qperm, int page, int g, int w16, int tid, int wave) {
+__device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, const PrepRegs& r, const unsigned char* raw,
+                                           unsigned char* ck, const float* qperm, int page, int g, int w16, int tid,
+                                           int wave) {
     const int lane = tid & 63;
     {
         // Value codes: dwords (group tg, word w, tokens 0..3) -> byte columns.  The reads came
@@ -495,23 +529,24 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const PrepRegs& r, co
 #pragma unroll
         for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = __builtin_amdgcn_alignbit(o[k], o[k], rot);
     }
-    const int t = tid >> 1;
     if ((tid & 1) == 0) {
         // Value scale and the per-token constant vmin - 4 * vscale (4: the offset of the
         // Value-code unpack)
+        const int t = tid >> 1;
         const float s = f16_to_f32(static_cast<uint16_t>(r.vsm & 0xffffu));
         reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
         reinterpret_cast<float*>(ck + kCkVmid)[t] = fmaf(-4.f, s, f16_to_f32(static_cast<uint16_t>(r.vsm >> 16)));
-    } else {
-        // the token's fp16-tier row, zero padded to w16p columns
-        const uint16_t* f16 = reinterpret_cast<const uint16_t*>(raw + kRawbF16) + t * w16;
-        uint4* dst = reinterpret_cast<uint4*>(ck + z.ck_v16 + 2 * t * z.w16p);
-        for (int c0 = 0; c0 < w16; c0 += 8) {
-            uint32_t v[8];
+    }
+    // fp16-tier repack: dwords tid and tid + 256, then (rows wider than 8) the rest
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = c0 + k < w16 ? f16[c0 + k] : 0u;
-            dst[c0 >> 3] = uint4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16)};
-        }
+    for (int i = 0; i < 2; ++i)
+        if (fm.dst[i] >= 0) *reinterpret_cast<uint32_t*>(ck + fm.dst[i]) = r.f16[i];
+    const int hw = z.w16p >> 1;
+    for (int d = tid + 512; d < kPage * hw; d += 256) {
+        const int t = d / hw, c = d - t * hw;
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(raw + kRawbF16) + t * w16 + 2 * c;
+        const uint32_t lo = 2 * c < w16 ? h[0] : 0u, hi = 2 * c + 1 < w16 ? h[1] : 0u;
+        reinterpret_cast<uint32_t*>(ck + z.ck_v16)[d] = lo | (hi << 16);
     }
     // Qs of the integer tiers and this wave's share of the bias.  The fp16 tier's Qs (plain q)
     // is set once.
@@ -538,11 +573,11 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const PrepRegs& r, co
     if (lane < 8) reinterpret_cast<float*>(ck + kCkBias)[4 * lane + wave] = bsum;
 }
 
-__device__ __forceinline__ void prepare_page(const LoopY& z, const unsigned char* raw, unsigned char* ck,
+__device__ __forceinline__ void prepare_page(const LoopY& z, const F16Map& fm, const unsigned char* raw, unsigned char* ck,
                                              const float* qperm, int page, int g, int w16, int tid, int wave) {
     PrepRegs r;
-    prep_load(z, raw, qperm, g, tid, wave, r);
-    prep_store(z, r, raw, ck, qperm, page, g, w16, tid, wave);
+    prep_load(z, fm, raw, qperm, g, tid, wave, r);
+    prep_store(z, fm, r, raw, ck, qperm, page, g, w16, tid, wave);
 }
 
 // q of the workgroup's heads, scaled into the log2 domain, into qlin [8][128] (0 for heads >= g).
@@ -654,7 +689,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         __syncthreads();  // qlin (aliased by prepared buffer 0) is dead from here on
         const int w16 = L.k_width[3];
         dma_barrier(pbeg + 1 < pend ? ds.per_page : 0);  // page pbeg landed (every wave's share)
-        prepare_page(z, rawb0, ck0, qperm, pbeg, g, w16, tid, wave);
+        const F16Map fm = f16_map(z, w16, tid);
+        prepare_page(z, fm, rawb0, ck0, qperm, pbeg, g, w16, tid, wave);
 
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
         const int sh = 2 * (n16 & 3);
@@ -667,13 +703,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             if (page + 2 < pend)
                 dma_page(ds, rawa_lds + ((rel + 2) % 3) * z.rawa_bytes, rawb_lds + (rel & 1) * z.rawb_bytes, z, page + 2,
                          wave);
-            // page + 1: its rest buffer is read now, its prepared buffer written after this
-            // page's compute
-            const bool prep_next = page + 1 < pend;
-            const unsigned char* raw_next = rawb0 + ((rel + 1) & 1) * z.rawb_bytes;
-            PrepRegs pr;
-            if (prep_next) prep_load(z, raw_next, qperm, g, tid, wave, pr);
-
             // ---- compute page ``page`` from its prepared buffer and Key codes ----
             const unsigned char* raw = rawa0 + (rel % 3) * z.rawa_bytes;
             const unsigned char* ck = ck0 + (rel & 1) * z.ck_bytes;
@@ -717,6 +746,26 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     const half8 bq = qs[(4 * (z.kf3 + s) + kb) * 16 + n16];
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ua), bq, acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ub), bq, acc1, 0, 0, 0);
+                }
+            }
+            // Value codes of the lane's 8 tokens for channel 16*nt + n16, unpacked while the score
+            // MFMAs drain: code bits to mantissa 8..9 under exponent 4, value 4 + c (the offset is
+            // folded into the per-token constant); tokens (0, 2) sit at byte bits sh, (1, 3) at 8 + sh
+            uint4 bu[8];
+            {
+                const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + kCkVt);
+                const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
+                const uint4 d0b = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8 + 4);
+                const uint4 d1a = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8);
+                const uint4 d1b = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8 + 4);
+                const uint32_t dlo[8] = {d0a.x, d0a.y, d0a.z, d0a.w, d0b.x, d0b.y, d0b.z, d0b.w};
+                const uint32_t dhi[8] = {d1a.x, d1a.y, d1a.z, d1a.w, d1b.x, d1b.y, d1b.z, d1b.w};
+#pragma unroll
+                for (int nt = 0; nt < 8; ++nt) {
+                    bu[nt].x = bfi(dlo[nt] << (8 - sh), kv.m2hi, kv.e4);
+                    bu[nt].y = bfi(dlo[nt] >> sh, kv.m2hi, kv.e4);
+                    bu[nt].z = bfi(dhi[nt] << (8 - sh), kv.m2hi, kv.e4);
+                    bu[nt].w = bfi(dhi[nt] >> sh, kv.m2hi, kv.e4);
                 }
             }
             // hi + lo columns (row_shl:8, zero outside the row).  The accumulator elements are
@@ -804,29 +853,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             m_run = m_new;
             l_run += psum;
             mid_run += pmid;
-            // ---- value product: codes of the lane's 8 tokens, channel 16*nt + n16 ----
-            const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + kCkVt);
-            const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
-            const uint4 d0b = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8 + 4);
-            const uint4 d1a = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8);
-            const uint4 d1b = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8 + 4);
-            const uint32_t dlo[8] = {d0a.x, d0a.y, d0a.z, d0a.w, d0b.x, d0b.y, d0b.z, d0b.w};
-            const uint32_t dhi[8] = {d1a.x, d1a.y, d1a.z, d1a.w, d1b.x, d1b.y, d1b.z, d1b.w};
+            // ---- value product: codes of the lane's 8 tokens (unpacked above), channel 16*nt + n16 ----
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
-                // code bits to mantissa 8..9 under exponent 4: value 4 + c (the offset is folded
-                // into the per-token constant); tokens (0, 2) sit at byte bits sh, (1, 3) at 8 + sh
-                uint4 bu;
-                bu.x = bfi(dlo[nt] << (8 - sh), kv.m2hi, kv.e4);
-                bu.y = bfi(dlo[nt] >> sh, kv.m2hi, kv.e4);
-                bu.z = bfi(dhi[nt] << (8 - sh), kv.m2hi, kv.e4);
-                bu.w = bfi(dhi[nt] >> sh, kv.m2hi, kv.e4);
                 float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
-                o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
+                o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu[nt]), o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }
-            if (prep_next)
-                prep_store(z, pr, raw_next, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm, page + 1, g, w16, tid, wave);
+            // ---- page + 1's prepared buffer (its rest buffer landed at the barrier) ----
+            if (page + 1 < pend)
+                prepare_page(z, fm, rawb0 + ((rel + 1) & 1) * z.rawb_bytes, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm,
+                             page + 1, g, w16, tid, wave);
         }
         // Reduce l and the midpoint term over the 4 lane groups of each head.
         l_run = rows_sum(l_run);
