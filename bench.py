@@ -39,6 +39,7 @@ def parse_args():
     p.add_argument("--kernel", default="auto", choices=["auto", "valu", "mfma"])
     p.add_argument("--pages-per-split", type=int, default=None)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-dense", action="store_true", help="skip the BF16 dense comparator")
     p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                    help="only run a plain device-to-device copy of BYTES (3 times) and exit: the reference "
@@ -149,6 +150,45 @@ def time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split):
     return ms / steps, wall / steps * 1e3
 
 
+def time_dense(cfg, steps, warmup):
+    """The BF16 dense comparator (lf_dense_decode) at the same shape: one layer's K/V cache of
+    all history + residual + new tokens, two layers alternated so no call reads a cache the
+    previous call left in the L2/MALL.  Returns (us per layer-step, bytes per layer-step)."""
+    import torch
+
+    from logitfill_amd.packed.dense import dense_decode
+
+    B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
+    T = cfg["pages"] * 128 + cfg["residual"] + 1
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    caches = []
+    for _ in range(2):
+        k = torch.randn(B, n_kv, T, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        v = torch.randn(B, n_kv, T, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        q = (torch.randn(B, n_q, D, device=dev, generator=gen) * D ** -0.5).to(torch.bfloat16)
+        caches.append((q, k, v))
+    out = torch.empty(B, n_q, D, device=dev, dtype=torch.bfloat16)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    for i in range(warmup):
+        q, k, v = caches[i & 1]
+        dense_decode(q, k, v, D ** -0.5, out=out, workspace=ws)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        q, k, v = caches[i & 1]
+        dense_decode(q, k, v, D ** -0.5, out=out, workspace=ws)
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    us = start.elapsed_time(end) * 1e3 / steps
+    nbytes = B * n_kv * T * D * 2 * 2 + 2 * B * n_q * D * 2
+    del caches, ws
+    torch.cuda.empty_cache()
+    return us, nbytes
+
+
 def cpu_baseline(cfg, n_seqs):
     """The oracle's dense path (dequantise whole history, concatenate, repeat_kv, fp32
     softmax attention) on one layer for ``n_seqs`` sequences, scaled to the batch."""
@@ -247,6 +287,19 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(args.config) if args.layers in (None, cfg["layers"]) else None},
     }
+    if not args.no_dense:
+        print("[bench] bf16 dense comparator ...", file=sys.stderr, flush=True)
+        dense_us, dense_bytes = time_dense(cfg, max(args.steps, 10), args.warmup)
+        result["dense_bf16"] = {
+            "what": "lf_dense_decode: BF16 dense split-K MFMA decode over the uncompressed K/V cache of the "
+                    "same shape (history + residual + new token), synthetic bf16 data",
+            "us_per_layer": round(dense_us, 2),
+            "hbm_gbs": round(dense_bytes / dense_us / 1e3, 1),
+            "bytes_per_layer_step": int(dense_bytes),
+            "floor_us_at_peak": round(dense_bytes / HBM_PEAK_GBS / 1e3, 2),
+            "speedup_packed_vs_dense": round(dense_us / us_layer, 3),
+            "speedup_packed_vs_dense_floor": round(dense_bytes / HBM_PEAK_GBS / 1e3 / us_layer, 3),
+        }
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seqs)

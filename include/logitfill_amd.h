@@ -166,8 +166,11 @@ int32_t lf_dequantize(const lf_packed_layer* layer, int32_t b, int32_t tokens,
 /*
  * BF16 dense decode attention (comparator; no reference counterpart): the
  * same split-K/merge over bf16 K/V [batch][n_kv][tokens][head_dim] (element
- * strides kv_stride_b/h/t), query bf16 [batch][n_q][head_dim], out bf16.
- * Workspace as lf_dense_decode_workspace_bytes().
+ * strides kv_stride_b/h/t, multiples of 8; channel stride 1), query bf16
+ * [batch][n_q][head_dim], out bf16, 16-byte aligned.  head_dim 128,
+ * n_q / n_kv <= 8, tokens_per_split a multiple of 128 (LF_E_UNSUPPORTED /
+ * LF_E_SHAPE otherwise).  Workspace as lf_dense_decode_workspace_bytes()
+ * (fp32 partials, no initialisation).
  */
 int64_t lf_dense_decode_workspace_bytes(int32_t batch, int32_t n_kv, int32_t n_q, int32_t head_dim,
                                         int32_t tokens, int32_t tokens_per_split);

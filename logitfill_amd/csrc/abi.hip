@@ -162,6 +162,7 @@ int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* 
     p.g = g;
     p.qscale = A.scaling * lf::kLog2e;
     p.part = static_cast<float*>(A.workspace);
+    p.dense_splits = 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (A.kernel != 1) {
         bool handled = false;
@@ -194,7 +195,7 @@ int32_t lf_dense_decode(const void* query, const void* k, const void* v, int32_t
     if (batch <= 0 || n_kv <= 0 || n_q <= 0 || n_q % n_kv != 0 || tokens <= 0) return LF_E_SHAPE;
     if (n_q / n_kv > 16) return LF_E_UNSUPPORTED;
     if (head_dim != 128) return LF_E_UNSUPPORTED;
-    if (tokens_per_split <= 0 || tokens_per_split % 64 != 0) return LF_E_SHAPE;
+    if (tokens_per_split <= 0 || tokens_per_split % 128 != 0) return LF_E_SHAPE;
     if (workspace_bytes < lf::dense_workspace_bytes(batch, n_kv, n_q, head_dim, tokens, tokens_per_split))
         return LF_E_WORKSPACE;
     return lf::launch_dense_decode(query, k, v, batch, n_q, n_kv, head_dim, tokens, kv_stride_b, kv_stride_h,

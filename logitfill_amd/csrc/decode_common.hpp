@@ -18,6 +18,8 @@ struct DecodeParams {
     int g;          // query heads per kv head
     float qscale;   // scaling * log2(e)
     float* part;    // [n_work][n_kv][g][D + 2]  (o[D], m, l)
+    int dense_splits;  // > 0: items b * dense_splits .. + dense_splits - 1 are sequence b's
+                       // (the dense comparator); 0: A.seq_work lists them
 };
 
 // Workspace layout shared by lf_decode_workspace_bytes and the kernels: the float

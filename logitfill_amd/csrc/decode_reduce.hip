@@ -21,8 +21,8 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     const int i = blockIdx.x % g;
     const int h = (blockIdx.x / g) % p.L.n_kv;
     const int b = blockIdx.x / (g * p.L.n_kv);
-    const int first = p.A.seq_work[2 * b];
-    const int count = p.A.seq_work[2 * b + 1];
+    const int first = p.dense_splits ? b * p.dense_splits : p.A.seq_work[2 * b];
+    const int count = p.dense_splits ? p.dense_splits : p.A.seq_work[2 * b + 1];
     const int tid = threadIdx.x;
     const int nw = blockDim.x / kWave;
 
