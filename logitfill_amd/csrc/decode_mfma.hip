@@ -442,8 +442,8 @@ __device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t rawa, uint32_t rawb
 // rows: odd threads (token tid / 2).
 struct PrepRegs {
     uint32_t vc[4];  // Value-code dwords: word tid % 8 of tokens 4 * (tid / 8) + (k + tid / 8) % 4
-    uint32_t vsm;    // Value scale (low half) and min (high half) of token tid / 2 (even tid)
-    uint32_t f16[2]; // fp16-tier dwords of the repack (see F16Map)
+    uint32_t vs, vm; // Value scale / min bits of token tid / 2 (used by even tid)
+    uint32_t f16[2][2];  // fp16-tier halves of the repack dwords (see F16Map)
     QsRegs qs;       // Qs operands of the lane's first block
 };
 
@@ -483,24 +483,22 @@ __device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, cons
     const uint32_t* vc = reinterpret_cast<const uint32_t*>(raw + kRawbVc) + 32 * tg + w;
 #pragma unroll
     for (int k = 0; k < 4; ++k) r.vc[k] = vc[8 * ((k + tg) & 3)];
-    if ((tid & 1) == 0) {
-        const uint16_t* vs = reinterpret_cast<const uint16_t*>(raw + kRawbVs);
-        const uint16_t* vm = reinterpret_cast<const uint16_t*>(raw + kRawbVm);
-        r.vsm = static_cast<uint32_t>(vs[tid >> 1]) | (static_cast<uint32_t>(vm[tid >> 1]) << 16);
-    }
+    // Every read below is unconditional (addresses clamped into the buffers), so the whole
+    // fetch goes out in one batch without a wait; what a thread does not need it ignores.
+    r.vs = reinterpret_cast<const uint16_t*>(raw + kRawbVs)[tid >> 1];
+    r.vm = reinterpret_cast<const uint16_t*>(raw + kRawbVm)[tid >> 1];
     // both halves of each repack dword: two 2-byte reads (rows of odd width are 2-byte aligned);
-    // the high half of the last column reads the next row or padding and is masked off
+    // the high half of the last column reads the next row or padding and is masked off later
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const uint16_t* h = reinterpret_cast<const uint16_t*>(raw + fm.src[i]);
-        r.f16[i] = (static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16)) & fm.keep[i];
+        r.f16[i][0] = h[0];
+        r.f16[i][1] = h[1];
     }
     const int lane = tid & 63, n = lane & 7, j = lane >> 3;
-    const int nbw = (z.nb_int + 3) >> 2, gb = wave * nbw + j;
-    if (n < g && j < nbw && gb < z.nb_int) {
-        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
-        qs_fetch(qperm + (gb * 8 + n) * 8, ksc + gb * 8, ksc + z.n_kslots / 2 + gb * 8, r.qs);
-    }
+    const int nbw = (z.nb_int + 3) >> 2, gb = min(wave * nbw + j, z.nb_int - 1);
+    const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
+    qs_fetch(qperm + (gb * 8 + n) * 8, ksc + gb * 8, ksc + z.n_kslots / 2 + gb * 8, r.qs);
 }
 
 // Integer-tier Qs and bias of head n for block gb from fetched operands.
@@ -533,14 +531,14 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
         // Value scale and the per-token constant vmin - 4 * vscale (4: the offset of the
         // Value-code unpack)
         const int t = tid >> 1;
-        const float s = f16_to_f32(static_cast<uint16_t>(r.vsm & 0xffffu));
+        const float s = f16_to_f32(static_cast<uint16_t>(r.vs));
         reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
-        reinterpret_cast<float*>(ck + kCkVmid)[t] = fmaf(-4.f, s, f16_to_f32(static_cast<uint16_t>(r.vsm >> 16)));
+        reinterpret_cast<float*>(ck + kCkVmid)[t] = fmaf(-4.f, s, f16_to_f32(static_cast<uint16_t>(r.vm)));
     }
     // fp16-tier repack: dwords tid and tid + 256, then (rows wider than 8) the rest
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-        if (fm.dst[i] >= 0) *reinterpret_cast<uint32_t*>(ck + fm.dst[i]) = r.f16[i];
+        if (fm.dst[i] >= 0) *reinterpret_cast<uint32_t*>(ck + fm.dst[i]) = (r.f16[i][0] | (r.f16[i][1] << 16)) & fm.keep[i];
     const int hw = z.w16p >> 1;
     for (int d = tid + 512; d < kPage * hw; d += 256) {
         const int t = d / hw, c = d - t * hw;
@@ -589,6 +587,131 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int b, int h, floa
                                 p.qscale
                           : 0.f;
     }
+}
+
+// Score operands of one page for one lane: Key-code rows of the three integer tiers, the
+// prepared fp16-tier rows and Qs, the lane's two token rows and MFMA coordinates.
+struct KTiles {
+    const uint32_t* k0;
+    const uint32_t* k1;
+    const uint32_t* k2;
+    const unsigned char* v16;
+    const half8* qs;
+    int kw0, kw1, kw2, w16p, tok0, tok1, kb, n16;
+};
+
+// S^T of the lane's two 16-token tiles, any K-step counts.  Integer tiers read up to 7 dwords
+// past their segment (inside the LDS allocation): those blocks have Qs == 0 and unpack to
+// finite values.
+__device__ __forceinline__ void score_tiles(const KTiles& t, const LoopY& z, const UnpackBits& kv, float4v& acc0,
+                                            float4v& acc1) {
+    acc0 = float4v{0.f, 0.f, 0.f, 0.f};
+    acc1 = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int s2 = 0; s2 < z.kst0 / 2; ++s2) {
+        const uint32_t wa = t.k0[t.tok0 * t.kw0 + 4 * s2 + t.kb];
+        const uint32_t wb = t.k0[t.tok1 * t.kw0 + 4 * s2 + t.kb];
+        const half8 bq0 = t.qs[(8 * s2 + t.kb) * 16 + t.n16];
+        const half8 bq1 = t.qs[(8 * s2 + 4 + t.kb) * 16 + t.n16];
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wa, kv), bq0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wb, kv), bq0, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wa, kv), bq1, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wb, kv), bq1, acc1, 0, 0, 0);
+    }
+    for (int s = 0; s < z.kst1; ++s) {
+        const half8 bq = t.qs[(4 * (z.kst0 + s) + t.kb) * 16 + t.n16];
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(t.k1[t.tok0 * t.kw1 + 4 * s + t.kb], kv), bq, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(t.k1[t.tok1 * t.kw1 + 4 * s + t.kb], kv), bq, acc1, 0, 0, 0);
+    }
+    for (int s = 0; s < z.kst2; ++s) {
+        const int w0 = 2 * (4 * s + t.kb);
+        const half8 bq = t.qs[(4 * (z.kf2 + s) + t.kb) * 16 + t.n16];
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(t.k2[t.tok0 * t.kw2 + w0], t.k2[t.tok0 * t.kw2 + w0 + 1]), bq,
+                                                      acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(t.k2[t.tok1 * t.kw2 + w0], t.k2[t.tok1 * t.kw2 + w0 + 1]), bq,
+                                                      acc1, 0, 0, 0);
+    }
+    for (int s = 0; s < z.kst3; ++s) {
+        const int col = 8 * (4 * s + t.kb);
+        const bool ok = col < t.w16p;
+        const int cc = ok ? col : 0;
+        const uint4 ra = *reinterpret_cast<const uint4*>(t.v16 + 2 * (t.tok0 * t.w16p + cc));
+        const uint4 rb = *reinterpret_cast<const uint4*>(t.v16 + 2 * (t.tok1 * t.w16p + cc));
+        const uint4 ua = ok ? ra : uint4{0, 0, 0, 0}, ub = ok ? rb : uint4{0, 0, 0, 0};
+        const half8 bq = t.qs[(4 * (z.kf3 + s) + t.kb) * 16 + t.n16];
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ua), bq, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ub), bq, acc1, 0, 0, 0);
+    }
+}
+
+// The same for K-step counts known at compile time (P2 int2 step pairs, S1 int4, S2 int8, S3
+// fp16 steps): every LDS read of the page is issued before the first unpack, so the page
+// costs one LDS round trip instead of one per step.
+template <int P2, int S1, int S2, int S3>
+__device__ __forceinline__ void score_tiles_fixed(const KTiles& t, const UnpackBits& kv, float4v& acc0, float4v& acc1) {
+    constexpr int F1 = 2 * P2, F2 = F1 + S1, F3 = F2 + S2;  // first K-step of each tier
+    uint32_t w2[P2][2], w4[S1 > 0 ? S1 : 1][2], w8[S2 > 0 ? S2 : 1][2][2];
+    uint4 wf[S3 > 0 ? S3 : 1][2];
+    half8 q2[P2][2], q4[S1 > 0 ? S1 : 1], q8[S2 > 0 ? S2 : 1], qf[S3 > 0 ? S3 : 1];
+    const int toks[2] = {t.tok0, t.tok1};
+#pragma unroll
+    for (int s2 = 0; s2 < P2; ++s2) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) w2[s2][i] = t.k0[toks[i] * t.kw0 + 4 * s2 + t.kb];
+        q2[s2][0] = t.qs[(8 * s2 + t.kb) * 16 + t.n16];
+        q2[s2][1] = t.qs[(8 * s2 + 4 + t.kb) * 16 + t.n16];
+    }
+#pragma unroll
+    for (int s = 0; s < S1; ++s) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) w4[s][i] = t.k1[toks[i] * t.kw1 + 4 * s + t.kb];
+        q4[s] = t.qs[(4 * (F1 + s) + t.kb) * 16 + t.n16];
+    }
+#pragma unroll
+    for (int s = 0; s < S2; ++s) {
+        const int w0 = 2 * (4 * s + t.kb);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            w8[s][i][0] = t.k2[toks[i] * t.kw2 + w0];
+            w8[s][i][1] = t.k2[toks[i] * t.kw2 + w0 + 1];
+        }
+        q8[s] = t.qs[(4 * (F2 + s) + t.kb) * 16 + t.n16];
+    }
+    bool okf[S3 > 0 ? S3 : 1];
+#pragma unroll
+    for (int s = 0; s < S3; ++s) {
+        const int col = 8 * (4 * s + t.kb);
+        okf[s] = col < t.w16p;
+        const int cc = okf[s] ? col : 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) wf[s][i] = *reinterpret_cast<const uint4*>(t.v16 + 2 * (toks[i] * t.w16p + cc));
+        qf[s] = t.qs[(4 * (F3 + s) + t.kb) * 16 + t.n16];
+    }
+    float4v acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int s2 = 0; s2 < P2; ++s2) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(w2[s2][i], kv), q2[s2][0], acc[i], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(w2[s2][i], kv), q2[s2][1], acc[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int s = 0; s < S1; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(w4[s][i], kv), q4[s], acc[i], 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < S2; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(w8[s][i][0], w8[s][i][1]), q8[s], acc[i], 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < S3; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint4 u = okf[s] ? wf[s][i] : uint4{0, 0, 0, 0};
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, u), qf[s], acc[i], 0, 0, 0);
+        }
+    acc0 = acc[0];
+    acc1 = acc[1];
 }
 
 __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
@@ -709,44 +832,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             const half8* qs = reinterpret_cast<const half8*>(ck + kCkQs);
             // Integer tiers read up to 7 dwords past their segment (inside the LDS allocation):
             // those blocks have Qs == 0 and unpack to finite values.
-            float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+            float4v acc0, acc1;
             {
-                const uint32_t* k0 = reinterpret_cast<const uint32_t*>(raw);
-                for (int s2 = 0; s2 < z.kst0 / 2; ++s2) {
-                    const uint32_t wa = k0[tok0 * kw0 + 4 * s2 + kb];
-                    const uint32_t wb = k0[tok1 * kw0 + 4 * s2 + kb];
-                    const half8 bq0 = qs[(8 * s2 + kb) * 16 + n16];
-                    const half8 bq1 = qs[(8 * s2 + 4 + kb) * 16 + n16];
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wa, kv), bq0, acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<0>(wb, kv), bq0, acc1, 0, 0, 0);
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wa, kv), bq1, acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack2<1>(wb, kv), bq1, acc1, 0, 0, 0);
-                }
-                const uint32_t* k1 = reinterpret_cast<const uint32_t*>(raw + 16 * z.seg0);
-                for (int s = 0; s < z.kst1; ++s) {
-                    const half8 bq = qs[(4 * (z.kst0 + s) + kb) * 16 + n16];
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok0 * kw1 + 4 * s + kb], kv), bq, acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack4(k1[tok1 * kw1 + 4 * s + kb], kv), bq, acc1, 0, 0, 0);
-                }
-                const uint32_t* k2 = reinterpret_cast<const uint32_t*>(raw + 16 * z.seg1);
-                for (int s = 0; s < z.kst2; ++s) {
-                    const int w0 = 2 * (4 * s + kb);
-                    const half8 bq = qs[(4 * (z.kf2 + s) + kb) * 16 + n16];
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok0 * kw2 + w0], k2[tok0 * kw2 + w0 + 1]), bq,
-                                                                  acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8(k2[tok1 * kw2 + w0], k2[tok1 * kw2 + w0 + 1]), bq,
-                                                                  acc1, 0, 0, 0);
-                }
-                const unsigned char* v16 = ck + z.ck_v16;
-                for (int s = 0; s < z.kst3; ++s) {
-                    const int col = 8 * (4 * s + kb);
-                    const bool ok = col < z.w16p;
-                    const uint4 ua = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok0 * z.w16p + col)) : uint4{0, 0, 0, 0};
-                    const uint4 ub = ok ? *reinterpret_cast<const uint4*>(v16 + 2 * (tok1 * z.w16p + col)) : uint4{0, 0, 0, 0};
-                    const half8 bq = qs[(4 * (z.kf3 + s) + kb) * 16 + n16];
-                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ua), bq, acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ub), bq, acc1, 0, 0, 0);
-                }
+                const KTiles kt{reinterpret_cast<const uint32_t*>(raw), reinterpret_cast<const uint32_t*>(raw + 16 * z.seg0),
+                                reinterpret_cast<const uint32_t*>(raw + 16 * z.seg1), ck + z.ck_v16, qs,
+                                kw0, kw1, kw2, z.w16p, tok0, tok1, kb, n16};
+                if (z.kst0 == 4 && z.kst1 == 1 && z.kst2 == 1 && z.kst3 == 1)
+                    score_tiles_fixed<2, 1, 1, 1>(kt, kv, acc0, acc1);
+                else if (z.kst0 == 4 && z.kst1 == 2 && z.kst2 == 1 && z.kst3 == 1)
+                    score_tiles_fixed<2, 2, 1, 1>(kt, kv, acc0, acc1);
+                else
+                    score_tiles(kt, z, kv, acc0, acc1);
             }
             // Value codes of the lane's 8 tokens for channel 16*nt + n16, unpacked while the score
             // MFMAs drain: code bits to mantissa 8..9 under exponent 4, value 4 + c (the offset is
@@ -768,25 +864,30 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     bu[nt].w = bfi(dhi[nt] >> sh, kv.m2hi, kv.e4);
                 }
             }
-            // hi + lo columns (row_shl:8, zero outside the row).  The accumulator elements are
-            // copied to scalars before the DPP move: applied to vector elements directly, this
-            // compiler emits one move for all of them.  The page's bias enters through the max.
-            float sv[8];
-            const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
+            // ---- online softmax (log2 domain), compact: lane n16 < 8 takes tile 0 and lane n16 + 8
+            // tile 1 of head n16 % 8, four tokens each; the hi and lo columns meet through
+            // row_ror:8.  The accumulator elements are copied to scalars before the DPP move:
+            // applied to vector elements directly, this compiler emits one move for all of them.
+            const bool lo_lane = n16 >= 8;
+            float sv[4];
+            {
+                const float a0[4] = {acc0[0], acc0[1], acc0[2], acc0[3]};
+                const float a1[4] = {acc1[0], acc1[1], acc1[2], acc1[3]};
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const int xi = __builtin_bit_cast(int, accs[r]);
-                sv[r] = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
+                for (int r = 0; r < 4; ++r) {
+                    const float own = lo_lane ? a1[r] : a0[r];
+                    const int send = __builtin_bit_cast(int, lo_lane ? a0[r] : a1[r]);
+                    sv[r] = own + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, send, 0x128, 0xf, 0xf, false));
+                }
             }
-            // ---- online softmax (log2 domain) ----
-            float bias = 0.f;
-            if (n16 < 8) {
-                const float4 bp = reinterpret_cast<const float4*>(ck + kCkBias)[n16];
+            float bias;
+            {
+                const float4 bp = reinterpret_cast<const float4*>(ck + kCkBias)[n16 & 7];
                 bias = (bp.x + bp.y) + (bp.z + bp.w);
             }
-            float mx = sv[0];
-#pragma unroll
-            for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+            float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), 0x128,
+                                                                                  0xf, 0xf, false)));
             mx = rows_max(mx);
             // The reference point m_run moves only when the page's max exceeds it by more than
             // kLazyRescale (probabilities stay below 2^kLazyRescale), so most pages skip the
@@ -795,42 +896,46 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             const bool grow = m_cand > m_run + kLazyRescale;
             const float m_new = grow ? m_cand : m_run;
             const float m_off = m_new - bias;  // p = 2^(sv + bias - m_new)
-            const float* vsc = reinterpret_cast<const float*>(ck + kCkVsc);
-            const float* vmd = reinterpret_cast<const float*>(ck + kCkVmid);
-            const float4 s_lo = *reinterpret_cast<const float4*>(vsc + 32 * wave + 4 * kb);
-            const float4 s_hi = *reinterpret_cast<const float4*>(vsc + 32 * wave + 16 + 4 * kb);
-            const float4 d_lo = *reinterpret_cast<const float4*>(vmd + 32 * wave + 4 * kb);
-            const float4 d_hi = *reinterpret_cast<const float4*>(vmd + 32 * wave + 16 + 4 * kb);
-            const float vs[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
-            const float vd[8] = {d_lo.x, d_lo.y, d_lo.z, d_lo.w, d_hi.x, d_hi.y, d_hi.z, d_hi.w};
-            float pp[8];
-            float psum = 0.f, pmid = 0.f;
+            const int tokl = 32 * wave + (lo_lane ? 16 : 0) + 4 * kb;  // the lane's first token
+            const float4 vs = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ck + kCkVsc) + tokl);
+            const float4 vd = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ck + kCkVmid) + tokl);
+            float pp[4];
+            float psum, pmid;
+            {
+                const float vsa[4] = {vs.x, vs.y, vs.z, vs.w}, vda[4] = {vd.x, vd.y, vd.z, vd.w};
+                psum = 0.f;
+                pmid = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float pi = __builtin_amdgcn_exp2f(sv[i] - m_off);
-                psum += pi;
-                pmid = fmaf(pi, vd[i], pmid);
-                pp[i] = pi * vs[i];
+                for (int r = 0; r < 4; ++r) {
+                    const float pi = __builtin_amdgcn_exp2f(sv[r] - m_off);
+                    psum += pi;
+                    pmid = fmaf(pi, vda[r], pmid);
+                    pp[r] = pi * vsa[r];
+                }
             }
-            // A operand of the value product: k order (t0,t2),(t1,t3),(t4,t6),(t5,t7) of the
-            // lane's tokens; hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8.
-            uint32_t ahi[4], alo[4];
-            const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+            // A operand of the value product, k order (t0,t2),(t1,t3) of tile 0 then of tile 1 (the
+            // lane's tokens 4*kb + r): rows n16 < 8 the hi parts, rows n16 >= 8 the lo parts.  Each
+            // lane splits its own four values and swaps the half its partner row needs.
+            uint32_t hp[2], lp[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float x0 = pp[order[2 * j]], x1 = pp[order[2 * j + 1]];
+            for (int j = 0; j < 2; ++j) {
+                const float x0 = pp[j], x1 = pp[j + 2];
                 const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
                 const half2v hv = {h0, h1};
                 const half2v lv = {static_cast<_Float16>(x0 - static_cast<float>(h0)),
                                    static_cast<_Float16>(x1 - static_cast<float>(h1))};
-                ahi[j] = __builtin_bit_cast(uint32_t, hv);
-                alo[j] = __builtin_bit_cast(uint32_t, lv);
+                hp[j] = __builtin_bit_cast(uint32_t, hv);
+                lp[j] = __builtin_bit_cast(uint32_t, lv);
             }
+            uint32_t rv[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                rv[j] = __builtin_amdgcn_update_dpp(0, lo_lane ? hp[j] : lp[j], 0x128, 0xf, 0xf, false);
             uint4 au;
-            au.x = __builtin_amdgcn_update_dpp(ahi[0], alo[0], 0x118, 0xf, 0xc, false);
-            au.y = __builtin_amdgcn_update_dpp(ahi[1], alo[1], 0x118, 0xf, 0xc, false);
-            au.z = __builtin_amdgcn_update_dpp(ahi[2], alo[2], 0x118, 0xf, 0xc, false);
-            au.w = __builtin_amdgcn_update_dpp(ahi[3], alo[3], 0x118, 0xf, 0xc, false);
+            au.x = lo_lane ? rv[0] : hp[0];
+            au.y = lo_lane ? rv[1] : hp[1];
+            au.z = lo_lane ? lp[0] : rv[0];
+            au.w = lo_lane ? lp[1] : rv[1];
             const half8 ap = __builtin_bit_cast(half8, au);
             // Rescale O when some head's max moved: alpha of the 4 output rows this lane holds
             // (rows 4*kb + r, head (4*kb + r) % 8); a same-wave LDS write then read is ordered
@@ -865,7 +970,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 prepare_page(z, fm, rawb0 + ((rel + 1) & 1) * z.rawb_bytes, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm,
                              page + 1, g, w16, tid, wave);
         }
-        // Reduce l and the midpoint term over the 4 lane groups of each head.
+        // Reduce l and the midpoint term over the two tiles (lanes n16, n16 ^ 8) and the 4 lane
+        // groups of each head.
+        l_run += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, l_run), 0x128, 0xf, 0xf, false));
+        mid_run += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mid_run), 0x128, 0xf, 0xf, false));
         l_run = rows_sum(l_run);
         mid_run = rows_sum(mid_run);
         // Rows r (hi, lanes kb 0..1) + rows r+8 (lo, lanes kb 2..3).
