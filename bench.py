@@ -40,6 +40,7 @@ def parse_args():
     p.add_argument("--pages-per-split", type=int, default=None)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-dense", action="store_true", help="skip the BF16 dense comparator")
+    p.add_argument("--no-compress", action="store_true", help="skip the page-compress (config 3) timing")
     p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                    help="only run a plain device-to-device copy of BYTES (3 times) and exit: the reference "
@@ -189,6 +190,59 @@ def time_dense(cfg, steps, warmup):
     return us, nbytes
 
 
+def time_compress(target_bit, steps, warmup):
+    """page compress of 64 sequences x 1 page x 4 kv heads x 28 layers at the
+    7B shape (one lf_pack_pages launch per layer, all 64 pages of the layer).  Returns
+    (us per pass over the 28 layers, page-heads per pass, bytes read, bytes written)."""
+    import torch
+
+    from logitfill_amd import _native, synth
+    from logitfill_amd.packed import PackedKVManager
+
+    B, n_q, n_kv, D, L = 64, 28, 4, 128, 28
+    dev = torch.device("cuda", 0)
+    levels = [synth.sample_tier_levels(n_kv, D, target_bit, seed=layer) for layer in range(L)]
+    mgr = PackedKVManager(levels, n_q, n_kv, D, 128, 128, 128, 2, dev, batch_size=B, capacity_tokens=128)
+    srcs = []
+    for layer in range(L):
+        d = synth.make_layer(B, n_q, n_kv, D, 128, target_bit, seed=layer, device=dev)
+        srcs.append((d.key.contiguous(), d.value.contiguous()))
+        mgr.layers[layer].reserve(128)
+    jobs = torch.tensor([(b, 0, 0) for b in range(B)], dtype=torch.int32, device=dev)
+    structs = [mgr.layers[layer].layer_struct() for layer in range(L)]
+    lib = _native.load()
+    stream = torch.cuda.current_stream(dev)
+
+    def one_pass():
+        for layer in range(L):
+            k, v = srcs[layer]
+            st = lib.lf_pack_pages(structs[layer], k.data_ptr(), v.data_ptr(), _native.LF_BF16, k.stride(0),
+                                   k.stride(1), k.stride(2), jobs.data_ptr(), B, stream.cuda_stream)
+            _native.check(st, "lf_pack_pages")
+
+    for _ in range(warmup):
+        one_pass()
+    torch.cuda.synchronize(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        one_pass()
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    us = start.elapsed_time(end) * 1e3 / steps
+    page_heads = B * n_kv * L
+    read = page_heads * 128 * D * 2 * 2
+    written = 0
+    for st in mgr.layers:
+        w, words = st.widths, st.words
+        per_head = (128 * 4 * sum(words) + 128 * 2 * w[3] + 4 * (w[0] + w[1] + w[2])   # K codes, fp16, scale+min
+                    + 128 * 4 * (D // 16) + 128 * 4 * (D // 128))                      # V codes, scale+min
+        written += B * n_kv * per_head
+    del srcs, mgr
+    torch.cuda.empty_cache()
+    return us, page_heads, read, written
+
+
 def cpu_baseline(cfg, n_seqs):
     """The oracle's dense path (dequantise whole history, concatenate, repeat_kv, fp32
     softmax attention) on one layer for ``n_seqs`` sequences, scaled to the batch."""
@@ -300,6 +354,19 @@ def main():
             "speedup_packed_vs_dense": round(dense_us / us_layer, 3),
             "speedup_packed_vs_dense_floor": round(dense_bytes / HBM_PEAK_GBS / 1e3 / us_layer, 3),
         }
+    if not args.no_compress:
+        print("[bench] page compress (config 3) ...", file=sys.stderr, flush=True)
+        comp = {}
+        for tb in (2.5, 3.0, 4.0):
+            us, ph, rd, wr = time_compress(tb, 10, 2)
+            comp[f"target_{tb}"] = {"us_per_pass": round(us, 1), "page_heads": ph,
+                                    "pages_per_s": round(ph / us * 1e6), "gbs": round((rd + wr) / us / 1e3, 1),
+                                    "hbm_frac": round((rd + wr) / us / 1e3 / HBM_PEAK_GBS, 4),
+                                    "bytes_read": rd, "bytes_written": wr}
+        result["compress_c3"] = {
+            "what": "lf_pack_pages, BASELINE config 3: 64 sequences x 1 page x 4 kv heads x 28 layers (one launch "
+                    "per layer), bf16 K/V from the config-0 distributions; pages_per_s counts page-heads",
+            **comp}
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seqs)
