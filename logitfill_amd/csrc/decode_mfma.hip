@@ -527,38 +527,45 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
 #pragma unroll
         for (int k = 0; k < 4; ++k) vt[tg * 36 + k * 8 + w] = __builtin_amdgcn_alignbit(o[k], o[k], rot);
     }
-    if ((tid & 1) == 0) {
+    {
         // Value scale and the per-token constant vmin - 4 * vscale (4: the offset of the
-        // Value-code unpack)
+        // Value-code unpack) of token tid / 2: computed by every thread, stored by the even ones
         const int t = tid >> 1;
         const float s = f16_to_f32(static_cast<uint16_t>(r.vs));
-        reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
-        reinterpret_cast<float*>(ck + kCkVmid)[t] = fmaf(-4.f, s, f16_to_f32(static_cast<uint16_t>(r.vm)));
+        const float mid = fmaf(-4.f, s, f16_to_f32(static_cast<uint16_t>(r.vm)));
+        if ((tid & 1) == 0) {
+            reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
+            reinterpret_cast<float*>(ck + kCkVmid)[t] = mid;
+        }
     }
     // fp16-tier repack: dwords tid and tid + 256, then (rows wider than 8) the rest
 #pragma unroll
     for (int i = 0; i < 2; ++i)
         if (fm.dst[i] >= 0) *reinterpret_cast<uint32_t*>(ck + fm.dst[i]) = (r.f16[i][0] | (r.f16[i][1] << 16)) & fm.keep[i];
     const int hw = z.w16p >> 1;
-    for (int d = tid + 512; d < kPage * hw; d += 256) {
-        const int t = d / hw, c = d - t * hw;
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(raw + kRawbF16) + t * w16 + 2 * c;
-        const uint32_t lo = 2 * c < w16 ? h[0] : 0u, hi = 2 * c + 1 < w16 ? h[1] : 0u;
-        reinterpret_cast<uint32_t*>(ck + z.ck_v16)[d] = lo | (hi << 16);
+    if (kPage * hw > 512) {
+        for (int d = tid + 512; d < kPage * hw; d += 256) {
+            const int t = d / hw, c = d - t * hw;
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(raw + kRawbF16) + t * w16 + 2 * c;
+            const uint32_t lo = 2 * c < w16 ? h[0] : 0u, hi = 2 * c + 1 < w16 ? h[1] : 0u;
+            reinterpret_cast<uint32_t*>(ck + z.ck_v16)[d] = lo | (hi << 16);
+        }
     }
     // Qs of the integer tiers and this wave's share of the bias.  The fp16 tier's Qs (plain q)
-    // is set once.
+    // is set once.  Every lane computes and writes its (clamped) block: lanes past the wave's
+    // share or past the last block rewrite another lane's block with the same values, rows of
+    // heads >= g get the zeros they hold (their q is 0); only owned lanes count in the bias.
     const int n = lane & 7, j = lane >> 3;
     const int nbw = (z.nb_int + 3) >> 2;
-    float bsum = 0.f;
-    if (n < g) {
-        half8* qs = reinterpret_cast<half8*>(ck + kCkQs);
-        const int gb = wave * nbw + j;
-        if (j < nbw && gb < z.nb_int) bsum = qs_block(z, r.qs, qs, page, gb, n);
+    half8* qs = reinterpret_cast<half8*>(ck + kCkQs);
+    const int gb_own = wave * nbw + j;
+    float bsum = qs_block(z, r.qs, qs, page, min(gb_own, z.nb_int - 1), n);
+    if (!(n < g && j < nbw && gb_own < z.nb_int)) bsum = 0.f;
+    if (nbw > 8) {
         const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
         for (int jj = j + 8; jj < nbw; jj += 8) {
             const int gb2 = wave * nbw + jj;
-            if (gb2 < z.nb_int) {
+            if (n < g && gb2 < z.nb_int) {
                 QsRegs q2;
                 qs_fetch(qperm + (gb2 * 8 + n) * 8, ksc + gb2 * 8, ksc + z.n_kslots / 2 + gb2 * 8, q2);
                 bsum += qs_block(z, q2, qs, page, gb2, n);
@@ -826,6 +833,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             if (page + 2 < pend)
                 dma_page(ds, rawa_lds + ((rel + 2) % 3) * z.rawa_bytes, rawb_lds + (rel & 1) * z.rawb_bytes, z, page + 2,
                          wave);
+            // page + 1's rest buffer landed at the barrier: its reads go out now, so their latency
+            // hides behind this page's compute; its prepared buffer is written after the compute
+            const bool prep_next = page + 1 < pend;
+            const unsigned char* raw_next = rawb0 + ((rel + 1) & 1) * z.rawb_bytes;
+            PrepRegs pr;
+            if (prep_next) prep_load(z, fm, raw_next, qperm, g, tid, wave, pr);
             // ---- compute page ``page`` from its prepared buffer and Key codes ----
             const unsigned char* raw = rawa0 + (rel % 3) * z.rawa_bytes;
             const unsigned char* ck = ck0 + (rel & 1) * z.ck_bytes;
@@ -965,10 +978,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu[nt]), o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }
-            // ---- page + 1's prepared buffer (its rest buffer landed at the barrier) ----
-            if (page + 1 < pend)
-                prepare_page(z, fm, rawb0 + ((rel + 1) & 1) * z.rawb_bytes, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm,
-                             page + 1, g, w16, tid, wave);
+            // ---- page + 1's prepared buffer ----
+            if (prep_next)
+                prep_store(z, fm, pr, raw_next, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm, page + 1, g, w16, tid, wave);
         }
         // Reduce l and the midpoint term over the two tiles (lanes n16, n16 ^ 8) and the 4 lane
         // groups of each head.

@@ -294,6 +294,249 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
     }
 }
 
+int pack_code_row(const lf_packed_layer& L);
+
+// ---------------------------------------------------------------------------------------
+// Fast path for the common shape: page = Key group = Value group = head_dim = 128, int2
+// Values, 2-byte inputs with 16-byte aligned rows.  1024 threads per page so a page is
+// packed with enough waves in flight; per element the division uses a correctly rounded
+// reciprocal of the group scale and one Markstein correction (see div_rn).
+//
+//   stage     both pages into LDS (rows padded to 130 halves)
+//   phase 1   Key min/max: thread (channel tid % 128, tokens 16 (tid / 128) + 0..15); the 16
+//             values stay in registers
+//   phase 2   per integer-tier slot: group min, scale, reciprocal; scale/min stored
+//   phase 3   Key codes of the thread's 16 tokens into an LDS byte row per token
+//   phase 4   Key words (token, word) assembled from 4/8/16 code bytes, fp16 tier copied
+//   phase 5   Values: thread (token tid / 8, channels 16 (tid % 8) + 0..15) = one code word;
+//             the token's min/max over its 8 threads by lane exchange
+// ---------------------------------------------------------------------------------------
+constexpr int kFastThreads = 1024;
+constexpr int kFastP = 128;
+constexpr int kFastLd = 130;  // halves per staged row
+
+// a / s rounded to nearest even from y = RN(1/s) (Markstein: q0 = RN(a*y) is within an ulp of
+// a/s, the residual a - q0*s is exact by FMA, and RN(q0 + r*y) is the correctly rounded
+// quotient when no step overflows or underflows).  a >= 0 here; a quotient below the normal
+// range rounds to code 0 either way.  Non-finite a (a range overflowing float) takes the
+// plain IEEE division.
+__device__ __forceinline__ float div_rn(float a, float s, float y) {
+    const float q0 = a * y;
+    const float r = fmaf(-q0, s, a);
+    float q = fmaf(r, y, q0);
+    if (__builtin_expect(!__builtin_isfinite(a), 0)) q = a / s;
+    return q;
+}
+
+template <bool IsHalf>
+__global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) {
+    const lf_packed_layer& L = a.L;
+    const int job = blockIdx.x;
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int b = a.jobs[3 * job + 0];
+    const int64_t tok0 = a.jobs[3 * job + 1];
+    const int page = a.jobs[3 * job + 2];
+    const int64_t dst_tok0 = static_cast<int64_t>(page) * kFastP;
+    constexpr int D = 128;
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                       // [128][130]
+    uint16_t* vpage = kpage + kFastP * kFastLd;                                 // [128][130]
+    float* pmin = reinterpret_cast<float*>(vpage + kFastP * kFastLd);           // [8][128]
+    float* pmax = pmin + 8 * D;                                                 // [8][128]
+    float4* prm = reinterpret_cast<float4*>(pmax + 8 * D);                      // [cw] lo, s, y, -
+    int16_t* chslot = reinterpret_cast<int16_t*>(prm + a.cw);                   // [128] slot of a channel, -1
+    uint8_t* codes = reinterpret_cast<uint8_t*>(chslot + D);                    // [128][cw]
+    const int cw = a.cw;
+
+    int koff[4];
+    koff[0] = 0;
+    koff[1] = L.k_width[0];
+    koff[2] = koff[1] + L.k_width[1];
+    koff[3] = koff[2] + L.k_width[2];
+    const int nslots = koff[3];
+
+    // ---- stage both pages; channel -> integer slot map (layout.py:49-68) ----
+    {
+        const uint16_t* ks = static_cast<const uint16_t*>(a.k_src) + b * a.sb + h * a.sh + tok0 * a.st;
+        const uint16_t* vs = static_cast<const uint16_t*>(a.v_src) + b * a.sb + h * a.sh + tok0 * a.st;
+        uint4 kv[2], vv[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + kFastThreads * i;  // 16-byte chunk: row idx / 16, column 8 (idx % 16)
+            kv[i] = *reinterpret_cast<const uint4*>(ks + (idx >> 4) * a.st + 8 * (idx & 15));
+            vv[i] = *reinterpret_cast<const uint4*>(vs + (idx >> 4) * a.st + 8 * (idx & 15));
+        }
+        if (tid < D) chslot[tid] = -1;
+        __syncthreads();
+        for (int t = 0; t < 3; ++t) {
+            const int cnt = L.k_width[t] ? L.tier_count[t][h] : 0;
+            for (int j = tid; j < cnt; j += kFastThreads)
+                chslot[L.tier_index[t][h * L.k_width[t] + j]] = static_cast<int16_t>(koff[t] + j);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + kFastThreads * i;
+            uint32_t* kd = reinterpret_cast<uint32_t*>(kpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
+            uint32_t* vd = reinterpret_cast<uint32_t*>(vpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
+            kd[0] = kv[i].x; kd[1] = kv[i].y; kd[2] = kv[i].z; kd[3] = kv[i].w;
+            vd[0] = vv[i].x; vd[1] = vv[i].y; vd[2] = vv[i].z; vd[3] = vv[i].w;
+        }
+        __syncthreads();
+    }
+
+    // ---- phase 1: Key min/max of channel c over tokens 16 ck .. 16 ck + 15 ----
+    const int c = tid & (D - 1), ck = tid >> 7;
+    float x[16];
+    {
+        float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[i] = elem_f32<uint16_t, IsHalf>(kpage[(16 * ck + i) * kFastLd + c]);
+            lo = fminf(lo, x[i]);
+            hi = fmaxf(hi, x[i]);
+        }
+        pmin[ck * D + c] = lo;
+        pmax[ck * D + c] = hi;
+    }
+    __syncthreads();
+
+    // ---- phase 2: per integer slot (tier t, local j): s = clamp((hi - lo) / qmax) (layout.py:12-18) ----
+    for (int sl = tid; sl < nslots; sl += kFastThreads) {
+        const int t = sl >= koff[2] ? 2 : sl >= koff[1] ? 1 : 0;
+        const int j = sl - koff[t];
+        const int cnt = L.tier_count[t][h];
+        const int qmax = (1 << (2 << t)) - 1;
+        const int64_t o = kgrp_idx(L, b, h, L.k_width[t], j, page);
+        if (j < cnt) {
+            const int ch = L.tier_index[t][h * L.k_width[t] + j];
+            float lo = pmin[ch], hi = pmax[ch];
+#pragma unroll
+            for (int k = 1; k < 8; ++k) {
+                lo = fminf(lo, pmin[k * D + ch]);
+                hi = fmaxf(hi, pmax[k * D + ch]);
+            }
+            const float sc = group_scale(hi, lo, qmax);
+            prm[sl] = float4{lo, sc, 1.0f / sc, 0.f};
+            L.k_scale[t][o] = f32_to_f16(sc);
+            L.k_min[t][o] = f32_to_f16(lo);
+        } else {
+            // padding slots: scale 1.0, min 0.0, code 0 (layout.py:84-85)
+            L.k_scale[t][o] = 0x3C00u;
+            L.k_min[t][o] = 0;
+        }
+    }
+    // padding slot codes are 0
+    for (int i = tid; i < kFastP * cw / 4; i += kFastThreads) reinterpret_cast<uint32_t*>(codes)[i] = 0;
+    __syncthreads();
+
+    // ---- phase 3: codes of channel c for its 16 tokens ----
+    {
+        const int sl = chslot[c];
+        if (sl >= 0) {
+            const int t = sl >= koff[2] ? 2 : sl >= koff[1] ? 1 : 0;
+            const float qmax = static_cast<float>((1 << (2 << t)) - 1);
+            const float4 pr = prm[sl];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float q = __builtin_rintf(div_rn(x[i] - pr.x, pr.y, pr.z));
+                codes[(16 * ck + i) * cw + sl] = static_cast<uint8_t>(fminf(fmaxf(q, 0.0f), qmax));
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 4: LSB-first words (layout.py:21-35, :94-97); fp16 tier (layout.py:101-111) ----
+    {
+        const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
+        const int n0 = kFastP * kw0, n1 = n0 + kFastP * kw1, n2 = n1 + kFastP * kw2;
+        for (int idx = tid; idx < n2; idx += kFastThreads) {
+            const int t = idx >= n1 ? 2 : idx >= n0 ? 1 : 0;
+            const int rel = idx - (t == 2 ? n1 : t == 1 ? n0 : 0);
+            const int words = t == 2 ? kw2 : t == 1 ? kw1 : kw0;
+            const int tau = rel / words, w = rel - tau * words;
+            const uint8_t* crow = codes + tau * cw + koff[t];
+            const int width = L.k_width[t];  // slots past the tier width belong to the next tier
+            uint32_t word = 0;
+            if (t == 0) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    if (16 * w + k < width) word |= static_cast<uint32_t>(crow[16 * w + k]) << (2 * k);
+            } else if (t == 1) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (8 * w + k < width) word |= static_cast<uint32_t>(crow[8 * w + k]) << (4 * k);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (4 * w + k < width) word |= static_cast<uint32_t>(crow[4 * w + k]) << (8 * k);
+            }
+            L.k_code[t][tok_row(L, b, h, dst_tok0 + tau) * words + w] = static_cast<int32_t>(word);
+        }
+        const int w16 = L.k_width[3];
+        if (w16 > 0) {
+            const int cnt = L.tier_count[3][h];
+            for (int idx = tid; idx < kFastP * w16; idx += kFastThreads) {
+                const int tau = idx / w16, j = idx - tau * w16;
+                uint16_t v = 0;
+                if (j < cnt) {
+                    const uint16_t raw = kpage[tau * kFastLd + L.tier_index[3][h * w16 + j]];
+                    v = IsHalf ? raw : f32_to_f16(bf16_to_f32(raw));
+                }
+                L.k_value16[tok_row(L, b, h, dst_tok0) * w16 + idx] = v;
+            }
+        }
+    }
+
+    // ---- phase 5: Values, one code word per thread (layout.py:115-129) ----
+    {
+        const int tk = tid >> 3, w = tid & 7;
+        const uint32_t* row = reinterpret_cast<const uint32_t*>(vpage + tk * kFastLd + 16 * w);
+        float v[16];
+        float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t pr = row[i];
+            v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr & 0xffffu));
+            v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr >> 16));
+            lo = fminf(lo, fminf(v[2 * i], v[2 * i + 1]));
+            hi = fmaxf(hi, fmaxf(v[2 * i], v[2 * i + 1]));
+        }
+        // the token's 8 threads are lanes 8k .. 8k + 7 of one wave
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            lo = fminf(lo, __shfl_xor(lo, off, kWave));
+            hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
+        }
+        const float sc = group_scale(hi, lo, 3);
+        const float y = 1.0f / sc;
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float q = __builtin_rintf(div_rn(v[i] - lo, sc, y));
+            word |= static_cast<uint32_t>(fminf(fmaxf(q, 0.0f), 3.0f)) << (2 * i);
+        }
+        const int64_t trow = tok_row(L, b, h, dst_tok0 + tk);
+        L.v_code[trow * (D / 16) + w] = static_cast<int32_t>(word);
+        if (w == 0) {
+            L.v_scale[trow] = f32_to_f16(sc);
+            L.v_min[trow] = f32_to_f16(lo);
+        }
+    }
+}
+
+bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
+    return vec16 && src_dtype != LF_FP32 && L.head_dim == 128 && L.page_size == kFastP && L.k_group == kFastP &&
+           L.v_group == 128 && L.bit_v == 2 && L.v_groups == 1 && L.v_words == 8;
+}
+
+size_t pack_fast_lds_bytes(const lf_packed_layer& L) {
+    const int cw = (pack_code_row(L) + 3) & ~3;
+    return 2 * static_cast<size_t>(kFastP) * kFastLd * 2 + 2 * 8 * 128 * 4 + static_cast<size_t>(cw) * 16 + 128 * 2 +
+           static_cast<size_t>(kFastP) * cw + 16;
+}
+
 int pack_code_row(const lf_packed_layer& L) {
     const int wsum = L.k_width[0] + L.k_width[1] + L.k_width[2];
     return wsum > L.head_dim ? wsum : L.head_dim;
@@ -337,9 +580,29 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
     a.vec16 = ((kp | vp) % 16 == 0) && ((sb * elem) % 16 == 0) && ((sh * elem) % 16 == 0) &&
               ((st * elem) % 16 == 0);
     a.cw = pack_code_row(L);
+    dim3 grid(n_jobs, L.n_kv);
+    if (pack_fast_ok(L, src_dtype, a.vec16 != 0)) {
+        a.cw = (pack_code_row(L) + 3) & ~3;
+        const size_t lds = pack_fast_lds_bytes(L);
+        if (lds <= 160 * 1024) {
+            static size_t fast_limit[2] = {64 * 1024, 64 * 1024};
+            const int half = src_dtype == LF_FP16;
+            const void* fn = half ? reinterpret_cast<const void*>(&pack_fast_kernel<true>)
+                                  : reinterpret_cast<const void*>(&pack_fast_kernel<false>);
+            if (lds > fast_limit[half]) {
+                const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         static_cast<int>(lds));
+                if (e != hipSuccess) return static_cast<int>(e);
+                fast_limit[half] = lds;
+            }
+            if (half) hipLaunchKernelGGL(pack_fast_kernel<true>, grid, dim3(kFastThreads), lds, stream, a);
+            else hipLaunchKernelGGL(pack_fast_kernel<false>, grid, dim3(kFastThreads), lds, stream, a);
+            const hipError_t err = hipGetLastError();
+            return err == hipSuccess ? LF_OK : static_cast<int>(err);
+        }
+    }
     const size_t lds = pack_lds_bytes(L, elem);
     if (lds > 160 * 1024) return LF_E_SHAPE;
-    dim3 grid(n_jobs, L.n_kv);
     int rc;
     if (src_dtype == LF_BF16) rc = launch_one<uint16_t, false>(a, grid, lds, stream);
     else if (src_dtype == LF_FP16) rc = launch_one<uint16_t, true>(a, grid, lds, stream);

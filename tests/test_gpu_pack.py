@@ -80,6 +80,31 @@ def test_edge_values_bit_exact(gpu):
     assert_history_equal(mgr.layers[0], 0, store)
 
 
+def test_edge_values_bit_exact_128(gpu):
+    """The same edge cases at the common shape (D 128, page = groups = 128, int2 Values: the
+    1024-thread page-compress path), plus a Value row with a huge range."""
+    D, T = 128, 256
+    levels = np.tile(np.array([0, 1, 2, 3, 0, 0, 1, 0]), 16)[None].repeat(2, 0)
+    key = torch.randn(1, 2, T, D) * 3
+    key[0, 0, :128, 0] = 7.0                                  # constant int2 group
+    key[0, 0, :, 1] = torch.linspace(-3e5, 3e5, T)           # int4, range > fp16 max * 15
+    key[0, 0, :, 4] = torch.tensor([0.0, 0.5, 1.5, 2.5, 3.0] * 51 + [0.0])   # int2 ties
+    key[0, 1, :, 0] = torch.randn(T) * 1e-30                 # tiny
+    key[0, 1, :, 3] = torch.randn(T) * 1e5                   # fp16 tier overflows
+    key[0, 1, :, 7] = -0.0
+    key[0, 1, 5, 8] = 3e38                                    # range overflows float: a = inf
+    key[0, 1, 6, 8] = -3e38
+    key = key.bfloat16()
+    value = (torch.randn(1, 2, T, D) * torch.logspace(-6, 6, D)).bfloat16()
+    value[0, 0, 3] = 1.0
+    value[0, 1, 9, :64] = 2e38
+    value[0, 1, 9, 64:] = -2e38
+    mgr = PackedKVManager([levels], 2, 2, D, 128, 128, 128, 2, gpu)
+    mgr.commit(0, key.to(gpu), value.to(gpu))
+    store = oracle_store(levels, f32(key[0]), f32(value[0]), 128, 128, 128, 2)
+    assert_history_equal(mgr.layers[0], 0, store)
+
+
 def test_division_sensitive_ties_on_device(gpu):
     """Groups where (x-lo)/s is exactly k+0.5 after IEEE division (x*(1/s) would round up)."""
     cases = [(1081804425, 1135190891), (1090252937, 1154556202), (1092564827, 1153771404)]
