@@ -298,11 +298,12 @@ int pack_code_row(const lf_packed_layer& L);
 
 // ---------------------------------------------------------------------------------------
 // Fast path for the common shape: page = Key group = Value group = head_dim = 128, int2
-// Values, 2-byte inputs with 16-byte aligned rows.  1024 threads per page so a page is
-// packed with enough waves in flight; per element the division uses a correctly rounded
-// reciprocal of the group scale and one Markstein correction (see div_rn).
+// Values, 2-byte inputs with 16-byte aligned rows.  Two workgroups of 1024 threads per page
+// and kv head (blockIdx.z 0: Key page, 1: Value page), so two run on a CU; per element the
+// division uses a correctly rounded reciprocal of the group scale and one Markstein
+// correction (see div_rn).
 //
-//   stage     both pages into LDS (rows padded to 130 halves)
+//   stage     the page into LDS (rows padded to 130 halves)
 //   phase 1   Key min/max: thread (channel tid % 128, tokens 16 (tid / 128) + 0..15); the 16
 //             values stay in registers
 //   phase 2   per integer-tier slot: group min, scale, reciprocal; scale/min stored
@@ -328,6 +329,47 @@ __device__ __forceinline__ float div_rn(float a, float s, float y) {
     return q;
 }
 
+// Phase 5 of the fast path: Values, one code word per thread (layout.py:115-129).
+template <bool IsHalf>
+__device__ __forceinline__ void pack_value_page(const lf_packed_layer& L, const uint16_t* vpage, int b, int h,
+                                                int64_t dst_tok0, int tid) {
+    constexpr int D = 128;
+    {
+        const int tk = tid >> 3, w = tid & 7;
+        const uint32_t* row = reinterpret_cast<const uint32_t*>(vpage + tk * kFastLd + 16 * w);
+        float v[16];
+        float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t pr = row[i];
+            v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr & 0xffffu));
+            v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr >> 16));
+            lo = fminf(lo, fminf(v[2 * i], v[2 * i + 1]));
+            hi = fmaxf(hi, fmaxf(v[2 * i], v[2 * i + 1]));
+        }
+        // the token's 8 threads are lanes 8k .. 8k + 7 of one wave
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            lo = fminf(lo, __shfl_xor(lo, off, kWave));
+            hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
+        }
+        const float sc = group_scale(hi, lo, 3);
+        const float y = 1.0f / sc;
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float q = __builtin_rintf(div_rn(v[i] - lo, sc, y));
+            word |= static_cast<uint32_t>(fminf(fmaxf(q, 0.0f), 3.0f)) << (2 * i);
+        }
+        const int64_t trow = tok_row(L, b, h, dst_tok0 + tk);
+        L.v_code[trow * (D / 16) + w] = static_cast<int32_t>(word);
+        if (w == 0) {
+            L.v_scale[trow] = f32_to_f16(sc);
+            L.v_min[trow] = f32_to_f16(lo);
+        }
+    }
+}
+
 template <bool IsHalf>
 __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) {
     const lf_packed_layer& L = a.L;
@@ -341,9 +383,9 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
     constexpr int D = 128;
 
     extern __shared__ __align__(16) unsigned char smem[];
-    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                       // [128][130]
-    uint16_t* vpage = kpage + kFastP * kFastLd;                                 // [128][130]
-    float* pmin = reinterpret_cast<float*>(vpage + kFastP * kFastLd);           // [8][128]
+    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                       // [128][130] (Key or Value page)
+    uint16_t* vpage = kpage;
+    float* pmin = reinterpret_cast<float*>(kpage + kFastP * kFastLd);           // [8][128]
     float* pmax = pmin + 8 * D;                                                 // [8][128]
     float4* prm = reinterpret_cast<float4*>(pmax + 8 * D);                      // [cw] lo, s, y, -
     int16_t* chslot = reinterpret_cast<int16_t*>(prm + a.cw);                   // [128] slot of a channel, -1
@@ -357,33 +399,38 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
     koff[3] = koff[2] + L.k_width[2];
     const int nslots = koff[3];
 
-    // ---- stage both pages; channel -> integer slot map (layout.py:49-68) ----
+    const bool value_part = blockIdx.z != 0;
+
+    // ---- stage the page; channel -> integer slot map (layout.py:49-68) ----
     {
-        const uint16_t* ks = static_cast<const uint16_t*>(a.k_src) + b * a.sb + h * a.sh + tok0 * a.st;
-        const uint16_t* vs = static_cast<const uint16_t*>(a.v_src) + b * a.sb + h * a.sh + tok0 * a.st;
-        uint4 kv[2], vv[2];
+        const uint16_t* src = static_cast<const uint16_t*>(value_part ? a.v_src : a.k_src) + b * a.sb + h * a.sh +
+                              tok0 * a.st;
+        uint4 kv[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + kFastThreads * i;  // 16-byte chunk: row idx / 16, column 8 (idx % 16)
-            kv[i] = *reinterpret_cast<const uint4*>(ks + (idx >> 4) * a.st + 8 * (idx & 15));
-            vv[i] = *reinterpret_cast<const uint4*>(vs + (idx >> 4) * a.st + 8 * (idx & 15));
+            kv[i] = *reinterpret_cast<const uint4*>(src + (idx >> 4) * a.st + 8 * (idx & 15));
         }
-        if (tid < D) chslot[tid] = -1;
-        __syncthreads();
-        for (int t = 0; t < 3; ++t) {
-            const int cnt = L.k_width[t] ? L.tier_count[t][h] : 0;
-            for (int j = tid; j < cnt; j += kFastThreads)
-                chslot[L.tier_index[t][h * L.k_width[t] + j]] = static_cast<int16_t>(koff[t] + j);
+        if (!value_part) {
+            if (tid < D) chslot[tid] = -1;
+            __syncthreads();
+            for (int t = 0; t < 3; ++t) {
+                const int cnt = L.k_width[t] ? L.tier_count[t][h] : 0;
+                for (int j = tid; j < cnt; j += kFastThreads)
+                    chslot[L.tier_index[t][h * L.k_width[t] + j]] = static_cast<int16_t>(koff[t] + j);
+            }
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + kFastThreads * i;
             uint32_t* kd = reinterpret_cast<uint32_t*>(kpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
-            uint32_t* vd = reinterpret_cast<uint32_t*>(vpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
             kd[0] = kv[i].x; kd[1] = kv[i].y; kd[2] = kv[i].z; kd[3] = kv[i].w;
-            vd[0] = vv[i].x; vd[1] = vv[i].y; vd[2] = vv[i].z; vd[3] = vv[i].w;
         }
         __syncthreads();
+    }
+    if (value_part) {
+        pack_value_page<IsHalf>(L, vpage, b, h, dst_tok0, tid);
+        return;
     }
 
     // ---- phase 1: Key min/max of channel c over tokens 16 ck .. 16 ck + 15 ----
@@ -489,41 +536,6 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
         }
     }
 
-    // ---- phase 5: Values, one code word per thread (layout.py:115-129) ----
-    {
-        const int tk = tid >> 3, w = tid & 7;
-        const uint32_t* row = reinterpret_cast<const uint32_t*>(vpage + tk * kFastLd + 16 * w);
-        float v[16];
-        float lo = __builtin_inff(), hi = -__builtin_inff();
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t pr = row[i];
-            v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr & 0xffffu));
-            v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr >> 16));
-            lo = fminf(lo, fminf(v[2 * i], v[2 * i + 1]));
-            hi = fmaxf(hi, fmaxf(v[2 * i], v[2 * i + 1]));
-        }
-        // the token's 8 threads are lanes 8k .. 8k + 7 of one wave
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            lo = fminf(lo, __shfl_xor(lo, off, kWave));
-            hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
-        }
-        const float sc = group_scale(hi, lo, 3);
-        const float y = 1.0f / sc;
-        uint32_t word = 0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float q = __builtin_rintf(div_rn(v[i] - lo, sc, y));
-            word |= static_cast<uint32_t>(fminf(fmaxf(q, 0.0f), 3.0f)) << (2 * i);
-        }
-        const int64_t trow = tok_row(L, b, h, dst_tok0 + tk);
-        L.v_code[trow * (D / 16) + w] = static_cast<int32_t>(word);
-        if (w == 0) {
-            L.v_scale[trow] = f32_to_f16(sc);
-            L.v_min[trow] = f32_to_f16(lo);
-        }
-    }
 }
 
 bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
@@ -533,7 +545,7 @@ bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
 
 size_t pack_fast_lds_bytes(const lf_packed_layer& L) {
     const int cw = (pack_code_row(L) + 3) & ~3;
-    return 2 * static_cast<size_t>(kFastP) * kFastLd * 2 + 2 * 8 * 128 * 4 + static_cast<size_t>(cw) * 16 + 128 * 2 +
+    return static_cast<size_t>(kFastP) * kFastLd * 2 + 2 * 8 * 128 * 4 + static_cast<size_t>(cw) * 16 + 128 * 2 +
            static_cast<size_t>(kFastP) * cw + 16;
 }
 
@@ -595,8 +607,9 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
                 if (e != hipSuccess) return static_cast<int>(e);
                 fast_limit[half] = lds;
             }
-            if (half) hipLaunchKernelGGL(pack_fast_kernel<true>, grid, dim3(kFastThreads), lds, stream, a);
-            else hipLaunchKernelGGL(pack_fast_kernel<false>, grid, dim3(kFastThreads), lds, stream, a);
+            const dim3 grid2(n_jobs, L.n_kv, 2);  // z: Key page, Value page
+            if (half) hipLaunchKernelGGL(pack_fast_kernel<true>, grid2, dim3(kFastThreads), lds, stream, a);
+            else hipLaunchKernelGGL(pack_fast_kernel<false>, grid2, dim3(kFastThreads), lds, stream, a);
             const hipError_t err = hipGetLastError();
             return err == hipSuccess ? LF_OK : static_cast<int>(err);
         }
