@@ -79,14 +79,14 @@ struct MfmaLayout {
                          // fp16-tier rows at 4608, padded to whole DMA blocks):
                          // [n_kslots] u32 Key scale / min page pairs
     int rawb_bytes;
-    int ck_v16;          // prepared: [128][w16p] fp16 Key fp16 tier, zero padded (after Qs)
+    int ck_v16;          // prepared: [128][w16p] fp16 Key fp16 tier, zero padded (after Qs), one spare dword
     int ck_bytes;
     int off_qperm;       // [nb][8 heads][8] fp32: q * scaling*log2e per slot (0 for padding)
     int off_tt;          // int16 tier table of this kv head (ranks -> channel ids), tiers back to back
     int off_small;       // alpha [waves][8], wave m/l/mid [waves][3][8]
-    int off_ck;          // two prepared buffers
-    int off_rawa;        // three Key-code buffers
-    int off_rawb;        // two rest buffers (prepared + Key-code + rest buffers form one alias region)
+    int slot_bytes;      // one page slot: Key-code buffer, then rest buffer
+    int off_ck;          // the prepared buffer
+    int off_raw;         // two page slots (prepared buffer + page slots form one alias region)
     int lds_bytes;
 };
 
@@ -104,6 +104,10 @@ __device__ __forceinline__ void dma_barrier(int n) {
     }
 #undef LF_W
 }
+
+// s_waitcnt lgkmcnt(0); s_barrier: every wave's LDS operations are done; DMA in flight stays
+// in flight (__syncthreads would also wait for it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // a[t] for a run-time t in 0..3 (or 0..2) through selects: a dynamic index into the kernel
 // argument would copy the whole argument block to scratch memory.
@@ -223,16 +227,16 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a0, uint32_t a1, uint32
 // spills and reloads the tuple whole inside the page loop.
 struct LoopY {
     int kst0, kst1, kst2, kst3, kf1, kf2, kf3, nb, nb_int, w16p;
-    int seg0, seg1, ja, rawa_bytes, rawb_ks, rawb_bytes, ck_v16, ck_bytes, n_kslots;
+    int seg0, seg1, ja, rawa_bytes, rawb_ks, slot_bytes, ck_v16, n_kslots;
 };
 
 __device__ __forceinline__ LoopY loop_y(const MfmaLayout& y) {
     LoopY z{y.kst[0], y.kst[1], y.kst[2], y.kst[3], y.kfirst[1], y.kfirst[2], y.kfirst[3], y.nb, y.nb_int, y.w16p,
-            y.seg_end[0], y.seg_end[1], y.ja, y.rawa_bytes, y.rawb_ks, y.rawb_bytes, y.ck_v16, y.ck_bytes, y.n_kslots};
+            y.seg_end[0], y.seg_end[1], y.ja, y.rawa_bytes, y.rawb_ks, y.slot_bytes, y.ck_v16, y.n_kslots};
     asm volatile("" : "+s"(z.kst0), "+s"(z.kst1), "+s"(z.kst2), "+s"(z.kst3), "+s"(z.kf1), "+s"(z.kf2), "+s"(z.kf3),
                       "+s"(z.nb), "+s"(z.nb_int), "+s"(z.w16p));
     asm volatile("" : "+s"(z.seg0), "+s"(z.seg1), "+s"(z.ja), "+s"(z.rawa_bytes), "+s"(z.rawb_ks),
-                      "+s"(z.rawb_bytes), "+s"(z.ck_v16), "+s"(z.ck_bytes), "+s"(z.n_kslots));
+                      "+s"(z.slot_bytes), "+s"(z.ck_v16), "+s"(z.n_kslots));
     return z;
 }
 
@@ -403,31 +407,30 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
     s.per_page = s.n_chunk + s.n_ks;
 }
 
-// Issue the DMA of page ``page``: region A into the Key-code buffer at LDS address ``rawa``,
-// region B and the slots into the rest buffer at ``rawb`` (32-bit LDS addresses); advance
-// the sources one page.
-__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t rawa, uint32_t rawb, const LoopY& z, int page,
-                                         int wave) {
-    // The per-instruction conditions and addresses are cheap scalar work; passing their inputs
-    // through an empty asm keeps the compiler from hoisting one register per instruction out
-    // of the page loop (which would exhaust the scalar registers).
-    int n_chunk = s.n_chunk, n_ks = s.n_ks, ja = z.ja, jw = wave;
-    asm volatile("" : "+s"(n_chunk), "+s"(n_ks), "+s"(ja), "+s"(jw));
+// Issue the DMA of page ``page`` into the page slot at LDS address ``slot`` (32-bit): block j
+// of region A lands at 1024 j, block j of region B at rawa_bytes + 1024 j = 1024 (ja + j), so
+// this wave's i-th 16-byte instruction (block wave + 4 i overall) lands at 1024 (wave + 4 i);
+// the slot dwords follow region B at rawa_bytes + rawb_ks.  The sources advance one page.
+__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t slot, const LoopY& z, int page, int wave) {
+    // The counts pass through an empty asm so the compiler keeps one compare per instruction
+    // instead of hoisting per-instruction conditions out of the page loop.
+    int n_chunk = __builtin_amdgcn_readfirstlane(s.n_chunk), n_ks = __builtin_amdgcn_readfirstlane(s.n_ks);
+    asm volatile("" : "+s"(n_chunk), "+s"(n_ks));
+    const uint32_t d16 = slot + 1024 * wave;
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
         if (i < n_chunk) {
-            const int j = kWaves * i + jw;
-            const uint32_t dst = j < ja ? rawa + 1024 * j : rawb + 1024 * (j - ja);
-            dma16(s.chunk[i], dst);
+            dma16(s.chunk[i], d16 + 4096 * i);
             s.chunk[i] += s.chunk_stride[i];
         }
     }
-    const uint32_t ksd = rawb + z.rawb_ks + jw * 256;
+    const uint32_t d4 = slot + z.rawa_bytes + z.rawb_ks + 256 * wave;
+    const uint32_t step = (page & 1) * 4;  // a slot dword holds pages (p & ~1, p | 1)
 #pragma unroll
     for (int i = 0; i < kMaxKsDma; ++i) {
         if (i < n_ks) {
-            dma4(s.ks[i], ksd + kWaves * 256 * i);
-            if (page & 1) s.ks[i] += 4;
+            dma4(s.ks[i], d4 + kWaves * 256 * i);
+            s.ks[i] += step;
         }
     }
 }
@@ -452,7 +455,7 @@ struct PrepRegs {
 // two halves each.  Offsets are fixed per layer, so they are computed once.
 struct F16Map {
     int src[2];      // byte offset of the dword's first half in the rest buffer (0 when unused)
-    int dst[2];      // byte offset of the dword in the prepared buffer, -1 past the end
+    int dst[2];      // byte offset of the dword in the prepared buffer (the spare dword past the end)
     uint32_t keep[2];  // 0xffff for each half that exists, else 0
 };
 
@@ -466,7 +469,7 @@ __device__ __forceinline__ F16Map f16_map(const LoopY& z, int w16, int tid) {
         const bool live = hw && t < kPage;
         const bool lo = live && 2 * c < w16, hi = live && 2 * c + 1 < w16;
         m.src[i] = lo ? kRawbF16 + 2 * (t * w16 + 2 * c) : 0;
-        m.dst[i] = live ? z.ck_v16 + 4 * d : -1;
+        m.dst[i] = z.ck_v16 + 4 * (live ? d : kPage * hw);  // past the end: the spare dword after the rows
         m.keep[i] = (lo ? 0xffffu : 0u) | (hi ? 0xffff0000u : 0u);
     }
     return m;
@@ -529,19 +532,17 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
     }
     {
         // Value scale and the per-token constant vmin - 4 * vscale (4: the offset of the
-        // Value-code unpack) of token tid / 2: computed by every thread, stored by the even ones
+        // Value-code unpack) of token tid / 2, stored by both threads of the pair (the same
+        // values; no branch, so the reads above stay in one batch)
         const int t = tid >> 1;
         const float s = f16_to_f32(static_cast<uint16_t>(r.vs));
         const float mid = fmaf(-4.f, s, f16_to_f32(static_cast<uint16_t>(r.vm)));
-        if ((tid & 1) == 0) {
-            reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
-            reinterpret_cast<float*>(ck + kCkVmid)[t] = mid;
-        }
+        reinterpret_cast<float*>(ck + kCkVsc)[t] = s;
+        reinterpret_cast<float*>(ck + kCkVmid)[t] = mid;
     }
     // fp16-tier repack: dwords tid and tid + 256, then (rows wider than 8) the rest
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-        if (fm.dst[i] >= 0) *reinterpret_cast<uint32_t*>(ck + fm.dst[i]) = (r.f16[i][0] | (r.f16[i][1] << 16)) & fm.keep[i];
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint32_t*>(ck + fm.dst[i]) = (r.f16[i][0] | (r.f16[i][1] << 16)) & fm.keep[i];
     const int hw = z.w16p >> 1;
     if (kPage * hw > 512) {
         for (int d = tid + 512; d < kPage * hw; d += 256) {
@@ -763,18 +764,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
 
     if (kind != 1) {
         // ---- pages (kind 0, 2) ----
-        // The first two pages' DMA goes out first; q, the tier table and the permuted q are
-        // built while it is in flight (the DMA targets do not overlap q).
+        // The first page's DMA goes out first; q, the tier table and the permuted q are built
+        // while it is in flight (the DMA target does not overlap q).
         const LoopY z = loop_y(y);
         DmaSrc ds;
         dma_setup(ds, L, y, b, h, pbeg, wave, lane);
-        unsigned char* rawa0 = smem + y.off_rawa;
-        unsigned char* rawb0 = smem + y.off_rawb;
-        unsigned char* ck0 = smem + y.off_ck;
-        const uint32_t lds0 = lds_addr(smem);  // LDS address of smem
-        const uint32_t rawa_lds = lds0 + y.off_rawa, rawb_lds = lds0 + y.off_rawb;
-        dma_page(ds, rawa_lds, rawb_lds, z, pbeg, wave);
-        if (pbeg + 1 < pend) dma_page(ds, rawa_lds + z.rawa_bytes, rawb_lds + z.rawb_bytes, z, pbeg + 1, wave);
+        unsigned char* raw0 = smem + y.off_raw;
+        unsigned char* ck = smem + y.off_ck;
+        const uint32_t raw_lds = lds_addr(smem) + y.off_raw;  // LDS address of page slot 0
+        dma_page(ds, raw_lds, z, pbeg, wave);
 
         // ---- q (scaled into the log2 domain) and this head's tier table ----
         int16_t* tt = reinterpret_cast<int16_t*>(smem + y.off_tt);
@@ -789,9 +787,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                                                  : int16_t(-1);
         }
         __syncthreads();
-        // q permuted into slot order (0 for padding slots and heads >= g).  The fp16 tier's Qs
-        // is this q (hi / lo) on every page: set once in both prepared buffers, as are the zero
-        // Qs rows of heads >= g in the integer tiers.
+        // q permuted into slot order (0 for padding slots and heads >= g), integer tiers only.
+        // The fp16 tier's Qs is this q (hi / lo) on every page: set once in the prepared buffer,
+        // as are the zero Qs rows of heads >= g in the integer tiers.
         for (int e = tid; e < y.nb * 64; e += kThreads) {
             const int gb = e >> 6, n = (e >> 3) & 7, pos = e & 7;
             const int tier = gb >= 4 * y.kfirst[3] ? 3 : gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
@@ -804,45 +802,59 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     if (c >= 0) v = qlin[n * kD + c];
                 }
             }
-            qperm[e] = v;
+            if (gb < y.nb_int) qperm[e] = v;
             if (gb >= y.nb_int || n >= g) {
                 const _Float16 hv = static_cast<_Float16>(v);
                 const _Float16 lv = static_cast<_Float16>(v - static_cast<float>(hv));
-#pragma unroll
-                for (int buf = 0; buf < 2; ++buf) {
-                    _Float16* qs = reinterpret_cast<_Float16*>(ck0 + buf * y.ck_bytes + kCkQs);
-                    qs[(gb * 16 + n) * 8 + pos] = hv;
-                    qs[(gb * 16 + 8 + n) * 8 + pos] = lv;
-                }
+                _Float16* qs = reinterpret_cast<_Float16*>(ck + kCkQs);
+                qs[(gb * 16 + n) * 8 + pos] = hv;
+                qs[(gb * 16 + 8 + n) * 8 + pos] = lv;
             }
         }
-        __syncthreads();  // qlin (aliased by prepared buffer 0) is dead from here on
         const int w16 = L.k_width[3];
-        dma_barrier(pbeg + 1 < pend ? ds.per_page : 0);  // page pbeg landed (every wave's share)
         const F16Map fm = f16_map(z, w16, tid);
-        prepare_page(z, fm, rawb0, ck0, qperm, pbeg, g, w16, tid, wave);
-
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
         const int sh = 2 * (n16 & 3);
         const int tok0 = 32 * wave + n16, tok1 = tok0 + 16;
         for (int page = pbeg; page < pend; ++page) {
             const int rel = page - pbeg;
-            // Page + 1 landed; page prepared; page - 1 computed, so its Key-code buffer and
-            // prepared buffer are free, and page's rest buffer was consumed by its preparation.
+            // Page landed (every wave's share) and page - 1 computed: the prepared buffer and
+            // page - 1's slot are free.  (On the first page this also orders the set-up above:
+            // qlin, which the prepared buffer aliases, is dead from here on.)
             dma_barrier(0);
-            if (page + 2 < pend)
-                dma_page(ds, rawa_lds + ((rel + 2) % 3) * z.rawa_bytes, rawb_lds + (rel & 1) * z.rawb_bytes, z, page + 2,
-                         wave);
-            // page + 1's rest buffer landed at the barrier: its reads go out now, so their latency
-            // hides behind this page's compute; its prepared buffer is written after the compute
-            const bool prep_next = page + 1 < pend;
-            const unsigned char* raw_next = rawb0 + ((rel + 1) & 1) * z.rawb_bytes;
+            // The preparation reads go out first; page + 1's DMA is issued while they are in
+            // flight (a DMA instruction can wait for the address unit, shared by the CU's waves).
+            const unsigned char* raw = raw0 + (rel & 1) * z.slot_bytes;
             PrepRegs pr;
-            if (prep_next) prep_load(z, fm, raw_next, qperm, g, tid, wave, pr);
-            // ---- compute page ``page`` from its prepared buffer and Key codes ----
-            const unsigned char* raw = rawa0 + (rel % 3) * z.rawa_bytes;
-            const unsigned char* ck = ck0 + (rel & 1) * z.ck_bytes;
+            prep_load(z, fm, raw + z.rawa_bytes, qperm, g, tid, wave, pr);
+            if (page + 1 < pend) dma_page(ds, raw_lds + ((rel + 1) & 1) * z.slot_bytes, z, page + 1, wave);
+            prep_store(z, fm, pr, raw + z.rawa_bytes, ck, qperm, page, g, w16, tid, wave);
+            lds_barrier();  // page prepared
+            // ---- compute page ``page`` from the prepared buffer and its Key codes ----
             const half8* qs = reinterpret_cast<const half8*>(ck + kCkQs);
+            // Value codes of the lane's 8 tokens for channel 16*nt + n16 (unpacked just before their
+            // product): code bits to mantissa 8..9 under exponent
+            // 4, value 4 + c (the offset is folded into the per-token constant); tokens (0, 2) sit at
+            // byte bits sh, (1, 3) at 8 + sh
+            uint32_t dlo[8], dhi[8];
+            {
+                const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + kCkVt);
+                const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
+                const uint4 d0b = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8 + 4);
+                const uint4 d1a = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8);
+                const uint4 d1b = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8 + 4);
+                dlo[0] = d0a.x; dlo[1] = d0a.y; dlo[2] = d0a.z; dlo[3] = d0a.w;
+                dlo[4] = d0b.x; dlo[5] = d0b.y; dlo[6] = d0b.z; dlo[7] = d0b.w;
+                dhi[0] = d1a.x; dhi[1] = d1a.y; dhi[2] = d1a.z; dhi[3] = d1a.w;
+                dhi[4] = d1b.x; dhi[5] = d1b.y; dhi[6] = d1b.z; dhi[7] = d1b.w;
+            }
+            // The page's other compute-phase reads go out with the score operands: bias partials,
+            // Value scale and midpoint constant of the lane's four tokens.
+            const bool lo_lane = n16 >= 8;
+            const int tokl = 32 * wave + (lo_lane ? 16 : 0) + 4 * kb;  // the lane's first token
+            const float4 bp = reinterpret_cast<const float4*>(ck + kCkBias)[n16 & 7];
+            const float4 vs = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ck + kCkVsc) + tokl);
+            const float4 vd = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ck + kCkVmid) + tokl);
             // Integer tiers read up to 7 dwords past their segment (inside the LDS allocation):
             // those blocks have Qs == 0 and unpack to finite values.
             float4v acc0, acc1;
@@ -857,31 +869,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 else
                     score_tiles(kt, z, kv, acc0, acc1);
             }
-            // Value codes of the lane's 8 tokens for channel 16*nt + n16, unpacked while the score
-            // MFMAs drain: code bits to mantissa 8..9 under exponent 4, value 4 + c (the offset is
-            // folded into the per-token constant); tokens (0, 2) sit at byte bits sh, (1, 3) at 8 + sh
-            uint4 bu[8];
-            {
-                const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + kCkVt);
-                const uint4 d0a = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8);
-                const uint4 d0b = *reinterpret_cast<const uint4*>(vt + (8 * wave + kb) * 36 + (n16 >> 2) * 8 + 4);
-                const uint4 d1a = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8);
-                const uint4 d1b = *reinterpret_cast<const uint4*>(vt + (8 * wave + 4 + kb) * 36 + (n16 >> 2) * 8 + 4);
-                const uint32_t dlo[8] = {d0a.x, d0a.y, d0a.z, d0a.w, d0b.x, d0b.y, d0b.z, d0b.w};
-                const uint32_t dhi[8] = {d1a.x, d1a.y, d1a.z, d1a.w, d1b.x, d1b.y, d1b.z, d1b.w};
-#pragma unroll
-                for (int nt = 0; nt < 8; ++nt) {
-                    bu[nt].x = bfi(dlo[nt] << (8 - sh), kv.m2hi, kv.e4);
-                    bu[nt].y = bfi(dlo[nt] >> sh, kv.m2hi, kv.e4);
-                    bu[nt].z = bfi(dhi[nt] << (8 - sh), kv.m2hi, kv.e4);
-                    bu[nt].w = bfi(dhi[nt] >> sh, kv.m2hi, kv.e4);
-                }
-            }
             // ---- online softmax (log2 domain), compact: lane n16 < 8 takes tile 0 and lane n16 + 8
             // tile 1 of head n16 % 8, four tokens each; the hi and lo columns meet through
             // row_ror:8.  The accumulator elements are copied to scalars before the DPP move:
             // applied to vector elements directly, this compiler emits one move for all of them.
-            const bool lo_lane = n16 >= 8;
             float sv[4];
             {
                 const float a0[4] = {acc0[0], acc0[1], acc0[2], acc0[3]};
@@ -893,11 +884,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     sv[r] = own + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, send, 0x128, 0xf, 0xf, false));
                 }
             }
-            float bias;
-            {
-                const float4 bp = reinterpret_cast<const float4*>(ck + kCkBias)[n16 & 7];
-                bias = (bp.x + bp.y) + (bp.z + bp.w);
-            }
+            const float bias = (bp.x + bp.y) + (bp.z + bp.w);
             float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
             mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), 0x128,
                                                                                   0xf, 0xf, false)));
@@ -909,9 +896,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             const bool grow = m_cand > m_run + kLazyRescale;
             const float m_new = grow ? m_cand : m_run;
             const float m_off = m_new - bias;  // p = 2^(sv + bias - m_new)
-            const int tokl = 32 * wave + (lo_lane ? 16 : 0) + 4 * kb;  // the lane's first token
-            const float4 vs = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ck + kCkVsc) + tokl);
-            const float4 vd = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ck + kCkVmid) + tokl);
             float pp[4];
             float psum, pmid;
             {
@@ -971,16 +955,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             m_run = m_new;
             l_run += psum;
             mid_run += pmid;
-            // ---- value product: codes of the lane's 8 tokens (unpacked above), channel 16*nt + n16 ----
+            // ---- value product: codes of the lane's 8 tokens, channel 16*nt + n16 ----
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
+                const uint4 bu = {bfi(dlo[nt] << (8 - sh), kv.m2hi, kv.e4), bfi(dlo[nt] >> sh, kv.m2hi, kv.e4),
+                                  bfi(dhi[nt] << (8 - sh), kv.m2hi, kv.e4), bfi(dhi[nt] >> sh, kv.m2hi, kv.e4)};
                 float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
-                o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu[nt]), o4, 0, 0, 0);
+                o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }
-            // ---- page + 1's prepared buffer ----
-            if (prep_next)
-                prep_store(z, fm, pr, raw_next, ck0 + ((rel + 1) & 1) * z.ck_bytes, qperm, page + 1, g, w16, tid, wave);
         }
         // Reduce l and the midpoint term over the two tiles (lanes n16, n16 ^ 8) and the 4 lane
         // groups of each head.
@@ -1221,23 +1204,22 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     y.rawb_bytes = y.rawb_ks + ((y.n_kslots + 63) / 64) * 256;
     // prepared buffer: fixed-offset parts, Qs [nb][16][8] fp16 at kCkQs, fp16-tier rows after it
     y.ck_v16 = kCkQs + y.nb * 16 * 16;
-    y.ck_bytes = round_up(y.ck_v16 + kPage * y.w16p * 2, 16);
+    y.ck_bytes = round_up(y.ck_v16 + kPage * y.w16p * 2 + 4, 16);  // + the spare dword of the repack
+    y.slot_bytes = y.rawa_bytes + y.rawb_bytes;
     int off = 0;
     y.off_qperm = off;
-    off += y.nb * 64 * 4;
+    off += y.nb_int * 64 * 4;
     y.off_tt = off;
     off += round_up(2 * (L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3]), 16);
     y.off_small = off;
     off += (kWaves * 8 + 2 * kWaves * 3 * 8) * 4;  // alpha, wave partial statistics
     off = round_up(off, 16);
     y.off_ck = off;
-    off += 2 * y.ck_bytes;
-    y.off_rawa = off;
-    off += 3 * y.rawa_bytes;
-    y.off_rawb = off;
-    off += 2 * y.rawb_bytes;
+    off += y.ck_bytes;
+    y.off_raw = off;
+    off += 2 * y.slot_bytes;
     // q [8][128], wave partial outputs [2 * waves][8][128] and residual probabilities
-    // [waves][32][8] alias the prepared, Key-code and rest buffers
+    // [waves][32][8] alias the prepared buffer and the page slots
     const int alias_bytes = (8 + 2 * kWaves * 8) * kD * 4 + kWaves * 32 * 8 * 4;
     if (off - y.off_ck < alias_bytes) off = y.off_ck + alias_bytes;
     y.lds_bytes = off;
