@@ -885,16 +885,36 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 }
             }
             const float bias = (bp.x + bp.y) + (bp.z + bp.w);
-            float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-            mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), 0x128,
-                                                                                  0xf, 0xf, false)));
-            mx = rows_max(mx);
-            // The reference point m_run moves only when the page's max exceeds it by more than
-            // kLazyRescale (probabilities stay below 2^kLazyRescale), so most pages skip the
-            // rescale of O and l.
-            const float m_cand = mx + bias;
-            const bool grow = m_cand > m_run + kLazyRescale;
-            const float m_new = grow ? m_cand : m_run;
+            // The reference point m_run moves only when some score of the page exceeds it by more
+            // than kLazyRescale (probabilities stay below 2^kLazyRescale).  Most pages have no such
+            // score: one ballot over the lanes' own maxima then skips the row maxima and the
+            // rescale of O and l.  (The first page always takes the long path: m_run = -inf.)
+            const float lmx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            float m_new = m_run;
+            if (__builtin_amdgcn_ballot_w64(lmx + bias > m_run + kLazyRescale)) {
+                float mx = fmaxf(lmx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, lmx),
+                                                                                              0x128, 0xf, 0xf, false)));
+                mx = rows_max(mx);
+                const float m_cand = mx + bias;
+                const bool grow = m_cand > m_run + kLazyRescale;
+                m_new = grow ? m_cand : m_run;
+                // Rescale O where a head's max moved: alpha of the 4 output rows this lane holds
+                // (rows 4*kb + r, head (4*kb + r) % 8); a same-wave LDS write then read is
+                // ordered by the LDS queue.
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
+                mid_run *= alpha;
+                if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = alpha;
+                __builtin_amdgcn_wave_barrier();
+                const float4 arow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * (kb & 1));
+#pragma unroll
+                for (int nt = 0; nt < 8; ++nt) {
+                    O[nt][0] *= arow.x;
+                    O[nt][1] *= arow.y;
+                    O[nt][2] *= arow.z;
+                    O[nt][3] *= arow.w;
+                }
+            }
             const float m_off = m_new - bias;  // p = 2^(sv + bias - m_new)
             float pp[4];
             float psum, pmid;
@@ -934,24 +954,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             au.z = lo_lane ? lp[0] : rv[0];
             au.w = lo_lane ? lp[1] : rv[1];
             const half8 ap = __builtin_bit_cast(half8, au);
-            // Rescale O when some head's max moved: alpha of the 4 output rows this lane holds
-            // (rows 4*kb + r, head (4*kb + r) % 8); a same-wave LDS write then read is ordered
-            // by the LDS queue.
-            if (__builtin_amdgcn_ballot_w64(n16 < 8 && grow)) {
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                l_run *= alpha;
-                mid_run *= alpha;
-                if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = alpha;
-                __builtin_amdgcn_wave_barrier();
-                const float4 arow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * (kb & 1));
-#pragma unroll
-                for (int nt = 0; nt < 8; ++nt) {
-                    O[nt][0] *= arow.x;
-                    O[nt][1] *= arow.y;
-                    O[nt][2] *= arow.z;
-                    O[nt][3] *= arow.w;
-                }
-            }
             m_run = m_new;
             l_run += psum;
             mid_run += pmid;

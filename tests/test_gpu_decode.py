@@ -194,3 +194,28 @@ def test_mfma_kernel_rejects_unsupported_shape(gpu):
     out = torch.empty_like(q)
     with pytest.raises(_native.LFError):
         decode_into(mgr, 0, q, q.clone(), q.clone(), 0.125, out, kernel=_native.KERNEL_MFMA)
+
+
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+@pytest.mark.parametrize("profile", ["ramp", "spike"])
+def test_score_growth_across_pages(gpu, kernel, profile):
+    """Keys scaled per token so the page maxima climb by far more than the kernels' lazy
+    rescale headroom (2^8) from page to page ("ramp"), or jump once mid-sequence and fall back
+    ("spike"): the running reference moves on later pages of one split item, so O, l and the
+    midpoint sums are rescaled inside the page loop, not only at the first page."""
+    n_q, n_kv, D, pages = 8, 2, 128, 24
+    T = pages * 128 + 40
+    d = synth.make_layer(2, n_q, n_kv, D, T, 2.5, seed=70)
+    t = torch.arange(T, dtype=torch.float32)
+    if profile == "ramp":
+        gain = 0.05 + 6.0 * t / T
+    else:
+        gain = torch.full((T,), 0.3)
+        gain[9 * 128:10 * 128] = 6.0
+    d.key = (d.key.float() * gain[None, None, :, None]).bfloat16()
+    d.query = (d.query.float() * 4.0).bfloat16()
+    mgr, lens = build(d, [pages, pages - 5], [40, 3], n_q, n_kv, D, gpu)
+    for pps in (64, 5):
+        out = run(mgr, d, gpu, D ** -0.5, KERNELS[kernel], pages_per_split=pps)
+        for b in range(2):
+            assert_decode_close(out[b], oracle_out(d, b, lens[b], n_q, n_kv, D ** -0.5))
