@@ -8,12 +8,11 @@
 //
 // Work: one workgroup of 4 waves per (split item, kv head); wave w computes
 // tokens 32w..32w+31 (two 16-token tiles) of every page of the item.  Pages arrive by LDS-DMA
-// (global_load_lds) two pages ahead of the page being computed: Key codes into
-// a ring of three LDS buffers, everything else into a ring of two.  Each page
-// is "prepared" (the per-page operands below) into one of two prepared buffers
-// one page ahead of its compute, so one barrier per page separates DMA,
-// preparation and compute of consecutive pages.  Partials (m, l, o) of each
-// item go to the workspace; decode_reduce_kernel merges them.
+// (global_load_lds) into a ring of two page slots, one page ahead of the page being computed.
+// Per page: a barrier (the page landed, the previous page is computed), the page's
+// "preparation" (the per-page operands below) into the one prepared buffer by all waves, a
+// second barrier, then the compute.  Partials (m, l, o) of each item go to the workspace;
+// decode_reduce_kernel merges them.  (A third slot, two pages in flight, measured no faster.)
 //
 // Scores.  With the Key scale folded into the query once per page,
 //     s[t][i] = sum_slot Qs[i][slot] * code[t][slot] + sum_c q_ic * min_c,
@@ -832,10 +831,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             lds_barrier();  // page prepared
             // ---- compute page ``page`` from the prepared buffer and its Key codes ----
             const half8* qs = reinterpret_cast<const half8*>(ck + kCkQs);
-            // Value codes of the lane's 8 tokens for channel 16*nt + n16 (unpacked just before their
-            // product): code bits to mantissa 8..9 under exponent
-            // 4, value 4 + c (the offset is folded into the per-token constant); tokens (0, 2) sit at
-            // byte bits sh, (1, 3) at 8 + sh
+            // Value codes of the lane's 8 tokens for channel 16*nt + n16, unpacked just before their
+            // product: code bits to mantissa 8..9 under exponent 4, value 4 + c (the offset is
+            // folded into the per-token constant); tokens (0, 2) sit at byte bits sh, (1, 3) at 8 + sh
             uint32_t dlo[8], dhi[8];
             {
                 const uint32_t* vt = reinterpret_cast<const uint32_t*>(ck + kCkVt);
