@@ -12,6 +12,7 @@ namespace lf {
 namespace {
 
 constexpr int kReduceLds = 2048;  // items whose weights are kept in LDS (more: recomputed per channel)
+constexpr int kFastItems = 16;    // up to this many items: one round of loads per thread, no LDS
 
 __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     __shared__ float w[kReduceLds];
@@ -25,6 +26,40 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     const int count = p.dense_splits ? p.dense_splits : p.A.seq_work[2 * b + 1];
     const int tid = threadIdx.x;
     const int nw = blockDim.x / kWave;
+
+    if (count <= kFastItems) {
+        // Every thread (one per channel) loads all items' (m, l) -- the same addresses across
+        // the workgroup -- and its channel's o, all before the first use: one load latency.
+        float m[kFastItems], l[kFastItems], o[kFastItems];
+#pragma unroll
+        for (int k = 0; k < kFastItems; ++k) {
+            m[k] = -__builtin_inff();
+            l[k] = 0.f;
+            o[k] = 0.f;
+            if (k < count) {
+                const float* r = part_rec(p, first + k, h, i);
+                m[k] = r[D];
+                l[k] = r[D + 1];
+                if (tid < D) o[k] = r[tid];
+            }
+        }
+        float M = m[0];
+#pragma unroll
+        for (int k = 1; k < kFastItems; ++k) M = fmaxf(M, m[k]);
+        float lsum = 0.f, osum = 0.f;
+        if (M != -__builtin_inff()) {
+#pragma unroll
+            for (int k = 0; k < kFastItems; ++k) {
+                const float wk = __builtin_amdgcn_exp2f(m[k] - M);  // 0 for the items past count
+                lsum = fmaf(wk, l[k], lsum);
+                osum = fmaf(wk, o[k], osum);
+            }
+        }
+        if (tid < D)
+            store_from_f32(p.A.out, (static_cast<int64_t>(b) * p.A.n_q + h * g + i) * D + tid, p.A.out_dtype,
+                           lsum > 0.f ? osum / lsum : 0.f);
+        return;
+    }
 
     // M = max over items
     float M = -__builtin_inff();
