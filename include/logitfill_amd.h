@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 3
+#define LF_ABI_VERSION 4
 
 /* Element types of query / residual / output tensors. */
 enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
@@ -134,6 +134,11 @@ typedef struct lf_decode_args {
     void* workspace; int64_t workspace_bytes; /* >= lf_decode_workspace_bytes(); needs
                                                  no initialisation                      */
     int32_t kernel;                           /* 0 auto, 1 VALU, 2 MFMA                 */
+    int32_t q_len;                            /* new query tokens per sequence (0 or 1:
+                                                 one); with q_len > 1 the query and out are
+                                                 [batch][n_q][q_len][head_dim], k_new/v_new
+                                                 [batch][n_kv][q_len][head_dim], and the
+                                                 workspace is sized for n_q * q_len rows  */
 } lf_decode_args;
 
 /* Workspace bytes for lf_decode_attention with ``n_work`` items: the fp32
@@ -141,14 +146,18 @@ typedef struct lf_decode_args {
 int64_t lf_decode_workspace_bytes(int32_t n_q, int32_t head_dim, int32_t n_work);
 
 /*
- * Decode attention for one new query token per sequence.  Replaces
+ * Decode attention for the new query token(s) of each sequence.  Replaces
  * logitfill_decode (reference src/logitfill/packed/kernel.cu:112-280) and the
  * dense fallback it protects (src/logitfill/packed/reference.py:30-56):
  *
  *   out[b, i] = softmax(scaling * q[b,i] . K_b^T) V_b,
  *   K_b = [dequant(history_b) ; tail_k[b, :, :tail_len[b]] ; k_new[b]]  (V likewise),
  *
- * with q head i reading kv head i / (n_q / n_kv).  Split-K over packed pages,
+ * with q head i reading kv head i / (n_q / n_kv).  With q_len > 1 new tokens (chunked
+ * scoring / speculative decoding; reference reference.py:18-27,48), query token j sees the
+ * whole history and tail and the new tokens 0..j (right-aligned causal mask); the (head,
+ * token) pairs are served as n_q * q_len query rows, by the VALU kernel (rows per kv head
+ * <= 16; the MFMA kernel takes q_len 1 only).  Split-K over packed pages,
  * then a second kernel merges the splits' softmax partials; accumulation in fp32; output
  * rounded to ``out_dtype``.  Requires bit_v == 2 (as the reference kernel,
  * reference.py:62) and n_q % n_kv == 0.

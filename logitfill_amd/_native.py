@@ -76,6 +76,7 @@ class DecodeArgs(ctypes.Structure):
         ("seq_work", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_int64),
         ("kernel", c_int32),
+        ("q_len", c_int32),
     ]
 
 
@@ -95,7 +96,7 @@ _SIGNATURES = {
                                   c_void_p]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 _LIB = None
 
 

@@ -144,7 +144,12 @@ int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* 
     if (!valid_dtype(A.q_dtype) || !valid_dtype(A.out_dtype) || !valid_dtype(A.tail_dtype)) return LF_E_DTYPE;
     if (A.k_new && !valid_dtype(A.new_dtype)) return LF_E_DTYPE;
     if (A.n_q <= 0 || A.n_q % layer->n_kv != 0) return LF_E_SHAPE;
-    const int g = A.n_q / layer->n_kv;
+    if (A.q_len < 0) return LF_E_SHAPE;
+    const int q_len = A.q_len > 1 ? A.q_len : 1;
+    // q_len new tokens: the kernels serve n_q * q_len query rows (row = head * q_len + token)
+    const int64_t rows = static_cast<int64_t>(A.n_q) * q_len;
+    if (rows > (1 << 20)) return LF_E_SHAPE;
+    const int g = static_cast<int>(rows / layer->n_kv);
     if (g > 16) return LF_E_UNSUPPORTED;
     if (layer->bit_v != 2) return LF_E_UNSUPPORTED;  // as reference.py:62
     const int D = layer->head_dim;
@@ -152,19 +157,22 @@ int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* 
     if (layer->v_groups > 8) return LF_E_UNSUPPORTED;
     if (A.tail_cap < 0 || (A.tail_cap > 0 && (!A.tail_k || !A.tail_v))) return LF_E_NULL;
     if (A.n_work <= 0) return LF_E_SHAPE;
-    if (A.workspace_bytes < lf_decode_workspace_bytes(A.n_q, D, A.n_work))
+    if (A.workspace_bytes < lf_decode_workspace_bytes(static_cast<int32_t>(rows), D, A.n_work))
         return LF_E_WORKSPACE;
     if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
+    if (q_len > 1 && A.kernel == 2) return LF_E_UNSUPPORTED;  // the MFMA kernel takes one token
 
     lf::DecodeParams p;
     p.L = *layer;
     p.A = A;
+    p.A.n_q = static_cast<int32_t>(rows);
     p.g = g;
+    p.q_len = q_len;
     p.qscale = A.scaling * lf::kLog2e;
     p.part = static_cast<float*>(A.workspace);
     p.dense_splits = 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (A.kernel != 1) {
+    if (A.kernel != 1 && q_len == 1) {
         bool handled = false;
         const int r = lf::launch_decode_mfma(p, s, &handled);
         if (handled || A.kernel == 2) return handled ? r : LF_E_UNSUPPORTED;

@@ -15,7 +15,8 @@ namespace lf {
 struct DecodeParams {
     lf_packed_layer L;
     lf_decode_args A;
-    int g;          // query heads per kv head
+    int g;          // query rows per kv head: (n_q / n_kv) * q_len, row = head * q_len + token
+    int q_len;      // new query tokens per sequence (A.n_q counts rows: n_q * q_len)
     float qscale;   // scaling * log2(e)
     float* part;    // [n_work][n_kv][g][D + 2]  (o[D], m, l)
     int dense_splits;  // > 0: items b * dense_splits .. + dense_splits - 1 are sequence b's

@@ -195,10 +195,14 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
         }
     }
     if (kind != 0) {
-        // Residual (kind 1, 2): the BF16 tail page then the new token (reference.py:35-44).
+        // Residual (kind 1, 2): the BF16 tail page then the new token(s) (reference.py:35-44).
+        // With q_len new tokens, row i (token i % q_len) sees new tokens 0 .. i % q_len
+        // (reference.py:18-27,48: the causal mask is right-aligned).
         const int tl = A.tail_len[b];
-        const int has_new = A.k_new != nullptr;
-        const int n_res = tl + has_new;
+        const int q_len = p.q_len;
+        const int n_new = A.k_new != nullptr ? q_len : 0;
+        const int n_res = tl + n_new;
+        const int64_t new_row0 = (static_cast<int64_t>(b) * L.n_kv + h) * q_len;  // first new row
         for (int t0 = 0; t0 < n_res; t0 += 64) {
             const int tt_lane = t0 + lane;
             const bool active = tt_lane < n_res;
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
                 kdt = A.tail_dtype;
             } else {
                 kp = A.k_new;
-                kbase = (static_cast<int64_t>(b) * L.n_kv + h) * D;
+                kbase = (new_row0 + (active ? tt_lane - tl : 0)) * D;
                 kdt = A.new_dtype;
             }
             float score[kMaxG];
@@ -223,6 +227,11 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
 #pragma unroll
                     for (int i = 0; i < kMaxG; ++i)
                         if (i < g) score[i] = fmaf(sm.qT[c][i], k, score[i]);
+                }
+                if (tt_lane >= tl && q_len > 1) {
+#pragma unroll
+                    for (int i = 0; i < kMaxG; ++i)
+                        if (tt_lane - tl > i % q_len) score[i] = -__builtin_inff();
                 }
             }
             float alpha[kMaxG];
@@ -241,7 +250,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
                         v = load_as_f32(A.tail_v, ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + tok) * D + c,
                                         A.tail_dtype);
                     else
-                        v = load_as_f32(A.v_new, (static_cast<int64_t>(b) * L.n_kv + h) * D + c, A.new_dtype);
+                        v = load_as_f32(A.v_new, (new_row0 + tok - tl) * D + c, A.new_dtype);
 #pragma unroll
                     for (int i = 0; i < kMaxG; ++i)
                         if (i < g) o[cc][i] = fmaf(sm.p[tt][i], v, o[cc][i]);

@@ -151,18 +151,23 @@ def kernel_choice() -> int:
 
 def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new, scaling: float,
                 out: torch.Tensor, kernel: int | None = None, pages_per_split: int | None = None) -> None:
-    """Enqueue the fused decode kernel for layer ``layer_idx`` writing ``out [B, n_q, D]``.
+    """Enqueue the fused decode kernel for layer ``layer_idx`` writing ``out``.
 
-    ``query [B, n_q, D]``; ``key_new/value_new [B, n_kv, D]`` or None.  Everything is
-    enqueued on the current stream; nothing synchronises.
+    One new token: ``query/out [B, n_q, D]``, ``key_new/value_new [B, n_kv, D]`` or None.
+    ``q_len`` new tokens: ``query/out [B, n_q, q_len, D]``, ``key_new/value_new
+    [B, n_kv, q_len, D]``; query token j sees the history, the tail and new tokens 0..j
+    (reference ``reference.py:18-27,48``).  Everything is enqueued on the current stream;
+    nothing synchronises.
     """
     layer = manager.layers[layer_idx]
     B, D = layer.batch, layer.head_dim
-    _expect(query, (B, manager.n_q, D), "query")
-    _expect(out, (B, manager.n_q, D), "out")
+    q_len = int(query.shape[2]) if query.dim() == 4 else 1
+    tok = (q_len,) if query.dim() == 4 else ()
+    _expect(query, (B, manager.n_q, *tok, D), "query")
+    _expect(out, (B, manager.n_q, *tok, D), "out")
     if key_new is not None:
-        _expect(key_new, (B, manager.n_kv, D), "key_new")
-        _expect(value_new, (B, manager.n_kv, D), "value_new")
+        _expect(key_new, (B, manager.n_kv, *tok, D), "key_new")
+        _expect(value_new, (B, manager.n_kv, *tok, D), "value_new")
     kernel = kernel_choice() if kernel is None else kernel
     P = layer.page_size
     hist_pages = [h // P for h in layer.hist_lens]
@@ -173,7 +178,7 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
         plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device, RESIDUAL_PAGES)
         layer.decode_plan = plan
     lib = _native.load()
-    nbytes = lib.lf_decode_workspace_bytes(manager.n_q, layer.head_dim, plan.n_work)
+    nbytes = lib.lf_decode_workspace_bytes(manager.n_q * q_len, layer.head_dim, plan.n_work)
     ws = manager.workspace(nbytes)
     tail_k, tail_v = layer.tail_buffers()
     a = _native.DecodeArgs()
@@ -204,22 +209,29 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws.numel()
     a.kernel = kernel
+    a.q_len = q_len
     st = lib.lf_decode_attention(layer.layer_struct(), a, _native.current_stream_ptr(layer.device))
     _native.check(st, "lf_decode_attention")
 
 
 def _kernel_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
                       value_new: torch.Tensor, scaling: float) -> torch.Tensor:
-    """One-token decode through the HIP kernel (replaces ``reference.py:59-109``)."""
+    """Decode through the HIP kernels (replaces ``reference.py:59-109``)."""
     B, n_q, q_len, D = query.shape
-    q = query.reshape(B, n_q, D)
-    if q.stride(-1) != 1 or not q.is_contiguous():
-        q = q.contiguous()
-    kn = key_new.reshape(B, manager.n_kv, D).contiguous()
-    vn = value_new.reshape(B, manager.n_kv, D).contiguous()
-    out = torch.empty(B, n_q, D, dtype=query.dtype, device=query.device)
+    if q_len == 1:
+        q = query.reshape(B, n_q, D).contiguous()
+        kn = key_new.reshape(B, manager.n_kv, D).contiguous()
+        vn = value_new.reshape(B, manager.n_kv, D).contiguous()
+        out = torch.empty(B, n_q, D, dtype=query.dtype, device=query.device)
+    else:
+        q, kn, vn = query.contiguous(), key_new.contiguous(), value_new.contiguous()
+        out = torch.empty(B, n_q, q_len, D, dtype=query.dtype, device=query.device)
     decode_into(manager, layer_idx, q, kn, vn, scaling, out)
-    return out.view(B, n_q, 1, D)
+    return out.view(B, n_q, q_len, D)
+
+
+# Query rows per kv head the multi-token kernel path serves ((n_q / n_kv) * q_len).
+MAX_ROWS_PER_KV_HEAD = 16
 
 
 def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
@@ -227,6 +239,8 @@ def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torc
     """``reference.py:112-116``: ``query [B, n_q, q_len, D]`` -> ``[B, n_q, q_len, D]``."""
     if not query.is_cuda:
         raise RuntimeError("logitfill_amd runs on ROCm devices only (there is no CPU path)")
-    if query.shape[-2] == 1 and manager.bit_v == 2:
+    q_len = int(query.shape[-2])
+    rows = manager.n_q // manager.n_kv * q_len
+    if manager.bit_v == 2 and (q_len == 1 or rows <= MAX_ROWS_PER_KV_HEAD):
         return _kernel_attention(manager, layer_idx, query, key_new, value_new, scaling)
     return reference_attention(manager, layer_idx, query, key_new, value_new, scaling)

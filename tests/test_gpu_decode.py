@@ -140,8 +140,8 @@ def test_decode_commit_loop_crossing_flushes(gpu):
     assert mgr.layers[0].hist_len == 384 and mgr.layers[0].tail_len == 9
 
 
-def test_multi_token_query_uses_device_dense_path(gpu):
-    """q_len > 1 (chunked scoring) takes the dense path with the right-aligned causal mask."""
+def test_multi_token_query_small_group(gpu):
+    """q_len > 1 (chunked scoring) with the right-aligned causal mask (rows 2 * 3 <= 16: kernel)."""
     n_q, n_kv, D = 4, 2, 128
     d = synth.make_layer(1, n_q, n_kv, D, 2 * 128 + 30, 2.5, seed=40)
     mgr, lens = build(d, [2], [20], n_q, n_kv, D, gpu)
@@ -219,3 +219,38 @@ def test_score_growth_across_pages(gpu, kernel, profile):
         out = run(mgr, d, gpu, D ** -0.5, KERNELS[kernel], pages_per_split=pps)
         for b in range(2):
             assert_decode_close(out[b], oracle_out(d, b, lens[b], n_q, n_kv, D ** -0.5))
+
+
+@pytest.mark.parametrize("g,q_len,tails", [(2, 2, [0, 63]), (4, 3, [127, 5]), (2, 8, [61, 0]), (7, 3, [9, 100])])
+def test_multi_token_packed_decode(gpu, g, q_len, tails):
+    """q_len new tokens per sequence (speculative decoding / chunked scoring, reference
+    reference.py:18-27,48): query token j sees the history, the tail and new tokens 0..j.
+    Rows (n_q / n_kv) * q_len <= 16 run the packed VALU kernel (every tail length across its
+    64-token chunks, split items with and without the residual); (7, 3) has 21 rows and takes
+    the dense dequantise path."""
+    n_kv, D = 2, 128
+    n_q = g * n_kv
+    pages = [6, 3]
+    T = max(p * 128 + t for p, t in zip(pages, tails)) + q_len
+    d = synth.make_layer(2, n_q, n_kv, D, T, 2.5, seed=100 + q_len)
+    mgr, lens = build(d, pages, tails, n_q, n_kv, D, gpu)
+    q = torch.randn(2, n_q, q_len, D, generator=torch.Generator().manual_seed(q_len)).bfloat16()
+    kn = torch.stack([d.key[b, :, lens[b]:lens[b] + q_len] for b in range(2)])
+    vn = torch.stack([d.value[b, :, lens[b]:lens[b] + q_len] for b in range(2)])
+    out = packed_attention(mgr, 0, q.to(gpu), kn.to(gpu), vn.to(gpu), D ** -0.5)
+    torch.cuda.synchronize()
+    for b in range(2):
+        store = oracle_store(d.levels, f32(d.key[b, :, :lens[b]]), f32(d.value[b, :, :lens[b]]))
+        ref = oatt.reference_attention(store, f32(q[b]), f32(kn[b]), f32(vn[b]), D ** -0.5, n_q, n_kv)
+        for j in range(q_len):
+            assert_decode_close(out[b, :, j], ref[:, j])
+    if g * q_len <= 16:
+        # split items: the residual rides with the first item of each sequence
+        out2 = torch.empty(2, n_q, q_len, D, dtype=torch.float32, device=gpu)
+        decode_into(mgr, 0, q.float().to(gpu).contiguous(), kn.to(gpu).contiguous(), vn.to(gpu).contiguous(),
+                    D ** -0.5, out2, pages_per_split=2)
+        torch.cuda.synchronize()
+        assert float((out2 - out.float()).abs().max()) < 2e-2
+        with pytest.raises(_native.LFError):
+            decode_into(mgr, 0, q.to(gpu).contiguous(), kn.to(gpu).contiguous(), vn.to(gpu).contiguous(),
+                        D ** -0.5, torch.empty_like(out), kernel=_native.KERNEL_MFMA)
