@@ -398,10 +398,14 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
     koff[2] = koff[1] + L.k_width[1];
     koff[3] = koff[2] + L.k_width[2];
     const int nslots = koff[3];
+    const int wall = koff[3] + L.k_width[3];
+    int16_t* tidx = reinterpret_cast<int16_t*>(codes + kFastP * cw);  // [wall] channel of each tier slot
+    int* tcnt = reinterpret_cast<int*>(tidx + ((wall + 1) & ~1));      // [4] tier counts of head h
 
     const bool value_part = blockIdx.z != 0;
 
-    // ---- stage the page; channel -> integer slot map (layout.py:49-68) ----
+    // ---- stage the page and this head's tier tables (layout.py:49-68): all their global loads
+    // go out before the first wait ----
     {
         const uint16_t* src = static_cast<const uint16_t*>(value_part ? a.v_src : a.k_src) + b * a.sb + h * a.sh +
                               tok0 * a.st;
@@ -411,20 +415,32 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
             const int idx = tid + kFastThreads * i;  // 16-byte chunk: row idx / 16, column 8 (idx % 16)
             kv[i] = *reinterpret_cast<const uint4*>(src + (idx >> 4) * a.st + 8 * (idx & 15));
         }
+        int my_idx = 0, my_cnt = 0;
         if (!value_part) {
+            // slot tid of tier t: its channel.  Constant indices into the kernel argument only
+            // (a lane-dependent one would copy the argument block to scratch memory).
+            if (tid < koff[1]) my_idx = L.tier_index[0][h * L.k_width[0] + tid];
+            else if (tid < koff[2]) my_idx = L.tier_index[1][h * L.k_width[1] + tid - koff[1]];
+            else if (tid < koff[3]) my_idx = L.tier_index[2][h * L.k_width[2] + tid - koff[2]];
+            else if (tid < wall) my_idx = L.tier_index[3][h * L.k_width[3] + tid - koff[3]];
+            if (tid == 0 && L.k_width[0]) my_cnt = L.tier_count[0][h];
+            else if (tid == 1 && L.k_width[1]) my_cnt = L.tier_count[1][h];
+            else if (tid == 2 && L.k_width[2]) my_cnt = L.tier_count[2][h];
+            else if (tid == 3 && L.k_width[3]) my_cnt = L.tier_count[3][h];
             if (tid < D) chslot[tid] = -1;
-            __syncthreads();
-            for (int t = 0; t < 3; ++t) {
-                const int cnt = L.k_width[t] ? L.tier_count[t][h] : 0;
-                for (int j = tid; j < cnt; j += kFastThreads)
-                    chslot[L.tier_index[t][h * L.k_width[t] + j]] = static_cast<int16_t>(koff[t] + j);
-            }
+            if (tid < wall) tidx[tid] = static_cast<int16_t>(my_idx);
+            if (tid < 4) tcnt[tid] = my_cnt;
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + kFastThreads * i;
             uint32_t* kd = reinterpret_cast<uint32_t*>(kpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
             kd[0] = kv[i].x; kd[1] = kv[i].y; kd[2] = kv[i].z; kd[3] = kv[i].w;
+        }
+        __syncthreads();
+        if (!value_part && tid < nslots) {  // channel -> integer slot map
+            const int t = tid >= koff[2] ? 2 : tid >= koff[1] ? 1 : 0;
+            if (tid - koff[t] < tcnt[t]) chslot[tidx[tid]] = static_cast<int16_t>(tid);
         }
         __syncthreads();
     }
@@ -453,11 +469,11 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
     for (int sl = tid; sl < nslots; sl += kFastThreads) {
         const int t = sl >= koff[2] ? 2 : sl >= koff[1] ? 1 : 0;
         const int j = sl - koff[t];
-        const int cnt = L.tier_count[t][h];
+        const int cnt = tcnt[t];
         const int qmax = (1 << (2 << t)) - 1;
         const int64_t o = kgrp_idx(L, b, h, L.k_width[t], j, page);
         if (j < cnt) {
-            const int ch = L.tier_index[t][h * L.k_width[t] + j];
+            const int ch = tidx[sl];
             float lo = pmin[ch], hi = pmax[ch];
 #pragma unroll
             for (int k = 1; k < 8; ++k) {
@@ -523,12 +539,12 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
         }
         const int w16 = L.k_width[3];
         if (w16 > 0) {
-            const int cnt = L.tier_count[3][h];
+            const int cnt = tcnt[3];
             for (int idx = tid; idx < kFastP * w16; idx += kFastThreads) {
                 const int tau = idx / w16, j = idx - tau * w16;
                 uint16_t v = 0;
                 if (j < cnt) {
-                    const uint16_t raw = kpage[tau * kFastLd + L.tier_index[3][h * w16 + j]];
+                    const uint16_t raw = kpage[tau * kFastLd + tidx[koff[3] + j]];
                     v = IsHalf ? raw : f32_to_f16(bf16_to_f32(raw));
                 }
                 L.k_value16[tok_row(L, b, h, dst_tok0) * w16 + idx] = v;
@@ -545,8 +561,9 @@ bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
 
 size_t pack_fast_lds_bytes(const lf_packed_layer& L) {
     const int cw = (pack_code_row(L) + 3) & ~3;
+    const int wall = L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3];
     return static_cast<size_t>(kFastP) * kFastLd * 2 + 2 * 8 * 128 * 4 + static_cast<size_t>(cw) * 16 + 128 * 2 +
-           static_cast<size_t>(kFastP) * cw + 16;
+           static_cast<size_t>(kFastP) * cw + static_cast<size_t>((wall + 1) & ~1) * 2 + 4 * 4 + 16;
 }
 
 int pack_code_row(const lf_packed_layer& L) {
