@@ -301,16 +301,21 @@ int pack_code_row(const lf_packed_layer& L);
 // Values, 2-byte inputs with 16-byte aligned rows.  Two workgroups of 1024 threads per page
 // and kv head (blockIdx.z 0: Key page, 1: Value page), so two run on a CU; per element the
 // division uses a correctly rounded reciprocal of the group scale and one Markstein
-// correction (see div_rn).
+// correction (see div_rn).  Every phase is branch-free per element.
 //
-//   stage     the page into LDS (rows padded to 130 halves)
-//   phase 1   Key min/max: thread (channel tid % 128, tokens 16 (tid / 128) + 0..15); the 16
-//             values stay in registers
-//   phase 2   per integer-tier slot: group min, scale, reciprocal; scale/min stored
-//   phase 3   Key codes of the thread's 16 tokens into an LDS byte row per token
-//   phase 4   Key words (token, word) assembled from 4/8/16 code bytes, fp16 tier copied
-//   phase 5   Values: thread (token tid / 8, channels 16 (tid % 8) + 0..15) = one code word;
-//             the token's min/max over its 8 threads by lane exchange
+//   stage     the page into LDS (rows padded to 130 halves), this head's tier tables, the
+//             code rows zeroed; padding slots' scale/min (1.0, 0.0) stored
+//   phase 1   Key min/max partials: thread (channel c = tid % 128, tokens 16 (tid / 128) + 0..15);
+//             the 16 values stay in registers
+//   phase 2   every thread merges the 8 partials of its own channel: min, scale, reciprocal
+//             (the token-block-0 thread stores the fp16 scale/min)
+//   phase 3   the channel's 16 codes into an LDS byte row per token; each integer tier has a
+//             16-byte aligned segment of the row, in slot order
+//   phase 4   thread (token tid / 8, q = tid % 8) assembles words q, q + 8, ... of the token's
+//             integer tiers from 16 / 8 / 4 code bytes (one LDS read each) and copies the fp16
+//             tier
+//   Values    thread (token tid / 8, channels 16 (tid % 8) + 0..15) = one code word; the
+//             token's min/max over its 8 threads by lane exchange
 // ---------------------------------------------------------------------------------------
 constexpr int kFastThreads = 1024;
 constexpr int kFastP = 128;
@@ -318,55 +323,92 @@ constexpr int kFastLd = 130;  // halves per staged row
 
 // a / s rounded to nearest even from y = RN(1/s) (Markstein: q0 = RN(a*y) is within an ulp of
 // a/s, the residual a - q0*s is exact by FMA, and RN(q0 + r*y) is the correctly rounded
-// quotient when no step overflows or underflows).  a >= 0 here; a quotient below the normal
-// range rounds to code 0 either way.  Non-finite a (a range overflowing float) takes the
-// plain IEEE division.
+// quotient when no step overflows or underflows).  a >= 0 here and a <= s * qmax unless s was
+// clamped to 1e5 (then a / s <= 3.5e33), so a * y cannot overflow for finite a; a quotient
+// below the normal range rounds to code 0 either way.  a = +inf (a range overflowing float)
+// gives +inf, as IEEE division does.
 __device__ __forceinline__ float div_rn(float a, float s, float y) {
     const float q0 = a * y;
     const float r = fmaf(-q0, s, a);
-    float q = fmaf(r, y, q0);
-    if (__builtin_expect(!__builtin_isfinite(a), 0)) q = a / s;
-    return q;
+    const float q = fmaf(r, y, q0);
+    return a == __builtin_inff() ? a : q;
+}
+
+// code = clamp(rint((x - lo) / s), 0, qmax) with div_rn.
+__device__ __forceinline__ uint32_t fast_code(float x, float lo, float s, float y, float qmax) {
+    const float q = __builtin_rintf(div_rn(x - lo, s, y));
+    return static_cast<uint32_t>(__builtin_amdgcn_fmed3f(q, 0.0f, qmax));
+}
+
+// Byte-per-code LDS row of the fast path: tier t's slots start at seg[t] (16-byte aligned).
+struct CodeSegs {
+    int seg[4];  // seg[3] = row bytes
+};
+
+__device__ __host__ inline CodeSegs code_segs(const lf_packed_layer& L) {
+    CodeSegs s;
+    s.seg[0] = 0;
+    s.seg[1] = (L.k_width[0] + 15) & ~15;
+    s.seg[2] = s.seg[1] + ((L.k_width[1] + 15) & ~15);
+    s.seg[3] = s.seg[2] + ((L.k_width[2] + 15) & ~15);
+    return s;
+}
+
+// Four byte codes (0..3) of a dword -> 8 bits, code k at bits 2k (bytes 1 and 3 fold onto 0 and 2).
+__device__ __forceinline__ uint32_t fold2(uint32_t d) { return d | (d >> 6); }
+
+// 16 int2 codes (one per byte) -> LSB-first word.
+__device__ __forceinline__ uint32_t word_int2(uint4 b) {
+    const uint32_t t0 = fold2(b.x), t1 = fold2(b.y), t2 = fold2(b.z), t3 = fold2(b.w);
+    // nibble bytes (t.byte0, t.byte2) of t0, t1 / t2, t3, then nibble pairs folded into bytes
+    const uint32_t p01 = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
+    const uint32_t p23 = __builtin_amdgcn_perm(t3, t2, 0x06040200u);
+    const uint32_t q01 = p01 | (p01 >> 4), q23 = p23 | (p23 >> 4);
+    return __builtin_amdgcn_perm(q23, q01, 0x06040200u);
+}
+
+// 8 int4 codes (one per byte) -> LSB-first word.
+__device__ __forceinline__ uint32_t word_int4(uint2 b) {
+    const uint32_t t0 = b.x | (b.x >> 4), t1 = b.y | (b.y >> 4);
+    return __builtin_amdgcn_perm(t1, t0, 0x06040200u);
 }
 
 // Phase 5 of the fast path: Values, one code word per thread (layout.py:115-129).
 template <bool IsHalf>
 __device__ __forceinline__ void pack_value_page(const lf_packed_layer& L, const uint16_t* vpage, int b, int h,
                                                 int64_t dst_tok0, int tid) {
-    constexpr int D = 128;
+    const int tk = tid >> 3, w = tid & 7;
+    const uint32_t* row = reinterpret_cast<const uint32_t*>(vpage + tk * kFastLd + 16 * w);  // 4-byte aligned
+    float v[16];
+    float lo = __builtin_inff(), hi = -__builtin_inff();
     {
-        const int tk = tid >> 3, w = tid & 7;
-        const uint32_t* row = reinterpret_cast<const uint32_t*>(vpage + tk * kFastLd + 16 * w);
-        float v[16];
-        float lo = __builtin_inff(), hi = -__builtin_inff();
+        uint32_t pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = row[i];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t pr = row[i];
-            v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr & 0xffffu));
-            v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr >> 16));
+            v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] & 0xffffu));
+            v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] >> 16));
             lo = fminf(lo, fminf(v[2 * i], v[2 * i + 1]));
             hi = fmaxf(hi, fmaxf(v[2 * i], v[2 * i + 1]));
         }
-        // the token's 8 threads are lanes 8k .. 8k + 7 of one wave
+    }
+    // the token's 8 threads are lanes 8k .. 8k + 7 of one wave
 #pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            lo = fminf(lo, __shfl_xor(lo, off, kWave));
-            hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
-        }
-        const float sc = group_scale(hi, lo, 3);
-        const float y = 1.0f / sc;
-        uint32_t word = 0;
+    for (int off = 1; off < 8; off <<= 1) {
+        lo = fminf(lo, __shfl_xor(lo, off, kWave));
+        hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
+    }
+    const float sc = group_scale(hi, lo, 3);
+    const float y = 1.0f / sc;
+    uint32_t word = 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float q = __builtin_rintf(div_rn(v[i] - lo, sc, y));
-            word |= static_cast<uint32_t>(fminf(fmaxf(q, 0.0f), 3.0f)) << (2 * i);
-        }
-        const int64_t trow = tok_row(L, b, h, dst_tok0 + tk);
-        L.v_code[trow * (D / 16) + w] = static_cast<int32_t>(word);
-        if (w == 0) {
-            L.v_scale[trow] = f32_to_f16(sc);
-            L.v_min[trow] = f32_to_f16(lo);
-        }
+    for (int i = 0; i < 16; ++i) word |= fast_code(v[i], lo, sc, y, 3.0f) << (2 * i);
+    const int64_t trow = tok_row(L, b, h, dst_tok0 + tk);
+    L.v_code[trow * 8 + w] = static_cast<int32_t>(word);
+    if (w == 0) {
+        L.v_scale[trow] = f32_to_f16(sc);
+        L.v_min[trow] = f32_to_f16(lo);
     }
 }
 
@@ -384,25 +426,16 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
 
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                       // [128][130] (Key or Value page)
-    uint16_t* vpage = kpage;
-    float* pmin = reinterpret_cast<float*>(kpage + kFastP * kFastLd);           // [8][128]
-    float* pmax = pmin + 8 * D;                                                 // [8][128]
-    float4* prm = reinterpret_cast<float4*>(pmax + 8 * D);                      // [cw] lo, s, y, -
-    int16_t* chslot = reinterpret_cast<int16_t*>(prm + a.cw);                   // [128] slot of a channel, -1
-    uint8_t* codes = reinterpret_cast<uint8_t*>(chslot + D);                    // [128][cw]
-    const int cw = a.cw;
-
-    int koff[4];
-    koff[0] = 0;
-    koff[1] = L.k_width[0];
-    koff[2] = koff[1] + L.k_width[1];
-    koff[3] = koff[2] + L.k_width[2];
-    const int nslots = koff[3];
-    const int wall = koff[3] + L.k_width[3];
-    int16_t* tidx = reinterpret_cast<int16_t*>(codes + kFastP * cw);  // [wall] channel of each tier slot
-    int* tcnt = reinterpret_cast<int*>(tidx + ((wall + 1) & ~1));      // [4] tier counts of head h
+    float2* pmm = reinterpret_cast<float2*>(kpage + kFastP * kFastLd);          // [8][128] partial (lo, hi)
+    uint8_t* codes = reinterpret_cast<uint8_t*>(pmm + 8 * D);                   // [128][cw] code bytes
+    const CodeSegs cs = code_segs(L);
+    const int cw = cs.seg[3];
+    int16_t* cpos = reinterpret_cast<int16_t*>(codes + kFastP * cw);            // [128] code byte of a channel, -1
+    int16_t* tidx16 = cpos + D;                                                 // [w16] channels of the fp16 tier
 
     const bool value_part = blockIdx.z != 0;
+    const int w0 = L.k_width[0], w1 = L.k_width[1], w2 = L.k_width[2], w16 = L.k_width[3];
+    const int koff1 = w0, koff2 = w0 + w1, nslots = w0 + w1 + w2, wall = nslots + w16;
 
     // ---- stage the page and this head's tier tables (layout.py:49-68): all their global loads
     // go out before the first wait ----
@@ -417,36 +450,46 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
         }
         int my_idx = 0, my_cnt = 0;
         if (!value_part) {
-            // slot tid of tier t: its channel.  Constant indices into the kernel argument only
-            // (a lane-dependent one would copy the argument block to scratch memory).
-            if (tid < koff[1]) my_idx = L.tier_index[0][h * L.k_width[0] + tid];
-            else if (tid < koff[2]) my_idx = L.tier_index[1][h * L.k_width[1] + tid - koff[1]];
-            else if (tid < koff[3]) my_idx = L.tier_index[2][h * L.k_width[2] + tid - koff[2]];
-            else if (tid < wall) my_idx = L.tier_index[3][h * L.k_width[3] + tid - koff[3]];
-            if (tid == 0 && L.k_width[0]) my_cnt = L.tier_count[0][h];
-            else if (tid == 1 && L.k_width[1]) my_cnt = L.tier_count[1][h];
-            else if (tid == 2 && L.k_width[2]) my_cnt = L.tier_count[2][h];
-            else if (tid == 3 && L.k_width[3]) my_cnt = L.tier_count[3][h];
-            if (tid < D) chslot[tid] = -1;
-            if (tid < wall) tidx[tid] = static_cast<int16_t>(my_idx);
-            if (tid < 4) tcnt[tid] = my_cnt;
+            // slot tid of tier t: its channel and the tier's count for head h.  Constant indices
+            // into the kernel argument only (a lane-dependent one would copy the argument block
+            // to scratch memory).
+            if (tid < koff1) { my_idx = L.tier_index[0][h * w0 + tid]; my_cnt = L.tier_count[0][h]; }
+            else if (tid < koff2) { my_idx = L.tier_index[1][h * w1 + tid - koff1]; my_cnt = L.tier_count[1][h]; }
+            else if (tid < nslots) { my_idx = L.tier_index[2][h * w2 + tid - koff2]; my_cnt = L.tier_count[2][h]; }
+            else if (tid < wall) { my_idx = L.tier_index[3][h * w16 + tid - nslots]; my_cnt = L.tier_count[3][h]; }
+            if (tid < D) cpos[tid] = -1;
+            for (int i = tid; i < kFastP * cw / 4; i += kFastThreads) reinterpret_cast<uint32_t*>(codes)[i] = 0;
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + kFastThreads * i;
+            // rows are 260 bytes apart: 4-byte aligned, so four dword stores
             uint32_t* kd = reinterpret_cast<uint32_t*>(kpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
             kd[0] = kv[i].x; kd[1] = kv[i].y; kd[2] = kv[i].z; kd[3] = kv[i].w;
         }
-        __syncthreads();
-        if (!value_part && tid < nslots) {  // channel -> integer slot map
-            const int t = tid >= koff[2] ? 2 : tid >= koff[1] ? 1 : 0;
-            if (tid - koff[t] < tcnt[t]) chslot[tidx[tid]] = static_cast<int16_t>(tid);
+        if (value_part) {
+            __syncthreads();
+            pack_value_page<IsHalf>(L, kpage, b, h, dst_tok0, tid);
+            return;
         }
         __syncthreads();
-    }
-    if (value_part) {
-        pack_value_page<IsHalf>(L, vpage, b, h, dst_tok0, tid);
-        return;
+        if (tid < wall) {
+            const int t = tid >= nslots ? 3 : tid >= koff2 ? 2 : tid >= koff1 ? 1 : 0;
+            const int j = tid - (t == 3 ? nslots : t == 2 ? koff2 : t == 1 ? koff1 : 0);
+            if (t == 3) {
+                tidx16[j] = static_cast<int16_t>(my_idx);
+            } else if (j < my_cnt) {
+                cpos[my_idx] = static_cast<int16_t>(cs.seg[t] + j);
+            } else {
+                // padding slots: scale 1.0, min 0.0, code 0 (layout.py:84-85)
+                const int width = t == 2 ? w2 : t == 1 ? w1 : w0;
+                const int64_t o = kgrp_idx(L, b, h, width, j, page);
+                uint16_t* ks = t == 2 ? L.k_scale[2] : t == 1 ? L.k_scale[1] : L.k_scale[0];
+                uint16_t* km = t == 2 ? L.k_min[2] : t == 1 ? L.k_min[1] : L.k_min[0];
+                ks[o] = 0x3C00u;
+                km[o] = 0;
+            }
+        }
     }
 
     // ---- phase 1: Key min/max of channel c over tokens 16 ck .. 16 ck + 15 ----
@@ -460,98 +503,74 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
             lo = fminf(lo, x[i]);
             hi = fmaxf(hi, x[i]);
         }
-        pmin[ck * D + c] = lo;
-        pmax[ck * D + c] = hi;
+        pmm[ck * D + c] = float2{lo, hi};
     }
     __syncthreads();
 
-    // ---- phase 2: per integer slot (tier t, local j): s = clamp((hi - lo) / qmax) (layout.py:12-18) ----
-    for (int sl = tid; sl < nslots; sl += kFastThreads) {
-        const int t = sl >= koff[2] ? 2 : sl >= koff[1] ? 1 : 0;
-        const int j = sl - koff[t];
-        const int cnt = tcnt[t];
-        const int qmax = (1 << (2 << t)) - 1;
-        const int64_t o = kgrp_idx(L, b, h, L.k_width[t], j, page);
-        if (j < cnt) {
-            const int ch = tidx[sl];
-            float lo = pmin[ch], hi = pmax[ch];
-#pragma unroll
-            for (int k = 1; k < 8; ++k) {
-                lo = fminf(lo, pmin[k * D + ch]);
-                hi = fmaxf(hi, pmax[k * D + ch]);
-            }
-            const float sc = group_scale(hi, lo, qmax);
-            prm[sl] = float4{lo, sc, 1.0f / sc, 0.f};
-            L.k_scale[t][o] = f32_to_f16(sc);
-            L.k_min[t][o] = f32_to_f16(lo);
-        } else {
-            // padding slots: scale 1.0, min 0.0, code 0 (layout.py:84-85)
-            L.k_scale[t][o] = 0x3C00u;
-            L.k_min[t][o] = 0;
-        }
-    }
-    // padding slot codes are 0
-    for (int i = tid; i < kFastP * cw / 4; i += kFastThreads) reinterpret_cast<uint32_t*>(codes)[i] = 0;
-    __syncthreads();
-
-    // ---- phase 3: codes of channel c for its 16 tokens ----
+    // ---- phases 2, 3: the channel's group scale (layout.py:12-18) and its 16 codes ----
     {
-        const int sl = chslot[c];
-        if (sl >= 0) {
-            const int t = sl >= koff[2] ? 2 : sl >= koff[1] ? 1 : 0;
-            const float qmax = static_cast<float>((1 << (2 << t)) - 1);
-            const float4 pr = prm[sl];
+        const int pos = cpos[c];
+        if (pos >= 0) {
+            float lo = __builtin_inff(), hi = -__builtin_inff();
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float q = __builtin_rintf(div_rn(x[i] - pr.x, pr.y, pr.z));
-                codes[(16 * ck + i) * cw + sl] = static_cast<uint8_t>(fminf(fmaxf(q, 0.0f), qmax));
+            for (int k = 0; k < 8; ++k) {
+                const float2 m = pmm[k * D + c];
+                lo = fminf(lo, m.x);
+                hi = fmaxf(hi, m.y);
             }
+            const int t = pos >= cs.seg[2] ? 2 : pos >= cs.seg[1] ? 1 : 0;
+            const int qm = t == 2 ? 255 : t == 1 ? 15 : 3;
+            const float sc = group_scale(hi, lo, qm);
+            const float y = 1.0f / sc;
+            if (ck == 0) {
+                const int j = pos - cs.seg[t];
+                const int width = t == 2 ? w2 : t == 1 ? w1 : w0;
+                const int64_t o = kgrp_idx(L, b, h, width, j, page);
+                uint16_t* ks = t == 2 ? L.k_scale[2] : t == 1 ? L.k_scale[1] : L.k_scale[0];
+                uint16_t* km = t == 2 ? L.k_min[2] : t == 1 ? L.k_min[1] : L.k_min[0];
+                ks[o] = f32_to_f16(sc);
+                km[o] = f32_to_f16(lo);
+            }
+            const float qmax = static_cast<float>(qm);
+            uint8_t* crow = codes + (16 * ck) * cw + pos;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) crow[i * cw] = static_cast<uint8_t>(fast_code(x[i], lo, sc, y, qmax));
         }
     }
     __syncthreads();
 
     // ---- phase 4: LSB-first words (layout.py:21-35, :94-97); fp16 tier (layout.py:101-111) ----
     {
+        const int tau = tid >> 3, q = tid & 7;
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
-        const int n0 = kFastP * kw0, n1 = n0 + kFastP * kw1, n2 = n1 + kFastP * kw2;
-        for (int idx = tid; idx < n2; idx += kFastThreads) {
-            const int t = idx >= n1 ? 2 : idx >= n0 ? 1 : 0;
-            const int rel = idx - (t == 2 ? n1 : t == 1 ? n0 : 0);
-            const int words = t == 2 ? kw2 : t == 1 ? kw1 : kw0;
-            const int tau = rel / words, w = rel - tau * words;
-            const uint8_t* crow = codes + tau * cw + koff[t];
-            const int width = L.k_width[t];  // slots past the tier width belong to the next tier
-            uint32_t word = 0;
-            if (t == 0) {
-#pragma unroll
-                for (int k = 0; k < 16; ++k)
-                    if (16 * w + k < width) word |= static_cast<uint32_t>(crow[16 * w + k]) << (2 * k);
-            } else if (t == 1) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (8 * w + k < width) word |= static_cast<uint32_t>(crow[8 * w + k]) << (4 * k);
+        const int nw = kw0 + kw1 + kw2;
+        const int64_t trow = tok_row(L, b, h, dst_tok0 + tau);
+        const uint8_t* crow = codes + tau * cw;
+        for (int wi = q; wi < nw; wi += 8) {
+            if (wi < kw0) {
+                const uint4 cb = *reinterpret_cast<const uint4*>(crow + 16 * wi);
+                L.k_code[0][trow * kw0 + wi] = static_cast<int32_t>(word_int2(cb));
+            } else if (wi < kw0 + kw1) {
+                const int w = wi - kw0;
+                const uint2 cb = *reinterpret_cast<const uint2*>(crow + cs.seg[1] + 8 * w);
+                L.k_code[1][trow * kw1 + w] = static_cast<int32_t>(word_int4(cb));
             } else {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (4 * w + k < width) word |= static_cast<uint32_t>(crow[4 * w + k]) << (8 * k);
+                const int w = wi - kw0 - kw1;
+                L.k_code[2][trow * kw2 + w] = *reinterpret_cast<const int32_t*>(crow + cs.seg[2] + 4 * w);
             }
-            L.k_code[t][tok_row(L, b, h, dst_tok0 + tau) * words + w] = static_cast<int32_t>(word);
         }
-        const int w16 = L.k_width[3];
         if (w16 > 0) {
-            const int cnt = tcnt[3];
-            for (int idx = tid; idx < kFastP * w16; idx += kFastThreads) {
-                const int tau = idx / w16, j = idx - tau * w16;
+            const int cnt = L.tier_count[3][h];
+            for (int j = q; j < w16; j += 8) {
                 uint16_t v = 0;
                 if (j < cnt) {
-                    const uint16_t raw = kpage[tau * kFastLd + tidx[koff[3] + j]];
+                    const uint16_t raw = kpage[tau * kFastLd + tidx16[j]];
                     v = IsHalf ? raw : f32_to_f16(bf16_to_f32(raw));
                 }
-                L.k_value16[tok_row(L, b, h, dst_tok0) * w16 + idx] = v;
+                L.k_value16[trow * w16 + j] = v;
             }
         }
     }
-
 }
 
 bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
@@ -560,10 +579,9 @@ bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
 }
 
 size_t pack_fast_lds_bytes(const lf_packed_layer& L) {
-    const int cw = (pack_code_row(L) + 3) & ~3;
-    const int wall = L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3];
-    return static_cast<size_t>(kFastP) * kFastLd * 2 + 2 * 8 * 128 * 4 + static_cast<size_t>(cw) * 16 + 128 * 2 +
-           static_cast<size_t>(kFastP) * cw + static_cast<size_t>((wall + 1) & ~1) * 2 + 4 * 4 + 16;
+    const int cw = code_segs(L).seg[3];
+    return static_cast<size_t>(kFastP) * kFastLd * 2 + 8 * 128 * 8 + static_cast<size_t>(kFastP) * cw + 128 * 2 +
+           static_cast<size_t>(L.k_width[3]) * 2 + 16;
 }
 
 int pack_code_row(const lf_packed_layer& L) {
@@ -611,7 +629,6 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
     a.cw = pack_code_row(L);
     dim3 grid(n_jobs, L.n_kv);
     if (pack_fast_ok(L, src_dtype, a.vec16 != 0)) {
-        a.cw = (pack_code_row(L) + 3) & ~3;
         const size_t lds = pack_fast_lds_bytes(L);
         if (lds <= 160 * 1024) {
             static size_t fast_limit[2] = {64 * 1024, 64 * 1024};
