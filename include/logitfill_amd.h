@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 4
+#define LF_ABI_VERSION 5
 
 /* Element types of query / residual / output tensors. */
 enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
@@ -101,6 +101,34 @@ int32_t lf_pack_pages(const lf_packed_layer* layer,
                       const void* k_src, const void* v_src, int32_t src_dtype,
                       int64_t src_stride_b, int64_t src_stride_h, int64_t src_stride_t,
                       const int32_t* jobs, int32_t n_jobs, void* stream);
+
+/* Page source of one layer for lf_pack_pages_multi: element strides, channel stride 1. */
+typedef struct lf_pack_source {
+    const void* k;
+    const void* v;
+    int64_t stride_b, stride_h, stride_t;
+} lf_pack_source;
+
+/*
+ * Page compress of several layers in one launch.  The reference flushes each
+ * layer's full page inside that layer's commit (src/logitfill/packed/cache.py:
+ * 48-81, one quantize_key_page + quantize_value_page per layer); every layer
+ * of a decode step fills its page on the same token, so a caller that defers
+ * the flushes to the end of the step packs all of them here at once (the
+ * packed pages are read only by the next step).  Same results as one
+ * lf_pack_pages call per layer.
+ *
+ * ``layers_host`` / ``srcs_host`` [n_layers]: host copies, used for the checks
+ * and launch sizing; ``layers_dev`` / ``srcs_dev``: the same arrays in DEVICE
+ * memory, read by the kernel.  ``jobs`` is a DEVICE int32 array [n_jobs][4] of
+ * (layer, b, src_token0, dst_page).  Every layer must have the same n_kv and
+ * take the fast shape (head_dim = page_size = k_group = v_group = 128,
+ * bit_v 2, 16-byte aligned rows of a 2-byte dtype); otherwise LF_E_UNSUPPORTED
+ * and nothing runs.
+ */
+int32_t lf_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_layer* layers_host,
+                            const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int32_t n_layers,
+                            int32_t src_dtype, const int32_t* jobs, int32_t n_jobs, void* stream);
 
 /*
  * Decode work plan (host function, no device access).  Sequence b's work is

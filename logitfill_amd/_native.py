@@ -14,6 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("liblogitfill_amd.so")
 
 LF_BF16, LF_FP16, LF_FP32 = 0, 1, 2
+LF_OK, LF_E_NULL, LF_E_SHAPE, LF_E_UNSUPPORTED, LF_E_WORKSPACE, LF_E_DTYPE = 0, -1, -2, -3, -4, -5
 KERNEL_AUTO, KERNEL_VALU, KERNEL_MFMA = 0, 1, 2
 
 
@@ -59,6 +60,13 @@ class PackedLayer(ctypes.Structure):
     ]
 
 
+class PackSource(ctypes.Structure):
+    """``lf_pack_source``."""
+
+    _fields_ = [("k", c_void_p), ("v", c_void_p), ("stride_b", c_int64), ("stride_h", c_int64),
+                ("stride_t", c_int64)]
+
+
 class DecodeArgs(ctypes.Structure):
     """``lf_decode_args``."""
 
@@ -86,6 +94,8 @@ _SIGNATURES = {
     "lf_status_string": (c_char_p, [c_int32]),
     "lf_pack_pages": (c_int32, [POINTER(PackedLayer), c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64,
                                 c_void_p, c_int32, c_void_p]),
+    "lf_pack_pages_multi": (c_int32, [c_void_p, POINTER(PackedLayer), c_void_p, POINTER(PackSource), c_int32,
+                                      c_int32, c_void_p, c_int32, c_void_p]),
     "lf_plan_decode": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "lf_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "lf_decode_attention": (c_int32, [POINTER(PackedLayer), POINTER(DecodeArgs), c_void_p]),
@@ -96,7 +106,7 @@ _SIGNATURES = {
                                   c_void_p]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _LIB = None
 
 

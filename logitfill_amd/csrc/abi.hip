@@ -8,6 +8,9 @@ namespace lf {
 int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v_src, int src_dtype,
                       int64_t sb, int64_t sh, int64_t st, const int32_t* jobs, int n_jobs,
                       hipStream_t stream);
+int launch_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_layer* layers_host,
+                            const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int n_layers,
+                            int src_dtype, const int32_t* jobs, int n_jobs, hipStream_t stream);
 int launch_decode_valu(const DecodeParams& p, hipStream_t stream);
 int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled);
 int launch_dequantize(const lf_packed_layer& L, int b, int tokens, float* k_out, float* v_out,
@@ -95,6 +98,22 @@ int32_t lf_pack_pages(const lf_packed_layer* layer, const void* k_src, const voi
     if (layer->page_size > 1024 || layer->head_dim > 512) return LF_E_SHAPE;
     return lf::launch_pack_pages(*layer, k_src, v_src, src_dtype, src_stride_b, src_stride_h, src_stride_t,
                                  jobs, n_jobs, static_cast<hipStream_t>(stream));
+}
+
+int32_t lf_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_layer* layers_host,
+                            const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int32_t n_layers,
+                            int32_t src_dtype, const int32_t* jobs, int32_t n_jobs, void* stream) {
+    if (n_layers < 0 || n_jobs < 0) return LF_E_SHAPE;
+    if (n_jobs == 0 || n_layers == 0) return n_jobs == 0 ? LF_OK : LF_E_SHAPE;
+    if (!layers_dev || !layers_host || !srcs_dev || !srcs_host || !jobs) return LF_E_NULL;
+    if (!valid_dtype(src_dtype)) return LF_E_DTYPE;
+    for (int32_t i = 0; i < n_layers; ++i) {
+        const int32_t st = check_layer(&layers_host[i]);
+        if (st != LF_OK) return st;
+        if (!srcs_host[i].k || !srcs_host[i].v) return LF_E_NULL;
+    }
+    return lf::launch_pack_pages_multi(layers_dev, layers_host, srcs_dev, srcs_host, n_layers, src_dtype, jobs,
+                                       n_jobs, static_cast<hipStream_t>(stream));
 }
 
 int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split, int32_t residual_pages,

@@ -412,15 +412,14 @@ __device__ __forceinline__ void pack_value_page(const lf_packed_layer& L, const 
     }
 }
 
+// One page of one kv head (blockIdx.y) of layer ``L``: the Key page (blockIdx.z == 0) or the
+// Value page.  Source rows tok0 .. tok0 + 127 of sequence b (element strides sb, sh, st) are
+// written as page ``page`` of sequence b.
 template <bool IsHalf>
-__global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) {
-    const lf_packed_layer& L = a.L;
-    const int job = blockIdx.x;
+__device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const void* k_src, const void* v_src,
+                                               int64_t sb, int64_t sh, int64_t st, int b, int64_t tok0, int page) {
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
-    const int b = a.jobs[3 * job + 0];
-    const int64_t tok0 = a.jobs[3 * job + 1];
-    const int page = a.jobs[3 * job + 2];
     const int64_t dst_tok0 = static_cast<int64_t>(page) * kFastP;
     constexpr int D = 128;
 
@@ -440,13 +439,12 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
     // ---- stage the page and this head's tier tables (layout.py:49-68): all their global loads
     // go out before the first wait ----
     {
-        const uint16_t* src = static_cast<const uint16_t*>(value_part ? a.v_src : a.k_src) + b * a.sb + h * a.sh +
-                              tok0 * a.st;
+        const uint16_t* src = static_cast<const uint16_t*>(value_part ? v_src : k_src) + b * sb + h * sh + tok0 * st;
         uint4 kv[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + kFastThreads * i;  // 16-byte chunk: row idx / 16, column 8 (idx % 16)
-            kv[i] = *reinterpret_cast<const uint4*>(src + (idx >> 4) * a.st + 8 * (idx & 15));
+            kv[i] = *reinterpret_cast<const uint4*>(src + (idx >> 4) * st + 8 * (idx & 15));
         }
         int my_idx = 0, my_cnt = 0;
         if (!value_part) {
@@ -573,6 +571,31 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) 
     }
 }
 
+template <bool IsHalf>
+__global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) {
+    const int job = blockIdx.x;
+    pack_fast_page<IsHalf>(a.L, a.k_src, a.v_src, a.sb, a.sh, a.st, a.jobs[3 * job + 0], a.jobs[3 * job + 1],
+                           a.jobs[3 * job + 2]);
+}
+
+// Several layers' pages in one launch: job = (layer, b, src_token0, dst_page); the layer's
+// descriptor and page source are read from device memory.
+struct PackMultiArgs {
+    const lf_packed_layer* layers;
+    const lf_pack_source* srcs;
+    const int32_t* jobs;
+};
+
+template <bool IsHalf>
+__global__ __launch_bounds__(kFastThreads) void pack_fast_multi_kernel(PackMultiArgs m) {
+    const int job = blockIdx.x;
+    const int layer = __builtin_amdgcn_readfirstlane(m.jobs[4 * job + 0]);
+    const lf_packed_layer& L = m.layers[layer];
+    const lf_pack_source& S = m.srcs[layer];
+    pack_fast_page<IsHalf>(L, S.k, S.v, S.stride_b, S.stride_h, S.stride_t, m.jobs[4 * job + 1], m.jobs[4 * job + 2],
+                           m.jobs[4 * job + 3]);
+}
+
 bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
     return vec16 && src_dtype != LF_FP32 && L.head_dim == 128 && L.page_size == kFastP && L.k_group == kFastP &&
            L.v_group == 128 && L.bit_v == 2 && L.v_groups == 1 && L.v_words == 8;
@@ -656,6 +679,40 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
     else if (src_dtype == LF_FP32) rc = launch_one<float, false>(a, grid, lds, stream);
     else return LF_E_DTYPE;
     if (rc != LF_OK) return rc;
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? LF_OK : static_cast<int>(err);
+}
+
+int launch_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_layer* layers_host,
+                            const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int n_layers,
+                            int src_dtype, const int32_t* jobs, int n_jobs, hipStream_t stream) {
+    if (src_dtype == LF_FP32) return LF_E_UNSUPPORTED;
+    size_t lds = 0;
+    for (int i = 0; i < n_layers; ++i) {
+        const lf_packed_layer& L = layers_host[i];
+        const lf_pack_source& S = srcs_host[i];
+        if (L.n_kv != layers_host[0].n_kv) return LF_E_SHAPE;
+        const uintptr_t kp = reinterpret_cast<uintptr_t>(S.k), vp = reinterpret_cast<uintptr_t>(S.v);
+        const bool vec16 = ((kp | vp) % 16 == 0) && ((S.stride_b * 2) % 16 == 0) && ((S.stride_h * 2) % 16 == 0) &&
+                           ((S.stride_t * 2) % 16 == 0);
+        if (!pack_fast_ok(L, src_dtype, vec16)) return LF_E_UNSUPPORTED;
+        const size_t l = pack_fast_lds_bytes(L);
+        lds = l > lds ? l : lds;
+    }
+    if (lds > 160 * 1024) return LF_E_SHAPE;
+    static size_t limit[2] = {64 * 1024, 64 * 1024};
+    const int half = src_dtype == LF_FP16;
+    const void* fn = half ? reinterpret_cast<const void*>(&pack_fast_multi_kernel<true>)
+                          : reinterpret_cast<const void*>(&pack_fast_multi_kernel<false>);
+    if (lds > limit[half]) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return static_cast<int>(e);
+        limit[half] = lds;
+    }
+    PackMultiArgs m{layers_dev, srcs_dev, jobs};
+    const dim3 grid(n_jobs, layers_host[0].n_kv, 2);  // z: Key page, Value page
+    if (half) hipLaunchKernelGGL(pack_fast_multi_kernel<true>, grid, dim3(kFastThreads), lds, stream, m);
+    else hipLaunchKernelGGL(pack_fast_multi_kernel<false>, grid, dim3(kFastThreads), lds, stream, m);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? LF_OK : static_cast<int>(err);
 }

@@ -78,6 +78,10 @@ class _LayerStore:
         self._tail_len_dev: Optional[torch.Tensor] = None
         self._tail_dirty = True
         self.decode_plan = None        # cached work plan, owned by the decode dispatcher
+        # Deferred flushes (extension): full residual pages (b, dst_page) not yet packed.  Set
+        # by the manager; every reader of the history packs them first.
+        self.defer_flush = False
+        self._pending: list[tuple[int, int]] = []
         if capacity_tokens:
             self.reserve(capacity_tokens)
 
@@ -115,6 +119,7 @@ class _LayerStore:
 
     def history_views(self, b: int = 0):
         """Reference-shaped views of sequence ``b``'s packed history (``cache.py:64-81``), or ``(None, None)``."""
+        self.flush()
         H = self.hist_lens[b]
         if H == 0:
             return None, None
@@ -217,6 +222,7 @@ class _LayerStore:
         self.tail_lens = [0] * self.batch
         self._tail_dirty = True
         self.decode_plan = None
+        self._pending = []
 
     def append(self, key: torch.Tensor, value: torch.Tensor) -> None:
         """``cache.py:48-62`` for one sequence: ``key/value [n_kv, T, D]``; flushes full pages."""
@@ -246,6 +252,7 @@ class _LayerStore:
             raise ValueError("lengths must give 0 <= length <= T for every sequence")
         if max(lens) == 0:
             return
+        self.flush()
         P = self.page_size
         if self._tail_k is None:
             self._tail_k = torch.zeros(B, H, P, D, dtype=key.dtype, device=self.device)
@@ -291,13 +298,21 @@ class _LayerStore:
                 idx = torch.tensor(bs, device=self.device)
                 self._tail_k[idx, :, tl:tl + n1] = key[idx, :, :n1]
                 self._tail_v[idx, :, tl:tl + n1] = value[idx, :, :n1]
-        # 2) pack full pages in place
+        # 2) pack full pages in place -- or, for a deferring store on a step that only completes
+        # residual pages, leave them full in the residual buffers until flush()
+        defer = self.defer_flush and bool(tail_jobs) and not src_jobs and not rest
         if tail_jobs or src_jobs:
             self.reserve(max(hist_pages) * P)
-            if tail_jobs:
-                self._pack(self._tail_k, self._tail_v, tail_jobs)
-            if src_jobs:
-                self._pack(key, value, src_jobs)
+            if defer:
+                for b, _, page in tail_jobs:
+                    self._pending.append((b, page))
+                    hist_pages[b] -= 1
+                    new_tail[b] = P
+            else:
+                if tail_jobs:
+                    self._pack(self._tail_k, self._tail_v, tail_jobs)
+                if src_jobs:
+                    self._pack(key, value, src_jobs)
         # 3) start the next residual pages
         for b, (pos, end) in rest.items():
             n = end - pos
@@ -305,6 +320,27 @@ class _LayerStore:
             self._tail_v[b, :, :n].copy_(value[b, :, pos:end])
         self.hist_lens = [p * P for p in hist_pages]
         self.tail_lens = new_tail
+        self._tail_dirty = True
+
+    @property
+    def pending(self) -> list[tuple[int, int]]:
+        """Deferred page flushes ``(b, dst_page)``."""
+        return list(self._pending)
+
+    def flush(self) -> None:
+        """Pack the deferred residual pages of this layer (one launch)."""
+        if not self._pending:
+            return
+        jobs = [(b, 0, page) for b, page in self._pending]
+        self._pack(self._tail_k, self._tail_v, jobs)
+        self._complete_pending()
+
+    def _complete_pending(self) -> None:
+        P = self.page_size
+        for b, _ in self._pending:
+            self.hist_lens[b] += P
+            self.tail_lens[b] = 0
+        self._pending = []
         self._tail_dirty = True
 
     def _pack(self, k_src: torch.Tensor, v_src: torch.Tensor, jobs: list) -> None:
@@ -358,6 +394,7 @@ class _LayerStore:
 
     def dequantize(self, b: int = 0):
         """``cache.py:83-90``: dense float32 ``(K, V) [n_kv, hist_len, D]`` of sequence ``b`` (HIP kernel)."""
+        self.flush()
         H = self.hist_lens[b]
         D = self.head_dim
         k = torch.empty(self.n_kv, H, D, dtype=torch.float32, device=self.device)
@@ -373,7 +410,8 @@ class PackedKVManager:
     """Per-layer packed KV for ``batch_size`` sequences (reference ``cache.py:93-140``)."""
 
     def __init__(self, levels, n_q: int, n_kv: int, head_dim: int, page_size: int, k_group_size: int,
-                 v_group_size: int, bit_v: int, device, *, batch_size: int = 1, capacity_tokens: int = 0):
+                 v_group_size: int, bit_v: int, device, *, batch_size: int = 1, capacity_tokens: int = 0,
+                 defer_flush: bool = False):
         self.n_q = int(n_q)
         self.n_kv = int(n_kv)
         self.head_dim = int(head_dim)
@@ -397,6 +435,63 @@ class PackedKVManager:
             self.layers.append(_LayerStore(values, page_size, k_group_size, v_group_size, bit_v, device=self.device,
                                            batch=self.batch_size, capacity_tokens=capacity_tokens))
         self._workspace: Optional[torch.Tensor] = None
+        self._flush_keepalive = None
+        self.defer_flush = bool(defer_flush)
+
+    @property
+    def defer_flush(self) -> bool:
+        """Extension: commits that complete residual pages leave them for ``flush_pending``.
+
+        The reference packs each layer's full page inside that layer's commit
+        (``cache.py:54-62``).  Every layer of a decode step fills its page on the
+        same token and the packed page is read only by the next step, so a
+        deferring manager packs all layers' pages in one launch at the end of the
+        step.  Readers of a layer's history (attention, dequantize, the history
+        views, the next append) pack that layer's pending pages first.
+        """
+        return self._defer_flush
+
+    @defer_flush.setter
+    def defer_flush(self, value: bool) -> None:
+        self._defer_flush = bool(value)
+        for layer in self.layers:
+            layer.defer_flush = self._defer_flush
+            if not value:
+                layer.flush()
+
+    def flush_pending(self) -> None:
+        """Pack every layer's deferred pages: one ``lf_pack_pages_multi`` launch."""
+        todo = [layer for layer in self.layers if layer._pending]
+        if not todo:
+            return
+        if len(todo) == 1:
+            todo[0].flush()
+            return
+        dtypes = {layer._tail_k.dtype for layer in todo}
+        n = len(todo)
+        structs = (_native.PackedLayer * n)(*[layer.layer_struct() for layer in todo])
+        srcs = (_native.PackSource * n)()
+        for i, layer in enumerate(todo):
+            tk, tv = layer._tail_k, layer._tail_v
+            srcs[i] = _native.PackSource(tk.data_ptr(), tv.data_ptr(), tk.stride(0), tk.stride(1), tk.stride(2))
+        st = _native.LF_E_UNSUPPORTED if len(dtypes) != 1 else None
+        if st is None:
+            dev_structs = torch.frombuffer(bytearray(structs), dtype=torch.uint8).to(self.device)
+            dev_srcs = torch.frombuffer(bytearray(srcs), dtype=torch.uint8).to(self.device)
+            jobs = [(i, b, 0, page) for i, layer in enumerate(todo) for b, page in layer._pending]
+            jobs_dev = torch.tensor(jobs, dtype=torch.int32).to(self.device)
+            st = _native.load().lf_pack_pages_multi(
+                dev_structs.data_ptr(), structs, dev_srcs.data_ptr(), srcs, n, _native.dtype_code(dtypes.pop()),
+                jobs_dev.data_ptr(), len(jobs), _native.current_stream_ptr(self.device))
+            self._flush_keepalive = (dev_structs, dev_srcs, jobs_dev)
+        if st == _native.LF_E_UNSUPPORTED:
+            # shapes outside the multi-layer kernel: one pack launch per layer
+            for layer in todo:
+                layer.flush()
+            return
+        _native.check(st, "lf_pack_pages_multi")
+        for layer in todo:
+            layer._complete_pending()
 
     def reset(self) -> None:
         self.seq_len = 0

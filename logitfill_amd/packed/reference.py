@@ -56,6 +56,7 @@ def reference_attention(manager, layer_idx: int, query: torch.Tensor, key_new: t
     History is dequantised by the HIP kernel; attention is float32.
     """
     layer = manager.layers[layer_idx]
+    layer.flush()  # deferred residual pages of this layer, if any
     if query.shape[0] != layer.batch:
         raise ValueError(f"query batch {query.shape[0]} != cache batch {layer.batch}")
     if not query.is_cuda:
@@ -160,6 +161,7 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     nothing synchronises.
     """
     layer = manager.layers[layer_idx]
+    layer.flush()  # deferred residual pages of this layer, if any
     B, D = layer.batch, layer.head_dim
     q_len = int(query.shape[2]) if query.dim() == 4 else 1
     tok = (q_len,) if query.dim() == 4 else ()

@@ -62,7 +62,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
         assert name in _native._SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.lf_abi_version() == 4
+    assert lib.lf_abi_version() == 5
     assert b"gfx950" in lib.lf_build_info()
 
 
@@ -70,6 +70,7 @@ def test_struct_layouts_match_c(tmp_path):
     fields = {
         "lf_packed_layer": [f for f, _ in _native.PackedLayer._fields_],
         "lf_decode_args": [f for f, _ in _native.DecodeArgs._fields_],
+        "lf_pack_source": [f for f, _ in _native.PackSource._fields_],
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for st, fs in fields.items():
@@ -83,7 +84,8 @@ def test_struct_layouts_match_c(tmp_path):
     subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
     out = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
                                                                check=True).stdout.split("\n") if line)
-    for st, cls in (("lf_packed_layer", _native.PackedLayer), ("lf_decode_args", _native.DecodeArgs)):
+    for st, cls in (("lf_packed_layer", _native.PackedLayer), ("lf_decode_args", _native.DecodeArgs),
+                    ("lf_pack_source", _native.PackSource)):
         assert int(out[st]) == ctypes.sizeof(cls), st
         for f in fields[st]:
             assert int(out[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
