@@ -34,7 +34,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2_k4"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2_k4", "c4"])
     p.add_argument("--layers", type=int, default=None)
     p.add_argument("--kernel", default="auto", choices=["auto", "valu", "mfma"])
     p.add_argument("--pages-per-split", type=int, default=None)
@@ -42,6 +42,8 @@ def parse_args():
     p.add_argument("--no-dense", action="store_true", help="skip the BF16 dense comparator")
     p.add_argument("--no-compress", action="store_true", help="skip the page-compress (config 3) timing")
     p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the other decode configs (c2 at target 3.0, c1, c4) reported beside the headline")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                    help="only run a plain device-to-device copy of BYTES (3 times) and exit: the reference "
                         "kernel that scales the PMC byte counters (FETCH_SIZE / WRITE_SIZE)")
@@ -104,22 +106,46 @@ def build_state(cfg, layers, dev):
     from logitfill_amd.packed import PackedKVManager
 
     B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
-    pages, resid, tb = cfg["pages"], cfg["residual"], cfg["target_bit"]
+    pages, resid, tb = seq_lengths(cfg)
     levels = [synth.sample_tier_levels(n_kv, D, tb, seed=layer) for layer in range(layers)]
     mgr = PackedKVManager(levels, n_q, n_kv, D, 128, 128, 128, 2, dev, batch_size=B,
-                          capacity_tokens=pages * 128)
+                          capacity_tokens=max(pages) * 128)
     inputs = []
+    T = max(pages) * 128 + 128  # every sequence's residual slice below is 127 tokens long
     for layer in range(layers):
-        d = synth.make_layer(B, n_q, n_kv, D, pages * 128 + resid, tb, seed=layer, device=dev)
+        d = synth.make_layer(B, n_q, n_kv, D, T, tb, seed=layer, device=dev)
         st = mgr.layers[layer]
-        st.fill_pages(d.key, d.value, [pages] * B)
-        if resid:
-            st.set_tail(d.key[:, :, pages * 128:], d.value[:, :, pages * 128:], [resid] * B)
+        st.fill_pages(d.key, d.value, pages)
+        if max(resid):
+            # sequence b's residual: its tokens right after its pages
+            rk = torch.stack([d.key[b, :, pages[b] * 128:pages[b] * 128 + 127] for b in range(B)])
+            rv = torch.stack([d.value[b, :, pages[b] * 128:pages[b] * 128 + 127] for b in range(B)])
+            st.set_tail(rk, rv, resid)
+            del rk, rv
         inputs.append((d.query.contiguous(), d.key_new.contiguous(), d.value_new.contiguous()))
         del d
         torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return mgr, inputs
+
+
+def context_text(cfg) -> str:
+    if cfg["pages"] is None:
+        return "ragged contexts U[4K, 64K] (full pages + residual 1-127, seeded)"
+    return f"{cfg['pages']} pages + {cfg['residual']} residual"
+
+
+def seq_lengths(cfg):
+    """Per-sequence (full pages, residual tokens) and the target bit of a config; c4's contexts
+    are ragged (uniform in [4K, 64K], seeded)."""
+    from logitfill_amd import synth
+
+    B = cfg["batch"]
+    if cfg["pages"] is None:
+        pages, resid = synth.ragged_lengths(B, seed=4)
+    else:
+        pages, resid = [cfg["pages"]] * B, [cfg["residual"]] * B
+    return pages, resid, cfg["target_bit"]
 
 
 def time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split):
@@ -149,6 +175,26 @@ def time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split):
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end)
     return ms / steps, wall / steps * 1e3
+
+
+def decode_point(cfg, layers, steps, warmup, kernel, pages_per_split, dev):
+    """Build ``layers`` layers of a config, time the decode; returns (us per layer-step, bytes per
+    layer-step, payload bytes per layer-step, wall ms per step) and frees the state."""
+    import torch
+
+    mgr, inputs = build_state(cfg, layers, dev)
+    ms_step, wall_ms = time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split)
+    n_q, n_kv, D = cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
+    pages, resid, _ = seq_lengths(cfg)
+    tot, pay = 0, 0
+    for st in mgr.layers:
+        for p, r in zip(pages, resid):
+            t, pl = algorithmic_bytes(st.widths, st.words, n_kv, n_q, D, p * 128, r + 1)
+            tot += t
+            pay += pl
+    del mgr, inputs
+    torch.cuda.empty_cache()
+    return ms_step * 1e3 / layers, tot / layers, pay / layers, wall_ms
 
 
 def time_dense(cfg, steps, warmup):
@@ -271,7 +317,8 @@ def cpu_baseline(cfg, n_seqs):
     from oracle import history as ohist
 
     B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
-    pages, resid, tb = cfg["pages"], cfg["residual"], cfg["target_bit"]
+    pages_b, resid_b, tb = seq_lengths(cfg)
+    pages, resid = pages_b[0], resid_b[0]
     cores = max(1, min(16, os.cpu_count() or 1))
     times = []
     with threadpool_limits(limits=cores):
@@ -314,23 +361,14 @@ def main():
     layers = args.layers or cfg["layers"]
     dev = torch.device("cuda", 0)
     kernel = {"auto": _native.KERNEL_AUTO, "valu": _native.KERNEL_VALU, "mfma": _native.KERNEL_MFMA}[args.kernel]
-    print(f"[bench] building {layers} layers of {args.config} ...", file=sys.stderr, flush=True)
-    mgr, inputs = build_state(cfg, layers, dev)
-    print("[bench] timing ...", file=sys.stderr, flush=True)
-    ms_step, wall_ms = time_decode(mgr, inputs, args.steps, args.warmup, kernel, args.pages_per_split)
-
+    print(f"[bench] building {layers} layers of {args.config} and timing ...", file=sys.stderr, flush=True)
+    us_layer, bytes_launch, pay_launch, wall_ms = decode_point(cfg, layers, args.steps, args.warmup, kernel,
+                                                               args.pages_per_split, dev)
+    ms_step = us_layer * layers / 1e3
     B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
-    H = cfg["pages"] * 128
-    R1 = cfg["residual"] + 1
-    tot_bytes = 0
-    pay_bytes = 0
-    for st in mgr.layers:
-        t, p = algorithmic_bytes(st.widths, st.words, n_kv, n_q, D, H, R1)
-        tot_bytes += t * B
-        pay_bytes += p * B
-    us_layer = ms_step * 1e3 / layers
-    launch_s = ms_step / 1e3 / layers
-    bytes_launch = tot_bytes / layers
+    tot_bytes = bytes_launch * layers
+    pay_bytes = pay_launch * layers
+    launch_s = us_layer / 1e6
     achieved = bytes_launch / launch_s / 1e9
     result = {
         "metric": "packed decode-attn us/step + achieved HBM GB/s (% of peak), 7B GQA shape @32K ctx",
@@ -346,8 +384,7 @@ def main():
         "dtype": "u8",
         "data": "synthetic (seeded logitfill_amd.synth: K~N(0,1)*LogNormal channel scale + outliers, V,Q~N)",
         "config": {"workload": f"{args.config}: packed decode attention, {layers} layers x batch {B}, "
-                               f"{n_q}q/{n_kv}kv heads, D {D}, {cfg['pages']} pages + {cfg['residual']} residual, "
-                               f"target_bit {cfg['target_bit']}",
+                               f"{n_q}q/{n_kv}kv heads, D {D}, {context_text(cfg)}, target_bit {cfg['target_bit']}",
                    "kernel": args.kernel, "layers": layers, "batch": B},
         "hbm_gbs": round(achieved, 1),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -358,7 +395,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(args.config) if args.layers in (None, cfg["layers"]) else None},
     }
-    if not args.no_dense:
+    if not args.no_dense and cfg["pages"] is not None:
         print("[bench] bf16 dense comparator ...", file=sys.stderr, flush=True)
         dense_us, dense_bytes = time_dense(cfg, max(args.steps, 10), args.warmup)
         result["dense_bf16"] = {
@@ -375,18 +412,33 @@ def main():
         print("[bench] page compress (config 3) ...", file=sys.stderr, flush=True)
         comp = {}
         for tb in (2.5, 3.0, 4.0):
-            us, us_layer, ph, rd, wr = time_compress(tb, 10, 2)
-            comp[f"target_{tb}"] = {"us_per_pass": round(us, 1), "page_heads": ph,
-                                    "pages_per_s": round(ph / us * 1e6), "gbs": round((rd + wr) / us / 1e3, 1),
-                                    "hbm_frac": round((rd + wr) / us / 1e3 / HBM_PEAK_GBS, 4),
+            us_c, us_c_layer, ph, rd, wr = time_compress(tb, 10, 2)
+            comp[f"target_{tb}"] = {"us_per_pass": round(us_c, 1), "page_heads": ph,
+                                    "pages_per_s": round(ph / us_c * 1e6), "gbs": round((rd + wr) / us_c / 1e3, 1),
+                                    "hbm_frac": round((rd + wr) / us_c / 1e3 / HBM_PEAK_GBS, 4),
                                     "bytes_read": rd, "bytes_written": wr,
-                                    "us_per_pass_one_launch_per_layer": round(us_layer, 1)}
+                                    "us_per_pass_one_launch_per_layer": round(us_c_layer, 1)}
         result["compress_c3"] = {
             "what": "BASELINE config 3: 64 sequences x 1 page x 4 kv heads x 28 layers, bf16 K/V from the "
                     "config-0 distributions; us_per_pass = one lf_pack_pages_multi launch for the 28 layers (a "
                     "deferring manager's end-of-step flush), us_per_pass_one_launch_per_layer = 28 lf_pack_pages "
                     "launches; pages_per_s counts page-heads",
             **comp}
+    if not args.no_extra and args.config == "c2" and args.layers is None:
+        extra = {}
+        for name, n_layers in (("c2_k4", None), ("c1", None), ("c4", 8)):
+            c = dict(synth.CONFIGS[name])
+            nl = n_layers or c["layers"]
+            print(f"[bench] {name} ({nl} layers) ...", file=sys.stderr, flush=True)
+            us_x, bytes_x, pay_x, _ = decode_point(c, nl, 10, 2, kernel, None, dev)
+            extra[name] = {"workload": f"{c['layers']}-layer model shape timed on {nl} distinct layers, batch "
+                                       f"{c['batch']}, {c['n_q']}q/{c['n_kv']}kv heads, {context_text(c)}, "
+                                       f"target_bit {c['target_bit']}",
+                           "us_per_layer_step": round(us_x, 2), "bytes_per_layer_step": int(bytes_x),
+                           "hbm_gbs": round(bytes_x / us_x / 1e3, 1),
+                           "hbm_frac": round(bytes_x / us_x / 1e3 / HBM_PEAK_GBS, 4),
+                           "payload_gbs": round(pay_x / us_x / 1e3, 1)}
+        result["other_configs"] = extra
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seqs)
