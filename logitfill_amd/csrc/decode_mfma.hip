@@ -815,7 +815,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
         const int sh = 2 * (n16 & 3);
         const int tok0 = 32 * wave + n16, tok1 = tok0 + 16;
-        for (int page = pbeg; page < pend; ++page) {
+        // Pages in chunks of 64; between chunks the midpoint term is folded into O (below).
+        for (int cbeg = pbeg; cbeg < pend; cbeg += 64) {
+        const int cend = min(cbeg + 64, pend);
+        for (int page = cbeg; page < cend; ++page) {
             const int rel = page - pbeg;
             // Page landed (every wave's share) and page - 1 computed: the prepared buffer and
             // page - 1's slot are free.  (On the first page this also orders the set-up above:
@@ -964,6 +967,33 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
                 O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }
+        }
+        // After each 64-page chunk (but the last), fold the midpoint term into O: the Value
+        // product accumulates p' * (4 + code) and the offset cancels against
+        // sum p * (vmin - 4 vscale) only when the two meet, so the rounding of that
+        // cancellation would otherwise grow with the pages of the item (one 256-page item:
+        // 3e-4 relative).  Head totals of mid_run (the two tiles, then the 4 lane groups) go
+        // to the hi rows 4 * kb + r of lanes kb < 2 through this wave's alpha row, and
+        // mid_run restarts at 0.
+        if (cend < pend) {
+            float mid = mid_run + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mid_run),
+                                                                                       0x128, 0xf, 0xf, false));
+            mid = rows_sum(mid);
+            if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = mid;
+            __builtin_amdgcn_wave_barrier();
+            if (kb < 2) {
+                const float4 mrow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * kb);
+#pragma unroll
+                for (int nt = 0; nt < 8; ++nt) {
+                    O[nt][0] += mrow.x;
+                    O[nt][1] += mrow.y;
+                    O[nt][2] += mrow.z;
+                    O[nt][3] += mrow.w;
+                }
+            }
+            mid_run = 0.f;
+            __builtin_amdgcn_wave_barrier();
+        }
         }
         // Reduce l and the midpoint term over the two tiles (lanes n16, n16 ^ 8) and the 4 lane
         // groups of each head.
