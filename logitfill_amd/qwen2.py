@@ -85,12 +85,19 @@ def detach_packed(model) -> None:
 
 class PackedDecoder:
     """Prefill + token-by-token decode of a ``Qwen2ForCausalLM`` over a packed cache (batch 1,
-    as the reference).  ``step`` returns the logits of the last position."""
+    as the reference).  ``step`` returns the logits of the last position.  After each forward
+    pass the manager's deferred page flushes (``defer_flush=True``: every layer's completed
+    page, one launch) are packed; with eager flushes there is nothing pending."""
 
     def __init__(self, model, manager, attention_fn=packed_attention):
         self.model, self.manager = model, manager
         attach_packed(model, manager, attention_fn)
         self.pos = 0
+
+    def _flush(self) -> None:
+        flush = getattr(self.manager, "flush_pending", None)  # managers without deferral have none
+        if flush is not None:
+            flush()
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
@@ -98,6 +105,7 @@ class PackedDecoder:
         n = input_ids.shape[-1]
         pos = torch.arange(n, device=input_ids.device)[None]
         logits = self.model(input_ids=input_ids, position_ids=pos, use_cache=False).logits
+        self._flush()
         self.pos = n
         return logits[:, -1]
 
@@ -106,5 +114,6 @@ class PackedDecoder:
         ids = token.view(1, 1)
         pos = torch.full((1, 1), self.pos, dtype=torch.long, device=ids.device)
         logits = self.model(input_ids=ids, position_ids=pos, use_cache=False).logits
+        self._flush()
         self.pos += 1
         return logits[:, -1]

@@ -24,13 +24,13 @@ def _model(dev):
     return Qwen2ForCausalLM(cfg).to(dev).float().eval()
 
 
-def _manager(dev):
+def _manager(dev, defer_flush=False):
     levels = [synth.sample_tier_levels(2, 128, 2.5, seed=s) for s in range(2)]
-    return PackedKVManager(levels, 4, 2, 128, 128, 128, 128, 2, dev)
+    return PackedKVManager(levels, 4, 2, 128, 128, 128, 128, 2, dev, defer_flush=defer_flush)
 
 
-def _run(model, dev, attention_fn, prompt, forced):
-    mgr = _manager(dev)
+def _run(model, dev, attention_fn, prompt, forced, defer_flush=False):
+    mgr = _manager(dev, defer_flush)
     dec = PackedDecoder(model, mgr, attention_fn)
     out = [dec.prefill(prompt).float()]
     for tok in forced:
@@ -70,3 +70,17 @@ def test_detach_restores_the_model(gpu):
     with torch.no_grad():
         after = model(input_ids=ids, use_cache=False).logits
     assert torch.equal(before, after)
+
+
+def test_deferred_flushes_give_the_same_logits(gpu):
+    """The decoder with deferred page flushes (both layers' page at position 384 packed by one
+    lf_pack_pages_multi launch after the step) reproduces the eager-flush logits exactly."""
+    model = _model(gpu)
+    g = torch.Generator().manual_seed(5)
+    prompt = torch.randint(0, 512, (1, 380), generator=g).to(gpu)
+    forced = torch.randint(0, 512, (10,), generator=g).to(gpu)
+    eager, _ = _run(model, gpu, packed_attention, prompt, forced)
+    lazy, mgr = _run(model, gpu, packed_attention, prompt, forced, defer_flush=True)
+    assert mgr.defer_flush and all(layer.pending == [] for layer in mgr.layers)
+    assert mgr.layers[0].hist_len == 384 and mgr.layers[1].hist_len == 384
+    assert torch.equal(eager, lazy)
