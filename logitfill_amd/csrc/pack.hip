@@ -298,26 +298,14 @@ int pack_code_row(const lf_packed_layer& L);
 
 // ---------------------------------------------------------------------------------------
 // Fast path for the common shape: page = Key group = Value group = head_dim = 128, int2
-// Values, 2-byte inputs with 16-byte aligned rows.  Two workgroups of 1024 threads per page
-// and kv head (blockIdx.z 0: Key page, 1: Value page), so two run on a CU; per element the
-// division uses a correctly rounded reciprocal of the group scale and one Markstein
-// correction (see div_rn).  Every phase is branch-free per element.
-//
-//   stage     the page into LDS (rows padded to 130 halves), this head's tier tables, the
-//             code rows zeroed; padding slots' scale/min (1.0, 0.0) stored
-//   phase 1   Key min/max partials: thread (channel c = tid % 128, tokens 16 (tid / 128) + 0..15);
-//             the 16 values stay in registers
-//   phase 2   every thread merges the 8 partials of its own channel: min, scale, reciprocal
-//             (the token-block-0 thread stores the fp16 scale/min)
-//   phase 3   the channel's 16 codes into an LDS byte row per token; each integer tier has a
-//             16-byte aligned segment of the row, in slot order
-//   phase 4   thread (token tid / 8, q = tid % 8) assembles words q, q + 8, ... of the token's
-//             integer tiers from 16 / 8 / 4 code bytes (one LDS read each) and copies the fp16
-//             tier
-//   Values    thread (token tid / 8, channels 16 (tid % 8) + 0..15) = one code word; the
-//             token's min/max over its 8 threads by lane exchange
+// Values, 2-byte inputs with 16-byte aligned rows.  Two workgroups of 512 threads per page and
+// kv head (blockIdx.z 0: Key page, 1: Value page), about 39 KB of LDS for a Key workgroup, so
+// four share a CU; per element the division uses a correctly rounded reciprocal of the group
+// scale and one Markstein correction (see div_rn), branch-free.  The phases are listed at
+// pack_fast_page.  Each integer tier has a 16-byte aligned segment of a token's code row (in
+// slot order), so a word's 16 / 8 / 4 code bytes are one LDS read.
 // ---------------------------------------------------------------------------------------
-constexpr int kFastThreads = 1024;
+constexpr int kFastThreads = 512;
 constexpr int kFastP = 128;
 constexpr int kFastLd = 130;  // halves per staged row
 
@@ -373,27 +361,22 @@ __device__ __forceinline__ uint32_t word_int4(uint2 b) {
     return __builtin_amdgcn_perm(t1, t0, 0x06040200u);
 }
 
-// Phase 5 of the fast path: Values, one code word per thread (layout.py:115-129).
+// Values of one token row: thread (token tk, channels 16 w + 0..15) holds its 32 bytes in ``r``
+// and produces one code word (layout.py:115-129); the token's min/max comes from its 8 lanes
+// (lanes 8k .. 8k + 7 of one wave) by lane exchange.
 template <bool IsHalf>
-__device__ __forceinline__ void pack_value_page(const lf_packed_layer& L, const uint16_t* vpage, int b, int h,
-                                                int64_t dst_tok0, int tid) {
-    const int tk = tid >> 3, w = tid & 7;
-    const uint32_t* row = reinterpret_cast<const uint32_t*>(vpage + tk * kFastLd + 16 * w);  // 4-byte aligned
+__device__ __forceinline__ void pack_value_row(const lf_packed_layer& L, const uint4 (&r)[2], int b, int h,
+                                               int64_t dst_tok, int w) {
+    const uint32_t pr[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
     float v[16];
     float lo = __builtin_inff(), hi = -__builtin_inff();
-    {
-        uint32_t pr[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = row[i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] & 0xffffu));
-            v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] >> 16));
-            lo = fminf(lo, fminf(v[2 * i], v[2 * i + 1]));
-            hi = fmaxf(hi, fmaxf(v[2 * i], v[2 * i + 1]));
-        }
+    for (int i = 0; i < 8; ++i) {
+        v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] & 0xffffu));
+        v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] >> 16));
+        lo = fminf(lo, fminf(v[2 * i], v[2 * i + 1]));
+        hi = fmaxf(hi, fmaxf(v[2 * i], v[2 * i + 1]));
     }
-    // the token's 8 threads are lanes 8k .. 8k + 7 of one wave
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) {
         lo = fminf(lo, __shfl_xor(lo, off, kWave));
@@ -404,7 +387,7 @@ __device__ __forceinline__ void pack_value_page(const lf_packed_layer& L, const 
     uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) word |= fast_code(v[i], lo, sc, y, 3.0f) << (2 * i);
-    const int64_t trow = tok_row(L, b, h, dst_tok0 + tk);
+    const int64_t trow = tok_row(L, b, h, dst_tok);
     L.v_code[trow * 8 + w] = static_cast<int32_t>(word);
     if (w == 0) {
         L.v_scale[trow] = f32_to_f16(sc);
@@ -412,9 +395,37 @@ __device__ __forceinline__ void pack_value_page(const lf_packed_layer& L, const 
     }
 }
 
+// LDS layout of the Key workgroup: the staged page (rows padded to 130 halves), partial
+// min/max, the fp16-tier values, the channel map; the code rows reuse the page once phase 1
+// has read it (or sit after the rest when they do not fit there).
+struct FastLds {
+    int pmm, f16, cpos, tidx, codes, total;
+};
+
+__device__ __host__ inline FastLds fast_lds(const lf_packed_layer& L) {
+    FastLds f;
+    const int page = kFastP * kFastLd * 2;
+    f.pmm = page;                                        // [4][128] float2
+    f.f16 = f.pmm + 4 * 128 * 8;                         // [128][w16] fp16
+    f.cpos = f.f16 + ((kFastP * L.k_width[3] * 2 + 15) & ~15);  // [128] int16
+    f.tidx = f.cpos + 128 * 2;                           // [w16] int16
+    const int end = f.tidx + ((L.k_width[3] * 2 + 15) & ~15);
+    const int cbytes = kFastP * code_segs(L).seg[3];
+    f.codes = cbytes <= page ? 0 : end;
+    f.total = (cbytes <= page ? end : end + cbytes) + 16;
+    return f;
+}
+
 // One page of one kv head (blockIdx.y) of layer ``L``: the Key page (blockIdx.z == 0) or the
 // Value page.  Source rows tok0 .. tok0 + 127 of sequence b (element strides sb, sh, st) are
-// written as page ``page`` of sequence b.
+// written as page ``page`` of sequence b.  512 threads: four workgroups share a CU.
+//   Value page  thread (token tid / 8 and + 64, 16 channels) reads its row slices from global
+//               memory directly: no LDS
+//   Key page    stage (page -> LDS, tier tables -> channel map); phase 1: thread (channel
+//               tid % 128, tokens 32 (tid / 128) + 0..31) min/max, fp16-tier values to LDS;
+//               phases 2, 3: the channel's scale and its 32 codes into byte rows over the
+//               page; phase 4: thread (token tid / 4, q) assembles words q, q + 4, ... of the
+//               token's integer tiers from 16 / 8 / 4 code bytes and copies the fp16 tier
 template <bool IsHalf>
 __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const void* k_src, const void* v_src,
                                                int64_t sb, int64_t sh, int64_t st, int b, int64_t tok0, int page) {
@@ -423,63 +434,68 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     const int64_t dst_tok0 = static_cast<int64_t>(page) * kFastP;
     constexpr int D = 128;
 
+    if (blockIdx.z != 0) {
+        // ---- Values: both rows' slices in flight before the first use ----
+        const uint16_t* src = static_cast<const uint16_t*>(v_src) + b * sb + h * sh + tok0 * st;
+        const int tk = tid >> 3, w = tid & 7;
+        uint4 r0[2], r1[2];
+        {
+            const uint4* a0 = reinterpret_cast<const uint4*>(src + tk * st + 16 * w);
+            const uint4* a1 = reinterpret_cast<const uint4*>(src + (tk + 64) * st + 16 * w);
+            r0[0] = a0[0]; r0[1] = a0[1]; r1[0] = a1[0]; r1[1] = a1[1];
+        }
+        pack_value_row<IsHalf>(L, r0, b, h, dst_tok0 + tk, w);
+        pack_value_row<IsHalf>(L, r1, b, h, dst_tok0 + tk + 64, w);
+        return;
+    }
+
     extern __shared__ __align__(16) unsigned char smem[];
-    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                       // [128][130] (Key or Value page)
-    float2* pmm = reinterpret_cast<float2*>(kpage + kFastP * kFastLd);          // [8][128] partial (lo, hi)
-    uint8_t* codes = reinterpret_cast<uint8_t*>(pmm + 8 * D);                   // [128][cw] code bytes
+    const FastLds fl = fast_lds(L);
+    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                  // [128][130]
+    float2* pmm = reinterpret_cast<float2*>(smem + fl.pmm);                // [4][128] partial (lo, hi)
+    uint16_t* f16v = reinterpret_cast<uint16_t*>(smem + fl.f16);           // [128][w16] fp16 tier
+    int16_t* cpos = reinterpret_cast<int16_t*>(smem + fl.cpos);            // [128] code byte of a channel,
+                                                                            // -1 - rank for the fp16 tier
+    uint8_t* codes = smem + fl.codes;                                      // [128][cw] code bytes
     const CodeSegs cs = code_segs(L);
     const int cw = cs.seg[3];
-    int16_t* cpos = reinterpret_cast<int16_t*>(codes + kFastP * cw);            // [128] code byte of a channel, -1
-    int16_t* tidx16 = cpos + D;                                                 // [w16] channels of the fp16 tier
 
-    const bool value_part = blockIdx.z != 0;
     const int w0 = L.k_width[0], w1 = L.k_width[1], w2 = L.k_width[2], w16 = L.k_width[3];
     const int koff1 = w0, koff2 = w0 + w1, nslots = w0 + w1 + w2, wall = nslots + w16;
 
     // ---- stage the page and this head's tier tables (layout.py:49-68): all their global loads
     // go out before the first wait ----
     {
-        const uint16_t* src = static_cast<const uint16_t*>(value_part ? v_src : k_src) + b * sb + h * sh + tok0 * st;
-        uint4 kv[2];
+        const uint16_t* src = static_cast<const uint16_t*>(k_src) + b * sb + h * sh + tok0 * st;
+        uint4 kv[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 4; ++i) {
             const int idx = tid + kFastThreads * i;  // 16-byte chunk: row idx / 16, column 8 (idx % 16)
             kv[i] = *reinterpret_cast<const uint4*>(src + (idx >> 4) * st + 8 * (idx & 15));
         }
+        // slot tid of tier t: its channel and the tier's count for head h (wall <= 512).
+        // Constant indices into the layer descriptor only (a lane-dependent one would copy it to
+        // scratch memory).
         int my_idx = 0, my_cnt = 0;
-        if (!value_part) {
-            // slot tid of tier t: its channel and the tier's count for head h.  Constant indices
-            // into the kernel argument only (a lane-dependent one would copy the argument block
-            // to scratch memory).
-            if (tid < koff1) { my_idx = L.tier_index[0][h * w0 + tid]; my_cnt = L.tier_count[0][h]; }
-            else if (tid < koff2) { my_idx = L.tier_index[1][h * w1 + tid - koff1]; my_cnt = L.tier_count[1][h]; }
-            else if (tid < nslots) { my_idx = L.tier_index[2][h * w2 + tid - koff2]; my_cnt = L.tier_count[2][h]; }
-            else if (tid < wall) { my_idx = L.tier_index[3][h * w16 + tid - nslots]; my_cnt = L.tier_count[3][h]; }
-            if (tid < D) cpos[tid] = -1;
-            for (int i = tid; i < kFastP * cw / 4; i += kFastThreads) reinterpret_cast<uint32_t*>(codes)[i] = 0;
-        }
+        if (tid < koff1) { my_idx = L.tier_index[0][h * w0 + tid]; my_cnt = L.tier_count[0][h]; }
+        else if (tid < koff2) { my_idx = L.tier_index[1][h * w1 + tid - koff1]; my_cnt = L.tier_count[1][h]; }
+        else if (tid < nslots) { my_idx = L.tier_index[2][h * w2 + tid - koff2]; my_cnt = L.tier_count[2][h]; }
+        else if (tid < wall) { my_idx = L.tier_index[3][h * w16 + tid - nslots]; my_cnt = L.tier_count[3][h]; }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 4; ++i) {
             const int idx = tid + kFastThreads * i;
             // rows are 260 bytes apart: 4-byte aligned, so four dword stores
             uint32_t* kd = reinterpret_cast<uint32_t*>(kpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
             kd[0] = kv[i].x; kd[1] = kv[i].y; kd[2] = kv[i].z; kd[3] = kv[i].w;
         }
-        if (value_part) {
-            __syncthreads();
-            pack_value_page<IsHalf>(L, kpage, b, h, dst_tok0, tid);
-            return;
-        }
-        __syncthreads();
+        // channel map: every channel sits in exactly one tier (rank < count), so every entry is
+        // written once; padding slots (rank >= count): scale 1.0, min 0.0, code 0 (layout.py:84-85)
         if (tid < wall) {
             const int t = tid >= nslots ? 3 : tid >= koff2 ? 2 : tid >= koff1 ? 1 : 0;
             const int j = tid - (t == 3 ? nslots : t == 2 ? koff2 : t == 1 ? koff1 : 0);
-            if (t == 3) {
-                tidx16[j] = static_cast<int16_t>(my_idx);
-            } else if (j < my_cnt) {
-                cpos[my_idx] = static_cast<int16_t>(cs.seg[t] + j);
-            } else {
-                // padding slots: scale 1.0, min 0.0, code 0 (layout.py:84-85)
+            if (j < my_cnt) {
+                cpos[my_idx] = static_cast<int16_t>(t == 3 ? -1 - j : (t == 2 ? cs.seg[2] : t == 1 ? cs.seg[1] : 0) + j);
+            } else if (t < 3) {
                 const int width = t == 2 ? w2 : t == 1 ? w1 : w0;
                 const int64_t o = kgrp_idx(L, b, h, width, j, page);
                 uint16_t* ks = t == 2 ? L.k_scale[2] : t == 1 ? L.k_scale[1] : L.k_scale[0];
@@ -488,84 +504,95 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
                 km[o] = 0;
             }
         }
+        __syncthreads();
     }
 
-    // ---- phase 1: Key min/max of channel c over tokens 16 ck .. 16 ck + 15 ----
+    // ---- phase 1: Key min/max of channel c over tokens 32 ck .. 32 ck + 31 ----
     const int c = tid & (D - 1), ck = tid >> 7;
-    float x[16];
+    const int pos = cpos[c];
+    float x[32];
     {
         float lo = __builtin_inff(), hi = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            x[i] = elem_f32<uint16_t, IsHalf>(kpage[(16 * ck + i) * kFastLd + c]);
+        for (int i = 0; i < 32; ++i) {
+            x[i] = elem_f32<uint16_t, IsHalf>(kpage[(32 * ck + i) * kFastLd + c]);
             lo = fminf(lo, x[i]);
             hi = fmaxf(hi, x[i]);
         }
         pmm[ck * D + c] = float2{lo, hi};
-    }
-    __syncthreads();
-
-    // ---- phases 2, 3: the channel's group scale (layout.py:12-18) and its 16 codes ----
-    {
-        const int pos = cpos[c];
-        if (pos >= 0) {
-            float lo = __builtin_inff(), hi = -__builtin_inff();
+        if (pos < 0) {  // fp16 tier (layout.py:101-111): exact for fp16 input, RNE for bf16
+            const int j = -1 - pos;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float2 m = pmm[k * D + c];
-                lo = fminf(lo, m.x);
-                hi = fmaxf(hi, m.y);
-            }
-            const int t = pos >= cs.seg[2] ? 2 : pos >= cs.seg[1] ? 1 : 0;
-            const int qm = t == 2 ? 255 : t == 1 ? 15 : 3;
-            const float sc = group_scale(hi, lo, qm);
-            const float y = 1.0f / sc;
-            if (ck == 0) {
-                const int j = pos - cs.seg[t];
-                const int width = t == 2 ? w2 : t == 1 ? w1 : w0;
-                const int64_t o = kgrp_idx(L, b, h, width, j, page);
-                uint16_t* ks = t == 2 ? L.k_scale[2] : t == 1 ? L.k_scale[1] : L.k_scale[0];
-                uint16_t* km = t == 2 ? L.k_min[2] : t == 1 ? L.k_min[1] : L.k_min[0];
-                ks[o] = f32_to_f16(sc);
-                km[o] = f32_to_f16(lo);
-            }
-            const float qmax = static_cast<float>(qm);
-            uint8_t* crow = codes + (16 * ck) * cw + pos;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) crow[i * cw] = static_cast<uint8_t>(fast_code(x[i], lo, sc, y, qmax));
+            for (int i = 0; i < 32; ++i) f16v[(32 * ck + i) * w16 + j] = f32_to_f16(x[i]);
         }
     }
+    __syncthreads();  // the page is dead: the code rows may overwrite it
+
+    // ---- phases 2, 3: the channel's group scale (layout.py:12-18) and its 32 codes; bytes of
+    // slots no channel writes are masked when the words are assembled ----
+    if (pos >= 0) {
+        float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float2 m = pmm[k * D + c];
+            lo = fminf(lo, m.x);
+            hi = fmaxf(hi, m.y);
+        }
+        const int t = pos >= cs.seg[2] ? 2 : pos >= cs.seg[1] ? 1 : 0;
+        const int qm = t == 2 ? 255 : t == 1 ? 15 : 3;
+        const float sc = group_scale(hi, lo, qm);
+        const float y = 1.0f / sc;
+        if (ck == 0) {
+            const int j = pos - (t == 2 ? cs.seg[2] : t == 1 ? cs.seg[1] : 0);
+            const int width = t == 2 ? w2 : t == 1 ? w1 : w0;
+            const int64_t o = kgrp_idx(L, b, h, width, j, page);
+            uint16_t* ks = t == 2 ? L.k_scale[2] : t == 1 ? L.k_scale[1] : L.k_scale[0];
+            uint16_t* km = t == 2 ? L.k_min[2] : t == 1 ? L.k_min[1] : L.k_min[0];
+            ks[o] = f32_to_f16(sc);
+            km[o] = f32_to_f16(lo);
+        }
+        const float qmax = static_cast<float>(qm);
+        uint8_t* crow = codes + (32 * ck) * cw + pos;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) crow[i * cw] = static_cast<uint8_t>(fast_code(x[i], lo, sc, y, qmax));
+    }
     __syncthreads();
 
-    // ---- phase 4: LSB-first words (layout.py:21-35, :94-97); fp16 tier (layout.py:101-111) ----
+    // ---- phase 4: LSB-first words (layout.py:21-35, :94-97), one loop per tier; fp16 tier ----
     {
-        const int tau = tid >> 3, q = tid & 7;
+        const int tau = tid >> 2, q = tid & 3;
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
-        const int nw = kw0 + kw1 + kw2;
+        const int c0 = w0 ? L.tier_count[0][h] : 0;
+        const int c1 = w1 ? L.tier_count[1][h] : 0;
+        const int c2 = w2 ? L.tier_count[2][h] : 0;
         const int64_t trow = tok_row(L, b, h, dst_tok0 + tau);
         const uint8_t* crow = codes + tau * cw;
-        for (int wi = q; wi < nw; wi += 8) {
-            if (wi < kw0) {
-                const uint4 cb = *reinterpret_cast<const uint4*>(crow + 16 * wi);
-                L.k_code[0][trow * kw0 + wi] = static_cast<int32_t>(word_int2(cb));
-            } else if (wi < kw0 + kw1) {
-                const int w = wi - kw0;
-                const uint2 cb = *reinterpret_cast<const uint2*>(crow + cs.seg[1] + 8 * w);
-                L.k_code[1][trow * kw1 + w] = static_cast<int32_t>(word_int4(cb));
-            } else {
-                const int w = wi - kw0 - kw1;
-                L.k_code[2][trow * kw2 + w] = *reinterpret_cast<const int32_t*>(crow + cs.seg[2] + 4 * w);
-            }
+        for (int w = q; w < kw0; w += 4) {
+            uint4 cb = *reinterpret_cast<const uint4*>(crow + 16 * w);
+            cb.x &= 0x03030303u; cb.y &= 0x03030303u; cb.z &= 0x03030303u; cb.w &= 0x03030303u;
+            const int nv = min(max(c0 - 16 * w, 0), 16);
+            const uint32_t keep = nv >= 16 ? 0xffffffffu : (1u << (2 * nv)) - 1u;
+            L.k_code[0][trow * kw0 + w] = static_cast<int32_t>(word_int2(cb) & keep);
+        }
+        for (int w = (q - kw0) & 3; w < kw1; w += 4) {
+            uint2 cb = *reinterpret_cast<const uint2*>(crow + cs.seg[1] + 8 * w);
+            cb.x &= 0x0f0f0f0fu; cb.y &= 0x0f0f0f0fu;
+            const int nv = min(max(c1 - 8 * w, 0), 8);
+            const uint32_t keep = nv >= 8 ? 0xffffffffu : (1u << (4 * nv)) - 1u;
+            L.k_code[1][trow * kw1 + w] = static_cast<int32_t>(word_int4(cb) & keep);
+        }
+        for (int w = (q - kw0 - kw1) & 3; w < kw2; w += 4) {
+            const uint32_t cb = *reinterpret_cast<const uint32_t*>(crow + cs.seg[2] + 4 * w);
+            const int nv = min(max(c2 - 4 * w, 0), 4);
+            const uint32_t keep = nv >= 4 ? 0xffffffffu : (1u << (8 * nv)) - 1u;
+            L.k_code[2][trow * kw2 + w] = static_cast<int32_t>(cb & keep);
         }
         if (w16 > 0) {
             const int cnt = L.tier_count[3][h];
-            for (int j = q; j < w16; j += 8) {
-                uint16_t v = 0;
-                if (j < cnt) {
-                    const uint16_t raw = kpage[tau * kFastLd + tidx16[j]];
-                    v = IsHalf ? raw : f32_to_f16(bf16_to_f32(raw));
-                }
-                L.k_value16[trow * w16 + j] = v;
+            const int64_t base = tok_row(L, b, h, dst_tok0) * w16;
+            for (int i = tid; i < kFastP * w16; i += kFastThreads) {
+                const int j = i % w16;
+                L.k_value16[base + i] = j < cnt ? f16v[i] : static_cast<uint16_t>(0);
             }
         }
     }
@@ -601,11 +628,7 @@ bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
            L.v_group == 128 && L.bit_v == 2 && L.v_groups == 1 && L.v_words == 8;
 }
 
-size_t pack_fast_lds_bytes(const lf_packed_layer& L) {
-    const int cw = code_segs(L).seg[3];
-    return static_cast<size_t>(kFastP) * kFastLd * 2 + 8 * 128 * 8 + static_cast<size_t>(kFastP) * cw + 128 * 2 +
-           static_cast<size_t>(L.k_width[3]) * 2 + 16;
-}
+size_t pack_fast_lds_bytes(const lf_packed_layer& L) { return static_cast<size_t>(fast_lds(L).total); }
 
 int pack_code_row(const lf_packed_layer& L) {
     const int wsum = L.k_width[0] + L.k_width[1] + L.k_width[2];
