@@ -71,7 +71,7 @@ def test_headline_shape_every_split_meets_the_bar(gpu):
     """The same c2 layer with 8-, 33- (the bench's) and 300-page items (one item per sequence):
     every split pattern meets the bar against the oracle.  A long item is where the Value
     product's offset cancellation (p * (4 + code) against the per-token constant) would build
-    up; the kernel folds it every 32 pages."""
+    up; the kernel folds it every 64 pages."""
     B, n_q, n_kv = 16, 28, 4
     d, mgr = _build(gpu, B, n_q, n_kv, [256] * B, [100] * B, 2.5, seed=12)
     scaling = 128 ** -0.5
