@@ -366,7 +366,7 @@ __device__ __forceinline__ uint32_t word_int4(uint2 b) {
 // (lanes 8k .. 8k + 7 of one wave) by lane exchange.
 template <bool IsHalf>
 __device__ __forceinline__ void pack_value_row(const lf_packed_layer& L, const uint4 (&r)[2], int b, int h,
-                                               int64_t dst_tok, int w) {
+                                               int64_t dst_tok, int w, uint16_t& sc16, uint16_t& lo16) {
     const uint32_t pr[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
     float v[16];
     float lo = __builtin_inff(), hi = -__builtin_inff();
@@ -389,10 +389,8 @@ __device__ __forceinline__ void pack_value_row(const lf_packed_layer& L, const u
     for (int i = 0; i < 16; ++i) word |= fast_code(v[i], lo, sc, y, 3.0f) << (2 * i);
     const int64_t trow = tok_row(L, b, h, dst_tok);
     L.v_code[trow * 8 + w] = static_cast<int32_t>(word);
-    if (w == 0) {
-        L.v_scale[trow] = f32_to_f16(sc);
-        L.v_min[trow] = f32_to_f16(lo);
-    }
+    sc16 = f32_to_f16(sc);
+    lo16 = f32_to_f16(lo);
 }
 
 // LDS layout of the Key workgroup: the staged page (rows padded to 130 halves), partial
@@ -433,6 +431,7 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     const int tid = threadIdx.x;
     const int64_t dst_tok0 = static_cast<int64_t>(page) * kFastP;
     constexpr int D = 128;
+    extern __shared__ __align__(16) unsigned char smem[];
 
     if (blockIdx.z != 0) {
         // ---- Values: both rows' slices in flight before the first use ----
@@ -444,12 +443,27 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
             const uint4* a1 = reinterpret_cast<const uint4*>(src + (tk + 64) * st + 16 * w);
             r0[0] = a0[0]; r0[1] = a0[1]; r1[0] = a1[0]; r1[1] = a1[1];
         }
-        pack_value_row<IsHalf>(L, r0, b, h, dst_tok0 + tk, w);
-        pack_value_row<IsHalf>(L, r1, b, h, dst_tok0 + tk + 64, w);
+        uint16_t s0, m0, s1, m1;
+        pack_value_row<IsHalf>(L, r0, b, h, dst_tok0 + tk, w, s0, m0);
+        pack_value_row<IsHalf>(L, r1, b, h, dst_tok0 + tk + 64, w, s1, m1);
+        // the page's 128 fp16 scales and mins are contiguous: gathered in LDS, each array leaves
+        // as one 256-byte store (token pairs; the row offset is even and the arrays 4-byte
+        // aligned, which the launcher checks)
+        uint16_t* vsm = reinterpret_cast<uint16_t*>(smem);  // [2][128]: scale, min
+        if (w == 0) {
+            vsm[tk] = s0;
+            vsm[tk + 64] = s1;
+            vsm[128 + tk] = m0;
+            vsm[128 + tk + 64] = m1;
+        }
+        __syncthreads();
+        if (tid < 128) {
+            uint16_t* dst = (tid < 64 ? L.v_scale : L.v_min) + tok_row(L, b, h, dst_tok0);
+            reinterpret_cast<uint32_t*>(dst)[tid & 63] = reinterpret_cast<const uint32_t*>(vsm)[tid];
+        }
         return;
     }
 
-    extern __shared__ __align__(16) unsigned char smem[];
     const FastLds fl = fast_lds(L);
     uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                  // [128][130]
     float2* pmm = reinterpret_cast<float2*>(smem + fl.pmm);                // [4][128] partial (lo, hi)
@@ -558,41 +572,61 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     }
     __syncthreads();
 
-    // ---- phase 4: LSB-first words (layout.py:21-35, :94-97), one loop per tier; fp16 tier ----
+    // ---- phase 4: LSB-first words (layout.py:21-35, :94-97), one loop per tier; fp16 tier.
+    // Word i of a tier's page block is (token i / kw, word i % kw): the page's rows are
+    // contiguous, so consecutive threads store consecutive dwords and every store instruction
+    // covers whole lines (a row-per-thread-group order leaves each line part-written by several
+    // instructions).  i / kw = (int)((i + 0.5) * (1 / kw)) in fp32 is exact for i < 128 kw,
+    // kw <= 64 (checked exhaustively) ----
     {
-        const int tau = tid >> 2, q = tid & 3;
         const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
         const int c0 = w0 ? L.tier_count[0][h] : 0;
         const int c1 = w1 ? L.tier_count[1][h] : 0;
         const int c2 = w2 ? L.tier_count[2][h] : 0;
-        const int64_t trow = tok_row(L, b, h, dst_tok0 + tau);
-        const uint8_t* crow = codes + tau * cw;
-        for (int w = q; w < kw0; w += 4) {
-            uint4 cb = *reinterpret_cast<const uint4*>(crow + 16 * w);
-            cb.x &= 0x03030303u; cb.y &= 0x03030303u; cb.z &= 0x03030303u; cb.w &= 0x03030303u;
-            const int nv = min(max(c0 - 16 * w, 0), 16);
-            const uint32_t keep = nv >= 16 ? 0xffffffffu : (1u << (2 * nv)) - 1u;
-            L.k_code[0][trow * kw0 + w] = static_cast<int32_t>(word_int2(cb) & keep);
+        const int64_t row0 = tok_row(L, b, h, dst_tok0);
+        const int n0 = kFastP * kw0, n1 = kFastP * kw1, n2 = kFastP * kw2;
+        {
+            const float rk = 1.0f / static_cast<float>(kw0);
+            int32_t* out = L.k_code[0] + row0 * kw0;
+            for (int i = tid; i < n0; i += kFastThreads) {
+                const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), w = i - tau * kw0;
+                uint4 cb = *reinterpret_cast<const uint4*>(codes + tau * cw + 16 * w);
+                cb.x &= 0x03030303u; cb.y &= 0x03030303u; cb.z &= 0x03030303u; cb.w &= 0x03030303u;
+                const int nv = min(max(c0 - 16 * w, 0), 16);
+                const uint32_t keep = nv >= 16 ? 0xffffffffu : (1u << (2 * nv)) - 1u;
+                out[i] = static_cast<int32_t>(word_int2(cb) & keep);
+            }
         }
-        for (int w = (q - kw0) & 3; w < kw1; w += 4) {
-            uint2 cb = *reinterpret_cast<const uint2*>(crow + cs.seg[1] + 8 * w);
-            cb.x &= 0x0f0f0f0fu; cb.y &= 0x0f0f0f0fu;
-            const int nv = min(max(c1 - 8 * w, 0), 8);
-            const uint32_t keep = nv >= 8 ? 0xffffffffu : (1u << (4 * nv)) - 1u;
-            L.k_code[1][trow * kw1 + w] = static_cast<int32_t>(word_int4(cb) & keep);
+        {
+            const float rk = 1.0f / static_cast<float>(kw1);
+            int32_t* out = L.k_code[1] + row0 * kw1;
+            for (int i = (tid - n0) & (kFastThreads - 1); i < n1; i += kFastThreads) {
+                const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), w = i - tau * kw1;
+                uint2 cb = *reinterpret_cast<const uint2*>(codes + tau * cw + cs.seg[1] + 8 * w);
+                cb.x &= 0x0f0f0f0fu; cb.y &= 0x0f0f0f0fu;
+                const int nv = min(max(c1 - 8 * w, 0), 8);
+                const uint32_t keep = nv >= 8 ? 0xffffffffu : (1u << (4 * nv)) - 1u;
+                out[i] = static_cast<int32_t>(word_int4(cb) & keep);
+            }
         }
-        for (int w = (q - kw0 - kw1) & 3; w < kw2; w += 4) {
-            const uint32_t cb = *reinterpret_cast<const uint32_t*>(crow + cs.seg[2] + 4 * w);
-            const int nv = min(max(c2 - 4 * w, 0), 4);
-            const uint32_t keep = nv >= 4 ? 0xffffffffu : (1u << (8 * nv)) - 1u;
-            L.k_code[2][trow * kw2 + w] = static_cast<int32_t>(cb & keep);
+        {
+            const float rk = 1.0f / static_cast<float>(kw2);
+            int32_t* out = L.k_code[2] + row0 * kw2;
+            for (int i = (tid - n0 - n1) & (kFastThreads - 1); i < n2; i += kFastThreads) {
+                const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), w = i - tau * kw2;
+                const uint32_t cb = *reinterpret_cast<const uint32_t*>(codes + tau * cw + cs.seg[2] + 4 * w);
+                const int nv = min(max(c2 - 4 * w, 0), 4);
+                const uint32_t keep = nv >= 4 ? 0xffffffffu : (1u << (8 * nv)) - 1u;
+                out[i] = static_cast<int32_t>(cb & keep);
+            }
         }
         if (w16 > 0) {
             const int cnt = L.tier_count[3][h];
-            const int64_t base = tok_row(L, b, h, dst_tok0) * w16;
-            for (int i = tid; i < kFastP * w16; i += kFastThreads) {
-                const int j = i % w16;
-                L.k_value16[base + i] = j < cnt ? f16v[i] : static_cast<uint16_t>(0);
+            const float rk = 1.0f / static_cast<float>(w16);
+            uint16_t* out = L.k_value16 + row0 * w16;
+            for (int i = (tid - n0 - n1 - n2) & (kFastThreads - 1); i < kFastP * w16; i += kFastThreads) {
+                const int j = i - w16 * static_cast<int>((static_cast<float>(i) + 0.5f) * rk);
+                out[i] = j < cnt ? f16v[i] : static_cast<uint16_t>(0);
             }
         }
     }
@@ -625,7 +659,8 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_multi_kernel(PackMulti
 
 bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
     return vec16 && src_dtype != LF_FP32 && L.head_dim == 128 && L.page_size == kFastP && L.k_group == kFastP &&
-           L.v_group == 128 && L.bit_v == 2 && L.v_groups == 1 && L.v_words == 8;
+           L.v_group == 128 && L.bit_v == 2 && L.v_groups == 1 && L.v_words == 8 && L.cap_tokens % 2 == 0 &&
+           (reinterpret_cast<uintptr_t>(L.v_scale) & 3) == 0 && (reinterpret_cast<uintptr_t>(L.v_min) & 3) == 0;
 }
 
 size_t pack_fast_lds_bytes(const lf_packed_layer& L) { return static_cast<size_t>(fast_lds(L).total); }
