@@ -18,9 +18,10 @@ Nothing here runs on the CPU: a missing extension or a CPU tensor raises.
 from __future__ import annotations
 
 import ctypes
-import math
+import functools
 import os
 
+import numpy as np
 import torch
 
 from logitfill_amd import _native
@@ -101,17 +102,38 @@ def _cu_count(device) -> int:
 RESIDUAL_PAGES = 5
 
 
+# Fixed cost of one split-K item (query load, page-ring start-up, the partial result's store
+# and its share of the cross-split reduce), in packed pages.
+ITEM_OVERHEAD_PAGES = 3
+
+
+@functools.lru_cache(maxsize=256)
+def _pages_per_split(pages: tuple, n_kv: int, residual_pages: int, slots: int) -> int:
+    p = np.asarray(pages, dtype=np.int64)
+    work = p + residual_pages
+    top = max(1, -(-n_kv * int(work.sum()) // slots))
+    size = np.arange(top, 0, -1, dtype=np.int64)[:, None]             # largest first
+    items = np.where(p[None, :] == 0, 1, -(-work[None, :] // size))   # lf_plan_decode's count
+    rounds = -(-(n_kv * items.sum(axis=1)) // slots)
+    largest = (-(-work[None, :] // items)).max(axis=1)
+    cost = rounds * (largest + ITEM_OVERHEAD_PAGES)
+    return int(size[int(np.argmin(cost)), 0])                          # ties: fewest items
+
+
 def choose_pages_per_split(hist_pages: list[int], n_kv: int, residual_pages: int = RESIDUAL_PAGES,
                            device=None) -> int:
-    """Work per split-K item, in pages.  The decode kernel holds two workgroups per CU; items
-    of ``total work / slots`` pages (each sequence's work being its pages plus its residual)
-    fill those slots once, so the launch runs in a single round."""
+    """Work per split-K item, in pages.  The decode kernel holds two workgroups per CU (the
+    slots).  Items of ``total work / slots`` pages fill the slots once when every sequence's
+    work (its pages plus its residual) divides evenly; with ragged lengths the per-sequence
+    rounding makes more items than slots, and the excess runs as a second round of full-size
+    items.  The size is therefore the one, up to that one-round size, that minimises
+    rounds x (largest item + the per-item cost), with ties going to fewer items; uniform
+    batches keep the one-round size."""
     forced = env_int("LOGITFILL_AMD_PAGES_PER_SPLIT", 0)
     if forced > 0:
         return forced
     slots = 2 * (_cu_count(device) if device is not None else 256)
-    total = n_kv * sum(p + residual_pages for p in hist_pages)
-    return max(1, math.ceil(total / slots))
+    return _pages_per_split(tuple(int(x) for x in hist_pages), int(n_kv), int(residual_pages), slots)
 
 
 class DecodePlan:

@@ -1,0 +1,87 @@
+"""Split-K item size for the decode launch (host logic, no GPU).
+
+The work list comes from the library's own planner (lf_plan_decode, host code); each item
+runs as one workgroup per kv head, two workgroups per CU.  The dispatch is simulated as a
+greedy list schedule (each item to the earliest free slot, in plan order), which is
+independent of the closed-form cost the chooser minimises."""
+import ctypes
+import heapq
+
+import pytest
+
+from logitfill_amd import _native, synth
+from logitfill_amd.packed.reference import ITEM_OVERHEAD_PAGES, RESIDUAL_PAGES, choose_pages_per_split
+
+SLOTS = 512  # 256 CUs x 2 workgroups
+
+
+def plan_items(hist_pages, pps):
+    """(b, page0, page1, flags) rows from lf_plan_decode."""
+    lib = _native.load()
+    B = len(hist_pages)
+    cap = sum(-(-(p + RESIDUAL_PAGES) // pps) for p in hist_pages) + B
+    hp = (ctypes.c_int32 * B)(*hist_pages)
+    work = (ctypes.c_int32 * (4 * cap))()
+    seq = (ctypes.c_int32 * (2 * B))()
+    n = lib.lf_plan_decode(hp, B, pps, RESIDUAL_PAGES, work, cap, seq)
+    assert n > 0
+    return [tuple(work[4 * i:4 * i + 4]) for i in range(n)]
+
+
+def makespan(hist_pages, n_kv, pps):
+    """Greedy list schedule of the plan's workgroups on SLOTS slots, in page units."""
+    slots = [0.0] * SLOTS
+    for b, p0, p1, flags in plan_items(hist_pages, pps):
+        cost = (p1 - p0) + (RESIDUAL_PAGES if flags else 0) + ITEM_OVERHEAD_PAGES
+        for _ in range(n_kv):
+            t = heapq.heappop(slots)
+            heapq.heappush(slots, t + cost)
+    return max(slots)
+
+
+def one_round_size(hist_pages, n_kv):
+    return -(-n_kv * sum(p + RESIDUAL_PAGES for p in hist_pages) // SLOTS)
+
+
+@pytest.mark.parametrize("hist_pages,n_kv,expect", [([256] * 16, 4, 33), ([64] * 8, 2, 3)])
+def test_uniform_batches_keep_one_round(hist_pages, n_kv, expect):
+    """c2 and c1: every sequence's work divides into the one-round size; the plan fills the
+    slots exactly once."""
+    pps = choose_pages_per_split(hist_pages, n_kv)
+    assert pps == expect == one_round_size(hist_pages, n_kv)
+    assert n_kv * len(plan_items(hist_pages, pps)) <= SLOTS
+
+
+def test_ragged_batch_avoids_the_second_round():
+    """c4 (32 sequences of U[4K, 64K] tokens, 8 kv heads): the one-round size leaves more
+    items than slots; the chosen size's simulated makespan is at least 25 % shorter and
+    within 10 % of the work bound."""
+    pages, _ = synth.ragged_lengths(32, seed=4)
+    n_kv = 8
+    top = one_round_size(pages, n_kv)
+    assert n_kv * len(plan_items(pages, top)) > SLOTS
+    pps = choose_pages_per_split(pages, n_kv)
+    assert 1 <= pps < top
+    chosen, naive = makespan(pages, n_kv, pps), makespan(pages, n_kv, top)
+    assert chosen <= 0.75 * naive
+    bound = sum(n_kv * (p + RESIDUAL_PAGES) for p in pages) / SLOTS
+    assert chosen <= 1.10 * (bound + ITEM_OVERHEAD_PAGES) + pps
+
+
+def test_chosen_size_is_best_of_the_scan_by_simulation():
+    """Over several seeded ragged batches the chosen size is within 5 % of the best simulated
+    makespan over every size up to the one-round size."""
+    for seed in (1, 2, 3):
+        pages, _ = synth.ragged_lengths(24, seed=seed)
+        n_kv = 8
+        top = one_round_size(pages, n_kv)
+        best = min(makespan(pages, n_kv, s) for s in range(max(1, top // 4), top + 1))
+        assert makespan(pages, n_kv, choose_pages_per_split(pages, n_kv)) <= 1.05 * best
+
+
+def test_edge_cases(monkeypatch):
+    assert choose_pages_per_split([0], 1) == 1
+    assert choose_pages_per_split([0, 0, 3], 2) >= 1
+    assert choose_pages_per_split([512], 8) == one_round_size([512], 8)
+    monkeypatch.setenv("LOGITFILL_AMD_PAGES_PER_SPLIT", "7")
+    assert choose_pages_per_split([256] * 16, 4) == 7
