@@ -123,8 +123,8 @@ typedef struct lf_pack_source {
  * memory, read by the kernel.  ``jobs`` is a DEVICE int32 array [n_jobs][4] of
  * (layer, b, src_token0, dst_page).  Every layer must have the same n_kv and
  * take the fast shape (head_dim = page_size = k_group = v_group = 128,
- * bit_v 2, 16-byte aligned rows of a 2-byte dtype); otherwise LF_E_UNSUPPORTED
- * and nothing runs.
+ * bit_v 2, 16-byte aligned rows of a 2-byte dtype, even cap_tokens, 4-byte
+ * aligned v_scale / v_min); otherwise LF_E_UNSUPPORTED and nothing runs.
  */
 int32_t lf_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_layer* layers_host,
                             const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int32_t n_layers,
