@@ -10,7 +10,9 @@
  * Conventions
  *  - Plain C: device pointers, sizes and strides only; no torch types.
  *  - The caller owns every buffer, including outputs and workspaces; the
- *    library never allocates device memory and keeps no global state.
+ *    library never allocates device memory and keeps no mutable global state
+ *    (no static variables written after load), so every entry point is
+ *    re-entrant and may be called from several host threads at once.
  *  - ``stream`` is a hipStream_t passed as ``void*`` (NULL = default stream).
  *    Nothing synchronises inside; all work is enqueued on ``stream``.
  *  - Return value: 0 = success; negative = argument/shape error (LF_E_*),
@@ -26,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 5
+#define LF_ABI_VERSION 6
 
 /* Element types of query / residual / output tensors. */
 enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
@@ -50,7 +52,10 @@ enum lf_status {
  *   k_scale[t]  fp16  [batch][n_kv][k_width[t]][cap_kgroups]    (page/group index innermost)
  *   k_min[t]    fp16  [batch][n_kv][k_width[t]][cap_kgroups]
  *   k_value16   fp16  [batch][n_kv][cap_tokens][k_width[3]]     (fp16 tier)
- *   v_code      int32 [batch][n_kv][cap_tokens][v_words]        (bit_v < 16)
+ *   v_code      int32 [batch][n_kv][cap_tokens][v_words]        (bit_v < 16; v_words =
+ *                                                                ceil(head_dim * bit_v / 32),
+ *                                                                the last word zero padded
+ *                                                                as layout.py:27-29 pads)
  *   v_scale     fp16  [batch][n_kv][cap_tokens][v_groups]       (bit_v < 16)
  *   v_min       fp16  [batch][n_kv][cap_tokens][v_groups]       (bit_v < 16)
  *   v_value16   fp16  [batch][n_kv][cap_tokens][head_dim]       (bit_v >= 16)
@@ -152,8 +157,11 @@ typedef struct lf_decode_args {
     const void* k_new;  const void* v_new;    /* [batch][n_kv][head_dim] or both NULL   */
     int32_t new_dtype;
     const void* tail_k; const void* tail_v;   /* [batch][n_kv][tail_cap][head_dim]      */
-    int32_t tail_dtype, tail_cap;
-    const int32_t* tail_len;                  /* device int32 [batch]                   */
+    int32_t tail_dtype, tail_cap;             /* 0 <= tail_cap <= page_size              */
+    const int32_t* tail_len;                  /* device int32 [batch], each in
+                                                 0 .. min(tail_cap, page_size - 1): a full
+                                                 residual page must be packed (flushed)
+                                                 first; larger values are clamped          */
     void* out; int32_t out_dtype;             /* [batch][n_q][head_dim]                 */
     int32_t n_q;
     float scaling;                            /* softmax scale (reference: attn.scaling) */
@@ -188,7 +196,11 @@ int64_t lf_decode_workspace_bytes(int32_t n_q, int32_t head_dim, int32_t n_work)
  * <= 16; the MFMA kernel takes q_len 1 only).  Split-K over packed pages,
  * then a second kernel merges the splits' softmax partials; accumulation in fp32; output
  * rounded to ``out_dtype``.  Requires bit_v == 2 (as the reference kernel,
- * reference.py:62) and n_q % n_kv == 0.
+ * reference.py:62), n_q % n_kv == 0, head_dim a power of two in 8 .. 512, at most
+ * 16 query rows per kv head (n_q / n_kv * q_len) and at most 64 Value groups;
+ * other shapes return LF_E_UNSUPPORTED (the Python layer then runs the dense
+ * dequantise-then-attend path on the device, as the reference falls back to its
+ * dense path, reference.py:105-108).
  */
 int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* args, void* stream);
 
@@ -216,6 +228,32 @@ int32_t lf_dense_decode(const void* query, const void* k, const void* v,
                         int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_t,
                         float scaling, void* out, int32_t tokens_per_split,
                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Layout helpers on the device (building blocks of the page packers, for callers of the
+ * reference's layout module).  All arrays are contiguous device memory.
+ *
+ * lf_asymmetric_codes -- reference src/logitfill/packed/layout.py:12-18.  ``x`` holds
+ * ``n_groups`` groups of ``group`` consecutive elements (dtype LF_BF16 / LF_FP16 /
+ * LF_FP32, upcast to float32 exactly); per group lo = min, hi = max,
+ * s = clamp((hi - lo) / (2^bits - 1), 1e-5, 1e5), code = clamp(rint((x - lo) / s), 0,
+ * 2^bits - 1), all IEEE float32 (the reference's arithmetic on float32 tensors).
+ * Writes codes int32 [n_groups][group], scale and lo float32 [n_groups].  1 <= bits <= 16.
+ *
+ * lf_pack_ints -- layout.py:21-35: LSB-first packing of each row of ``codes`` int32
+ * [rows][n] (non-negative) into words int32 [rows][ceil(n / (32 / bits))]: slot j goes to
+ * word j / per at bit (j % per) * bits, per = 32 / bits, missing slots are zero.
+ *
+ * lf_unpack_ints -- layout.py:38-46: the first ``count`` slots of each row of ``words``
+ * int32 [rows][n_words] as codes int32 [rows][count]; count <= n_words * (32 / bits).
+ *
+ * bits must divide 32 for pack / unpack (1, 2, 4, 8, 16).
+ */
+int32_t lf_asymmetric_codes(const void* x, int32_t dtype, int64_t n_groups, int32_t group, int32_t bits,
+                            int32_t* codes, float* scale, float* lo, void* stream);
+int32_t lf_pack_ints(const int32_t* codes, int64_t rows, int32_t n, int32_t bits, int32_t* words, void* stream);
+int32_t lf_unpack_ints(const int32_t* words, int64_t rows, int32_t n_words, int32_t count, int32_t bits,
+                       int32_t* codes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -104,9 +104,13 @@ _SIGNATURES = {
     "lf_dense_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
                                   c_int64, c_int64, c_int64, c_float, c_void_p, c_int32, c_void_p, c_int64,
                                   c_void_p]),
+    "lf_asymmetric_codes": (c_int32, [c_void_p, c_int32, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                      c_void_p]),
+    "lf_pack_ints": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p]),
+    "lf_unpack_ints": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 _LIB = None
 
 

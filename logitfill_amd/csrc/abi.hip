@@ -1,7 +1,7 @@
 // extern "C" entry points of liblogitfill_amd.so (declared in include/logitfill_amd.h).
 //
 // Validation happens here, before anything is enqueued: a negative LF_E_* code
-// means nothing ran.  The library keeps no state and allocates nothing.
+// means nothing ran.  The library keeps no mutable state and allocates nothing.
 #include "decode_common.hpp"
 
 namespace lf {
@@ -19,6 +19,11 @@ int launch_dense_decode(const void* query, const void* k, const void* v, int bat
                         int head_dim, int tokens, int64_t sb, int64_t sh, int64_t st, float scaling,
                         void* out, int tokens_per_split, void* workspace, hipStream_t stream);
 int64_t dense_workspace_bytes(int batch, int n_kv, int n_q, int head_dim, int tokens, int tokens_per_split);
+int launch_asymmetric_codes(const void* x, int dtype, int64_t n_groups, int group, int bits, int32_t* codes,
+                            float* scale, float* lo, hipStream_t stream);
+int launch_pack_ints(const int32_t* codes, int64_t rows, int n, int bits, int32_t* words, hipStream_t stream);
+int launch_unpack_ints(const int32_t* words, int64_t rows, int n_words, int count, int bits, int32_t* codes,
+                       hipStream_t stream);
 }  // namespace lf
 
 namespace {
@@ -56,7 +61,7 @@ int32_t check_layer(const lf_packed_layer* L, bool need_k = true, bool need_v = 
             if (L->bit_v != 2 && L->bit_v != 4 && L->bit_v != 8) return LF_E_SHAPE;
             if (L->v_group <= 0 || L->head_dim % L->v_group != 0) return LF_E_SHAPE;
             if (L->v_groups != L->head_dim / L->v_group) return LF_E_SHAPE;
-            if ((L->head_dim * L->bit_v) % 32 != 0 || L->v_words != L->head_dim * L->bit_v / 32) return LF_E_SHAPE;
+            if (L->v_words != (L->head_dim * L->bit_v + 31) / 32) return LF_E_SHAPE;  // last word padded
             if (!L->v_code || !L->v_scale || !L->v_min) return LF_E_NULL;
         }
     }
@@ -172,9 +177,10 @@ int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* 
     if (g > 16) return LF_E_UNSUPPORTED;
     if (layer->bit_v != 2) return LF_E_UNSUPPORTED;  // as reference.py:62
     const int D = layer->head_dim;
-    if (D != 64 && D != 128 && D != 256) return LF_E_UNSUPPORTED;
-    if (layer->v_groups > 8) return LF_E_UNSUPPORTED;
-    if (A.tail_cap < 0 || (A.tail_cap > 0 && (!A.tail_k || !A.tail_v))) return LF_E_NULL;
+    if (D < 8 || D > 512 || (D & (D - 1)) != 0) return LF_E_UNSUPPORTED;
+    if (layer->v_groups > 64) return LF_E_UNSUPPORTED;
+    if (A.tail_cap < 0 || A.tail_cap > layer->page_size) return LF_E_SHAPE;
+    if (A.tail_cap > 0 && (!A.tail_k || !A.tail_v)) return LF_E_NULL;
     if (A.n_work <= 0) return LF_E_SHAPE;
     if (A.workspace_bytes < lf_decode_workspace_bytes(static_cast<int32_t>(rows), D, A.n_work))
         return LF_E_WORKSPACE;
@@ -220,7 +226,7 @@ int32_t lf_dense_decode(const void* query, const void* k, const void* v, int32_t
                         int32_t tokens_per_split, void* workspace, int64_t workspace_bytes, void* stream) {
     if (!query || !k || !v || !out || !workspace) return LF_E_NULL;
     if (batch <= 0 || n_kv <= 0 || n_q <= 0 || n_q % n_kv != 0 || tokens <= 0) return LF_E_SHAPE;
-    if (n_q / n_kv > 16) return LF_E_UNSUPPORTED;
+    if (n_q / n_kv > 8) return LF_E_UNSUPPORTED;
     if (head_dim != 128) return LF_E_UNSUPPORTED;
     if (tokens_per_split <= 0 || tokens_per_split % 128 != 0) return LF_E_SHAPE;
     if (workspace_bytes < lf::dense_workspace_bytes(batch, n_kv, n_q, head_dim, tokens, tokens_per_split))
@@ -228,6 +234,36 @@ int32_t lf_dense_decode(const void* query, const void* k, const void* v, int32_t
     return lf::launch_dense_decode(query, k, v, batch, n_q, n_kv, head_dim, tokens, kv_stride_b, kv_stride_h,
                                    kv_stride_t, scaling, out, tokens_per_split, workspace,
                                    static_cast<hipStream_t>(stream));
+}
+
+int32_t lf_asymmetric_codes(const void* x, int32_t dtype, int64_t n_groups, int32_t group, int32_t bits,
+                            int32_t* codes, float* scale, float* lo, void* stream) {
+    if (!valid_dtype(dtype)) return LF_E_DTYPE;
+    if (n_groups < 0 || group <= 0 || bits < 1 || bits > 16) return LF_E_SHAPE;
+    if (n_groups == 0) return LF_OK;
+    if (!x || !codes || !scale || !lo) return LF_E_NULL;
+    if (n_groups > (static_cast<int64_t>(1) << 33)) return LF_E_SHAPE;
+    return lf::launch_asymmetric_codes(x, dtype, n_groups, group, bits, codes, scale, lo,
+                                       static_cast<hipStream_t>(stream));
+}
+
+int32_t lf_pack_ints(const int32_t* codes, int64_t rows, int32_t n, int32_t bits, int32_t* words, void* stream) {
+    if (rows < 0 || n < 0 || bits <= 0 || 32 % bits != 0) return LF_E_SHAPE;
+    if (rows == 0 || n == 0) return LF_OK;
+    if (!codes || !words) return LF_E_NULL;
+    const int per = 32 / bits;
+    if (rows * ((n + per - 1) / per) > (static_cast<int64_t>(1) << 40)) return LF_E_SHAPE;
+    return lf::launch_pack_ints(codes, rows, n, bits, words, static_cast<hipStream_t>(stream));
+}
+
+int32_t lf_unpack_ints(const int32_t* words, int64_t rows, int32_t n_words, int32_t count, int32_t bits,
+                       int32_t* codes, void* stream) {
+    if (rows < 0 || n_words < 0 || count < 0 || bits <= 0 || 32 % bits != 0) return LF_E_SHAPE;
+    if (static_cast<int64_t>(count) > static_cast<int64_t>(n_words) * (32 / bits)) return LF_E_SHAPE;
+    if (rows == 0 || count == 0) return LF_OK;
+    if (!words || !codes) return LF_E_NULL;
+    if (rows * count > (static_cast<int64_t>(1) << 40)) return LF_E_SHAPE;
+    return lf::launch_unpack_ints(words, rows, n_words, count, bits, codes, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

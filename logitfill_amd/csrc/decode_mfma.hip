@@ -1267,14 +1267,8 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
         return LF_OK;
     }
     *handled = true;
-    // Raise the dynamic-LDS limit to what this launch needs.
-    static int lds_limit = 64 * 1024;
-    if (mp.y.lds_bytes > lds_limit) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, mp.y.lds_bytes);
-        if (e != hipSuccess) return static_cast<int>(e);
-        lds_limit = mp.y.lds_bytes;
-    }
+    const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&decode_mfma_kernel), mp.y.lds_bytes);
+    if (rc != LF_OK) return rc;
     hipLaunchKernelGGL(decode_mfma_kernel, dim3(p.A.n_work, p.L.n_kv), dim3(kThreads), mp.y.lds_bytes, stream, mp);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);

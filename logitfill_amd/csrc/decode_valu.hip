@@ -11,8 +11,8 @@
 // channels for the value accumulation.  The Key scale is folded into the
 // query once per Key group:
 //     score_i = sum_c q_ic (code_c s_c + m_c) = sum_slot (q s)_slot code_slot + sum_c q_ic m_c
-// This kernel is the general path (any g <= 16, D in {64,128,256}); the MFMA
-// kernel covers the fast shapes.
+// This kernel is the general path (any g <= 16, head_dim a power of two in 8..512, up to 64
+// Value groups, Value rows of ceil(D / 16) words); the MFMA kernel covers the fast shapes.
 #include "decode_common.hpp"
 
 namespace lf {
@@ -20,14 +20,29 @@ namespace {
 
 constexpr int kMaxG = 16;
 
-template <int D>
-struct ValuSmem {
-    float qT[D][kMaxG];          // q * scaling * log2(e), channel-major
-    float p[64][kMaxG];          // probabilities of the current chunk
-    float vsc[64][8];            // V scale per token and channel group
-    float vmn[64][8];            // V min
-    uint32_t vcode[64][D / 16];  // V codes of the chunk
+// Dynamic LDS of one workgroup (floats unless noted), in this order:
+//   qT    [D][kMaxG]        q * scaling * log2(e), channel-major
+//   p     [64][kMaxG]       probabilities of the current chunk
+//   vsc   [64][v_groups]    Value scale per token and channel group
+//   vmn   [64][v_groups]    Value min
+//   vcode [64][v_words]     Value code words of the chunk (uint32)
+//   qp    [n_slots][kMaxG]  q * Key scale per tier slot of the current Key group
+struct ValuLds {
+    int qT, p, vsc, vmn, vcode, qp, total;
 };
+
+__host__ __device__ inline ValuLds valu_lds(int D, int v_groups, int v_words, int n_slots) {
+    ValuLds o;
+    int off = 0;
+    o.qT = off;    off += D * kMaxG * 4;
+    o.p = off;     off += 64 * kMaxG * 4;
+    o.vsc = off;   off += 64 * v_groups * 4;
+    o.vmn = off;   off += 64 * v_groups * 4;
+    o.vcode = off; off += 64 * v_words * 4;
+    o.qp = off;    off += n_slots * kMaxG * 4;
+    o.total = off;
+    return o;
+}
 
 __device__ __forceinline__ int slot_tier(const int* off, int slot) {
     return slot < off[1] ? 0 : slot < off[2] ? 1 : slot < off[3] ? 2 : 3;
@@ -45,27 +60,34 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
     const int b = w4[0];
     const int pbeg = w4[1], pend = w4[2], kind = w4[3];
 
-    __shared__ ValuSmem<D> sm;
-    extern __shared__ float qp[];  // [n_slots][kMaxG]  (dynamic)
-
-    // q, pre-scaled into the log2 domain.
-    for (int idx = lane; idx < kMaxG * D; idx += 64) {
-        const int i = idx / D, c = idx % D;
-        float v = 0.f;
-        if (i < g) v = load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + i) * D + c, A.q_dtype);
-        sm.qT[c][i] = v * p.qscale;
-    }
-    __syncthreads();
-
     int off[4];
     off[0] = 0;
     off[1] = L.k_width[0];
     off[2] = off[1] + L.k_width[1];
     off[3] = off[2] + L.k_width[2];
     const int n_slots = off[3] + L.k_width[3];
+    const int vgs = L.v_groups;
+    const int vws = L.v_words;
+    const ValuLds lay = valu_lds(D, vgs, vws, n_slots);
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* qT = reinterpret_cast<float*>(smem + lay.qT);        // [D][kMaxG]
+    float* pb = reinterpret_cast<float*>(smem + lay.p);         // [64][kMaxG]
+    float* vsc = reinterpret_cast<float*>(smem + lay.vsc);      // [64][vgs]
+    float* vmn = reinterpret_cast<float*>(smem + lay.vmn);      // [64][vgs]
+    uint32_t* vcode = reinterpret_cast<uint32_t*>(smem + lay.vcode);  // [64][vws]
+    float* qp = reinterpret_cast<float*>(smem + lay.qp);        // [n_slots][kMaxG]
+
+    // q, pre-scaled into the log2 domain.
+    for (int idx = lane; idx < kMaxG * D; idx += 64) {
+        const int i = idx / D, c = idx % D;
+        float v = 0.f;
+        if (i < g) v = load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + i) * D + c, A.q_dtype);
+        qT[c * kMaxG + i] = v * p.qscale;
+    }
+    __syncthreads();
 
     float m[kMaxG], lsum[kMaxG];
-    constexpr int CPL = D / 64;  // channels per lane
+    constexpr int CPL = D >= 64 ? D / 64 : 1;  // channels per lane (lanes >= D idle when D < 64)
     float o[CPL][kMaxG];
 #pragma unroll
     for (int i = 0; i < kMaxG; ++i) {
@@ -82,11 +104,11 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
             if (i < g) {
                 const float s = active ? score[i] : -__builtin_inff();
                 const float mnew = fmaxf(m[i], wave_max(s));
-                alpha[i] = __builtin_amdgcn_exp2f(m[i] - mnew);
+                alpha[i] = mnew == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m[i] - mnew);
                 const float pi = active ? __builtin_amdgcn_exp2f(s - mnew) : 0.f;
                 lsum[i] = lsum[i] * alpha[i] + pi;
                 m[i] = mnew;
-                sm.p[lane][i] = pi;
+                pb[lane * kMaxG + i] = pi;
             }
         }
     };
@@ -94,111 +116,109 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
     if (kind != 1) {  // pages (kind 0, 2)
         const int kg = L.k_group;
         const int chunk = kg < 64 ? kg : 64;
-        const int vgs = L.v_groups;
         const int64_t tok_end = static_cast<int64_t>(pend) * L.page_size;
         for (int64_t tok = static_cast<int64_t>(pbeg) * L.page_size; tok < tok_end; tok += kg) {
             const int64_t kgi = tok / kg;
-            {
-                // Fold this Key group's scale into q; collect sum_c q_c m_c.
-                float bias[kMaxG];
+            // Fold this Key group's scale into q; collect sum_c q_c m_c.
+            float bias[kMaxG];
 #pragma unroll
-                for (int i = 0; i < kMaxG; ++i) bias[i] = 0.f;
-                __syncthreads();
-                for (int slot = lane; slot < n_slots; slot += 64) {
-                    const int t = slot_tier(off, slot);
-                    const int j = slot - off[t];
-                    const int cnt = L.tier_count[t][h];
-                    float* row = qp + slot * kMaxG;
-                    if (j >= cnt) {
+            for (int i = 0; i < kMaxG; ++i) bias[i] = 0.f;
+            __syncthreads();
+            for (int slot = lane; slot < n_slots; slot += 64) {
+                const int t = slot_tier(off, slot);
+                const int j = slot - off[t];
+                const int cnt = L.tier_count[t][h];
+                float* row = qp + slot * kMaxG;
+                if (j >= cnt) {
 #pragma unroll
-                        for (int i = 0; i < kMaxG; ++i) row[i] = 0.f;
-                        continue;
-                    }
-                    const int c = L.tier_index[t][h * L.k_width[t] + j];
-                    if (t == 3) {
+                    for (int i = 0; i < kMaxG; ++i) row[i] = 0.f;
+                    continue;
+                }
+                const int c = L.tier_index[t][h * L.k_width[t] + j];
+                if (t == 3) {
 #pragma unroll
-                        for (int i = 0; i < kMaxG; ++i) row[i] = sm.qT[c][i];
-                    } else {
-                        const int64_t gi = kgrp_idx(L, b, h, L.k_width[t], j, kgi);
-                        const float s = f16_to_f32(L.k_scale[t][gi]);
-                        const float mn = f16_to_f32(L.k_min[t][gi]);
+                    for (int i = 0; i < kMaxG; ++i) row[i] = qT[c * kMaxG + i];
+                } else {
+                    const int64_t gi = kgrp_idx(L, b, h, L.k_width[t], j, kgi);
+                    const float s = f16_to_f32(L.k_scale[t][gi]);
+                    const float mn = f16_to_f32(L.k_min[t][gi]);
 #pragma unroll
-                        for (int i = 0; i < kMaxG; ++i) {
-                            row[i] = sm.qT[c][i] * s;
-                            bias[i] += sm.qT[c][i] * mn;
-                        }
+                    for (int i = 0; i < kMaxG; ++i) {
+                        row[i] = qT[c * kMaxG + i] * s;
+                        bias[i] += qT[c * kMaxG + i] * mn;
                     }
                 }
+            }
 #pragma unroll
-                for (int i = 0; i < kMaxG; ++i) bias[i] = wave_sum(bias[i]);
-                __syncthreads();
-                // Process the group's chunks.
-                for (int64_t t0 = tok; t0 < tok + kg; t0 += chunk) {
-                    const bool active = lane < chunk;
-                    const int64_t row = tok_row(L, b, h, t0 + (active ? lane : 0));
-                    float score[kMaxG];
+            for (int i = 0; i < kMaxG; ++i) bias[i] = wave_sum(bias[i]);
+            __syncthreads();
+            // Process the group's chunks.
+            for (int64_t t0 = tok; t0 < tok + kg; t0 += chunk) {
+                const bool active = lane < chunk;
+                const int64_t row = tok_row(L, b, h, t0 + (active ? lane : 0));
+                float score[kMaxG];
 #pragma unroll
-                    for (int i = 0; i < kMaxG; ++i) score[i] = bias[i];
-                    for (int t = 0; t < 3; ++t) {
-                        const int words = L.k_words[t];
-                        const int bits = 2 << t;
-                        const int per = 32 / bits;
-                        const uint32_t mask = (1u << bits) - 1u;
-                        const int width = L.k_width[t];
-                        for (int w = 0; w < words; ++w) {
-                            const uint32_t word = static_cast<uint32_t>(L.k_code[t][row * words + w]);
-                            const int kmax = min(per, width - w * per);
-                            for (int k = 0; k < kmax; ++k) {
-                                const float cf = static_cast<float>((word >> (k * bits)) & mask);
-                                const float* qrow = qp + (off[t] + w * per + k) * kMaxG;
-#pragma unroll
-                                for (int i = 0; i < kMaxG; ++i)
-                                    if (i < g) score[i] = fmaf(qrow[i], cf, score[i]);
-                            }
-                        }
-                    }
-                    for (int j = 0; j < L.k_width[3]; ++j) {
-                        const float v = f16_to_f32(L.k_value16[row * L.k_width[3] + j]);
-                        const float* qrow = qp + (off[3] + j) * kMaxG;
-#pragma unroll
-                        for (int i = 0; i < kMaxG; ++i)
-                            if (i < g) score[i] = fmaf(qrow[i], v, score[i]);
-                    }
-                    float alpha[kMaxG];
-                    softmax_step(score, active, alpha);
-                    if (active) {
-                        for (int vg = 0; vg < vgs; ++vg) {
-                            sm.vsc[lane][vg] = f16_to_f32(L.v_scale[row * vgs + vg]);
-                            sm.vmn[lane][vg] = f16_to_f32(L.v_min[row * vgs + vg]);
-                        }
-                        for (int w = 0; w < D / 16; ++w)
-                            sm.vcode[lane][w] = static_cast<uint32_t>(L.v_code[row * L.v_words + w]);
-                    }
-                    __syncthreads();
-#pragma unroll
-                    for (int cc = 0; cc < CPL; ++cc) {
-                        const int c = lane + 64 * cc;
-                        const int vg = c / L.v_group;
-#pragma unroll
-                        for (int i = 0; i < kMaxG; ++i) o[cc][i] *= alpha[i];
-                        for (int tt = 0; tt < chunk; ++tt) {
-                            const uint32_t code = (sm.vcode[tt][c >> 4] >> (2 * (c & 15))) & 3u;
-                            const float v = static_cast<float>(code) * sm.vsc[tt][vg] + sm.vmn[tt][vg];
+                for (int i = 0; i < kMaxG; ++i) score[i] = bias[i];
+                for (int t = 0; t < 3; ++t) {
+                    const int words = L.k_words[t];
+                    const int bits = 2 << t;
+                    const int per = 32 / bits;
+                    const uint32_t mask = (1u << bits) - 1u;
+                    const int width = L.k_width[t];
+                    for (int w = 0; w < words; ++w) {
+                        const uint32_t word = static_cast<uint32_t>(L.k_code[t][row * words + w]);
+                        const int kmax = min(per, width - w * per);
+                        for (int k = 0; k < kmax; ++k) {
+                            const float cf = static_cast<float>((word >> (k * bits)) & mask);
+                            const float* qrow = qp + (off[t] + w * per + k) * kMaxG;
 #pragma unroll
                             for (int i = 0; i < kMaxG; ++i)
-                                if (i < g) o[cc][i] = fmaf(sm.p[tt][i], v, o[cc][i]);
+                                if (i < g) score[i] = fmaf(qrow[i], cf, score[i]);
                         }
                     }
-                    __syncthreads();
                 }
+                for (int j = 0; j < L.k_width[3]; ++j) {
+                    const float v = f16_to_f32(L.k_value16[row * L.k_width[3] + j]);
+                    const float* qrow = qp + (off[3] + j) * kMaxG;
+#pragma unroll
+                    for (int i = 0; i < kMaxG; ++i)
+                        if (i < g) score[i] = fmaf(qrow[i], v, score[i]);
+                }
+                float alpha[kMaxG];
+                softmax_step(score, active, alpha);
+                if (active) {
+                    for (int vg = 0; vg < vgs; ++vg) {
+                        vsc[lane * vgs + vg] = f16_to_f32(L.v_scale[row * vgs + vg]);
+                        vmn[lane * vgs + vg] = f16_to_f32(L.v_min[row * vgs + vg]);
+                    }
+                    for (int w = 0; w < vws; ++w) vcode[lane * vws + w] = static_cast<uint32_t>(L.v_code[row * vws + w]);
+                }
+                __syncthreads();
+#pragma unroll
+                for (int cc = 0; cc < CPL; ++cc) {
+                    const int c = lane + 64 * cc;
+                    const int vg = (c < D ? c : 0) / L.v_group;
+#pragma unroll
+                    for (int i = 0; i < kMaxG; ++i) o[cc][i] *= alpha[i];
+                    if (c >= D) continue;
+                    for (int tt = 0; tt < chunk; ++tt) {
+                        const uint32_t code = (vcode[tt * vws + (c >> 4)] >> (2 * (c & 15))) & 3u;
+                        const float v = static_cast<float>(code) * vsc[tt * vgs + vg] + vmn[tt * vgs + vg];
+#pragma unroll
+                        for (int i = 0; i < kMaxG; ++i)
+                            if (i < g) o[cc][i] = fmaf(pb[tt * kMaxG + i], v, o[cc][i]);
+                    }
+                }
+                __syncthreads();
             }
         }
     }
     if (kind != 0) {
         // Residual (kind 1, 2): the BF16 tail page then the new token(s) (reference.py:35-44).
         // With q_len new tokens, row i (token i % q_len) sees new tokens 0 .. i % q_len
-        // (reference.py:18-27,48: the causal mask is right-aligned).
-        const int tl = A.tail_len[b];
+        // (reference.py:18-27,48: the causal mask is right-aligned).  tail_len is clamped to
+        // the residual buffer.
+        const int tl = min(max(A.tail_len[b], 0), A.tail_cap);
         const int q_len = p.q_len;
         const int n_new = A.k_new != nullptr ? q_len : 0;
         const int n_res = tl + n_new;
@@ -226,7 +246,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
                     const float k = load_as_f32(kp, kbase + c, kdt);
 #pragma unroll
                     for (int i = 0; i < kMaxG; ++i)
-                        if (i < g) score[i] = fmaf(sm.qT[c][i], k, score[i]);
+                        if (i < g) score[i] = fmaf(qT[c * kMaxG + i], k, score[i]);
                 }
                 if (tt_lane >= tl && q_len > 1) {
 #pragma unroll
@@ -243,6 +263,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
                 const int c = lane + 64 * cc;
 #pragma unroll
                 for (int i = 0; i < kMaxG; ++i) o[cc][i] *= alpha[i];
+                if (c >= D) continue;
                 for (int tt = 0; tt < cnt; ++tt) {
                     const int tok = t0 + tt;
                     float v;
@@ -253,7 +274,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
                         v = load_as_f32(A.v_new, (new_row0 + tok - tl) * D + c, A.new_dtype);
 #pragma unroll
                     for (int i = 0; i < kMaxG; ++i)
-                        if (i < g) o[cc][i] = fmaf(sm.p[tt][i], v, o[cc][i]);
+                        if (i < g) o[cc][i] = fmaf(pb[tt * kMaxG + i], v, o[cc][i]);
                 }
             }
             __syncthreads();
@@ -264,7 +285,8 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
     for (int i = 0; i < g; ++i) {
         float* r = part_rec(p, item, h, i);
 #pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) r[lane + 64 * cc] = o[cc][i];
+        for (int cc = 0; cc < CPL; ++cc)
+            if (lane + 64 * cc < D) r[lane + 64 * cc] = o[cc][i];
         const float lt = wave_sum(lsum[i]);
         if (lane == 0) {
             r[D] = m[i];
@@ -273,17 +295,34 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
     }
 }
 
+template <int D>
+int launch_valu_d(const DecodeParams& p, size_t lds, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&decode_valu_kernel<D>);
+    const int rc = allow_dynamic_lds(fn, lds);
+    if (rc != LF_OK) return rc;
+    hipLaunchKernelGGL(decode_valu_kernel<D>, dim3(p.A.n_work, p.L.n_kv), dim3(64), lds, stream, p);
+    return LF_OK;
+}
+
 }  // namespace
 
 int launch_decode_valu(const DecodeParams& p, hipStream_t stream) {
     const int D = p.L.head_dim;
     const int n_slots = p.L.k_width[0] + p.L.k_width[1] + p.L.k_width[2] + p.L.k_width[3];
-    const size_t dyn = static_cast<size_t>(n_slots) * kMaxG * sizeof(float);
-    dim3 grid(p.A.n_work, p.L.n_kv), block(64);
-    if (D == 64) hipLaunchKernelGGL(decode_valu_kernel<64>, grid, block, dyn, stream, p);
-    else if (D == 128) hipLaunchKernelGGL(decode_valu_kernel<128>, grid, block, dyn, stream, p);
-    else if (D == 256) hipLaunchKernelGGL(decode_valu_kernel<256>, grid, block, dyn, stream, p);
-    else return LF_E_SHAPE;
+    const size_t lds = static_cast<size_t>(valu_lds(D, p.L.v_groups, p.L.v_words, n_slots).total);
+    if (lds > 160 * 1024) return LF_E_UNSUPPORTED;
+    int rc;
+    switch (D) {
+        case 8: rc = launch_valu_d<8>(p, lds, stream); break;
+        case 16: rc = launch_valu_d<16>(p, lds, stream); break;
+        case 32: rc = launch_valu_d<32>(p, lds, stream); break;
+        case 64: rc = launch_valu_d<64>(p, lds, stream); break;
+        case 128: rc = launch_valu_d<128>(p, lds, stream); break;
+        case 256: rc = launch_valu_d<256>(p, lds, stream); break;
+        case 512: rc = launch_valu_d<512>(p, lds, stream); break;
+        default: return LF_E_UNSUPPORTED;
+    }
+    if (rc != LF_OK) return rc;
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);
     return launch_decode_reduce(p, stream);

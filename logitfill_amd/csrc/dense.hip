@@ -314,13 +314,8 @@ int launch_dense_decode(const void* query, const void* k, const void* v, int bat
     p.n_splits = (tokens + tps - 1) / tps;
     p.qscale = scaling * 1.4426950408889634f;
     p.part = static_cast<float*>(workspace);
-    static bool lds_raised = false;
-    if (!lds_raised) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dense_decode_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-        if (e != hipSuccess) return static_cast<int>(e);
-        lds_raised = true;
-    }
+    const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&dense_decode_kernel), kLds);
+    if (rc != LF_OK) return rc;
     hipLaunchKernelGGL(dense_decode_kernel, dim3(p.n_splits, batch * n_kv), dim3(kThreads), kLds, stream, p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);

@@ -52,6 +52,17 @@ __device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float
     else static_cast<float*>(p)[i] = v;
 }
 
+// ---- launch helpers -------------------------------------------------------
+
+// Allow ``bytes`` of dynamic LDS for kernel ``fn`` on the current device; launches above
+// 64 KB need the attribute.  Called before every such launch (a host-side call on the
+// function's per-device state), so the library itself caches nothing.
+inline int allow_dynamic_lds(const void* fn, size_t bytes) {
+    if (bytes <= 64 * 1024) return LF_OK;
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    return e == hipSuccess ? LF_OK : static_cast<int>(e);
+}
+
 // ---- wave reductions ----------------------------------------------------
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -679,13 +679,8 @@ size_t pack_lds_bytes(const lf_packed_layer& L, int elem) {
 
 template <typename T, bool IsHalf>
 int launch_one(const PackJobArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-    static size_t lds_limit = 64 * 1024;
-    if (lds > lds_limit) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&pack_pages_kernel<T, IsHalf>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (e != hipSuccess) return static_cast<int>(e);
-        lds_limit = lds;
-    }
+    const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&pack_pages_kernel<T, IsHalf>), lds);
+    if (rc != LF_OK) return rc;
     hipLaunchKernelGGL((pack_pages_kernel<T, IsHalf>), grid, dim3(kPackThreads), lds, stream, a);
     return LF_OK;
 }
@@ -712,16 +707,11 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
     if (pack_fast_ok(L, src_dtype, a.vec16 != 0)) {
         const size_t lds = pack_fast_lds_bytes(L);
         if (lds <= 160 * 1024) {
-            static size_t fast_limit[2] = {64 * 1024, 64 * 1024};
             const int half = src_dtype == LF_FP16;
             const void* fn = half ? reinterpret_cast<const void*>(&pack_fast_kernel<true>)
                                   : reinterpret_cast<const void*>(&pack_fast_kernel<false>);
-            if (lds > fast_limit[half]) {
-                const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                         static_cast<int>(lds));
-                if (e != hipSuccess) return static_cast<int>(e);
-                fast_limit[half] = lds;
-            }
+            const int rc = allow_dynamic_lds(fn, lds);
+            if (rc != LF_OK) return rc;
             const dim3 grid2(n_jobs, L.n_kv, 2);  // z: Key page, Value page
             if (half) hipLaunchKernelGGL(pack_fast_kernel<true>, grid2, dim3(kFastThreads), lds, stream, a);
             else hipLaunchKernelGGL(pack_fast_kernel<false>, grid2, dim3(kFastThreads), lds, stream, a);
@@ -749,7 +739,7 @@ int launch_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_l
     for (int i = 0; i < n_layers; ++i) {
         const lf_packed_layer& L = layers_host[i];
         const lf_pack_source& S = srcs_host[i];
-        if (L.n_kv != layers_host[0].n_kv) return LF_E_SHAPE;
+        if (L.n_kv != layers_host[0].n_kv) return LF_E_UNSUPPORTED;  // one grid shape for all layers
         const uintptr_t kp = reinterpret_cast<uintptr_t>(S.k), vp = reinterpret_cast<uintptr_t>(S.v);
         const bool vec16 = ((kp | vp) % 16 == 0) && ((S.stride_b * 2) % 16 == 0) && ((S.stride_h * 2) % 16 == 0) &&
                            ((S.stride_t * 2) % 16 == 0);
@@ -758,15 +748,11 @@ int launch_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_l
         lds = l > lds ? l : lds;
     }
     if (lds > 160 * 1024) return LF_E_SHAPE;
-    static size_t limit[2] = {64 * 1024, 64 * 1024};
     const int half = src_dtype == LF_FP16;
     const void* fn = half ? reinterpret_cast<const void*>(&pack_fast_multi_kernel<true>)
                           : reinterpret_cast<const void*>(&pack_fast_multi_kernel<false>);
-    if (lds > limit[half]) {
-        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (e != hipSuccess) return static_cast<int>(e);
-        limit[half] = lds;
-    }
+    const int rc = allow_dynamic_lds(fn, lds);
+    if (rc != LF_OK) return rc;
     PackMultiArgs m{layers_dev, srcs_dev, jobs};
     const dim3 grid(n_jobs, layers_host[0].n_kv, 2);  // z: Key page, Value page
     if (half) hipLaunchKernelGGL(pack_fast_multi_kernel<true>, grid, dim3(kFastThreads), lds, stream, m);

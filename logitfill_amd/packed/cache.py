@@ -31,6 +31,7 @@ from logitfill_amd.packed.layout import (
     make_layer_struct,
     tier_tables,
     tier_widths,
+    value_words,
 )
 
 
@@ -167,7 +168,7 @@ class _LayerStore:
             s["v_value16"] = torch.zeros(B, H, cap, D, dtype=torch.float16, device=dev)
         else:
             vg = D // self.v_group_size
-            s["v_code"] = torch.zeros(B, H, cap, D * self.bit_v // 32, dtype=torch.int32, device=dev)
+            s["v_code"] = torch.zeros(B, H, cap, value_words(D, self.bit_v), dtype=torch.int32, device=dev)
             s["v_scale"] = torch.zeros(B, H, cap, vg, dtype=torch.float16, device=dev)
             s["v_min"] = torch.zeros(B, H, cap, vg, dtype=torch.float16, device=dev)
         if old is not None and old_cap:
@@ -521,46 +522,80 @@ class PackedKVManager:
 
 
 try:
-    from transformers.cache_utils import Cache as _TransformersCache
-except ImportError:  # pragma: no cover - exercised only when transformers is absent
-    _TransformersCache = object
+    from transformers.cache_utils import Cache as _HFCache
+except ImportError:  # pragma: no cover - transformers is optional for the cache itself
+    _HFCache = object
 
 
-class LogitFillCache(_TransformersCache):
-    """Cache handle so ``generate`` can read the packed sequence length (reference ``cache.py:149-183``)."""
+def _init_hf_base(obj) -> None:
+    """Run the transformers ``Cache`` constructor with no cache layers.  transformers 5.x
+    requires ``layers`` (or a layer class); 4.x takes no arguments; without transformers the
+    base is ``object``."""
+    if _HFCache is object:
+        return
+    import inspect
+
+    params = inspect.signature(_HFCache.__init__).parameters
+    if "layers" in params:
+        _HFCache.__init__(obj, layers=[])
+    else:
+        _HFCache.__init__(obj)
+
+
+class LogitFillCache(_HFCache):
+    """transformers ``Cache`` view of a ``PackedKVManager`` (reference ``cache.py:149-183``).
+
+    Passed as ``past_key_values`` so that a model's forward and ``generate`` derive positions
+    and mask sizes from the packed sequence length.  It holds no tensors: the packed attention
+    forward reads and commits the manager itself, so ``update`` is an error, and beam search
+    (``reorder_cache``) is not supported.  Works with transformers 4.x (``get_mask_sizes``
+    receives the cache positions) and 5.x (it receives the query length).
+    """
 
     def __init__(self, manager: PackedKVManager):
-        try:
-            super().__init__()
-        except TypeError:
-            pass
+        _init_hf_base(self)
         self.manager = manager
-        self.key_cache = []
-        self.value_cache = []
 
+    # -- lengths ------------------------------------------------------------------------------
     def get_seq_length(self, layer_idx: int = 0) -> int:
-        del layer_idx
         return int(self.manager.seq_len)
+
+    def get_query_offset(self, layer_idx: int = 0) -> int:
+        return int(self.manager.seq_len)
+
+    def get_mask_sizes(self, query, layer_idx: int = 0):
+        """``(kv_length, kv_offset)``: the packed tokens plus the ``query`` tokens (an int, or
+        the tensor of cache positions older transformers pass), offset 0."""
+        q_len = int(query) if isinstance(query, int) else int(query.shape[0])
+        return int(self.manager.seq_len) + q_len, 0
+
+    def get_max_length(self, layer_idx: int | None = None) -> int:
+        return -1  # grows without a bound
 
     def get_max_cache_shape(self, layer_idx: int = 0):
         return None
 
-    def get_mask_sizes(self, cache_position, layer_idx: int = 0):
-        del layer_idx
-        query_length = int(cache_position.shape[0])
-        return self.manager.seq_len + query_length, 0
+    @property
+    def is_compileable(self) -> bool:
+        return False
 
-    def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
-        raise RuntimeError("packed attention writes the LogitFill manager directly")
+    # -- writes ---------------------------------------------------------------------------------
+    def update(self, key_states, value_states, layer_idx, *args, **kwargs):
+        raise RuntimeError("the packed attention forward commits to the PackedKVManager itself; "
+                           "LogitFillCache.update must not be reached")
+
+    def note_layer(self, layer_idx: int, seq_len: int) -> None:
+        """Called by the attention forward after each layer's commit; the length lives in the
+        manager, so there is nothing to record."""
 
     def reset(self) -> None:
         self.manager.reset()
 
-    def note_layer(self, layer_idx: int, seq_len: int) -> None:
-        del layer_idx, seq_len
+    def crop(self, tokens_to_remove: int) -> None:
+        raise NotImplementedError("packed pages cannot be cropped")
 
-    def reorder_cache(self, beam_idx: torch.Tensor) -> None:
-        raise NotImplementedError("packed LogitFill cache does not support beam search")
+    def reorder_cache(self, beam_idx) -> None:
+        raise NotImplementedError("beam search is not supported by the packed cache")
 
 
 def env_int(name: str, default: int) -> int:

@@ -3,6 +3,8 @@
 Same names, arguments and return structures as the reference's
 ``logitfill.packed.layout`` (``src/logitfill/packed/layout.py``):
 
+* ``asymmetric_codes``, ``pack_ints``, ``unpack_ints`` -- the element-wise
+  helpers (``layout.py:12-46``), as HIP kernels;
 * ``tier_tables(levels)`` -- host integer work on the tiny ``[heads, dim]``
   level map (``layout.py:49-68``);
 * ``quantize_key_page`` / ``quantize_value_page`` -- run the HIP page-compress
@@ -56,11 +58,76 @@ def tier_tables(levels: torch.Tensor) -> dict:
     return {"tiers": tables, "tier": levels.to(torch.int32)}
 
 
+def value_words(dim: int, bits: int) -> int:
+    """int32 words of one token's packed Value row: ``ceil(dim * bits / 32)``, the last word zero
+    padded (``layout.py:27-29``)."""
+    per = 32 // int(bits)
+    return -(-int(dim) // per)
+
+
 def tier_widths(table: dict) -> tuple[list[int], list[int]]:
     """``(width_t for t=0..3, words_t for t=0..2)`` of a layer table."""
     widths = [int(table[t]["width"]) for t in range(4)]
     words = [(widths[t] + (16 >> t) - 1) // (16 >> t) for t in range(3)]
     return widths, words
+
+
+def asymmetric_codes(grouped: torch.Tensor, bits: int):
+    """Min-max codes over the last axis on the device (reference ``layout.py:12-18``).
+
+    ``grouped [..., group]`` (bfloat16, float16 or float32; computed in float32, the
+    reference's arithmetic on its float32 inputs).  Returns ``(codes int32 [..., group],
+    scale float32 [...], low float32 [...])`` with ``scale = clamp((max - min) / (2^bits - 1),
+    1e-5, 1e5)`` and ``codes = clamp(round_half_even((x - min) / scale), 0, 2^bits - 1)``.
+    """
+    device = _require_device(grouped)
+    x = grouped.contiguous()
+    lead = tuple(x.shape[:-1])
+    group = int(x.shape[-1]) if x.dim() else 1
+    n_groups = x.numel() // max(group, 1)
+    codes = torch.empty(x.shape, dtype=torch.int32, device=device)
+    scale = torch.empty(lead, dtype=torch.float32, device=device)
+    low = torch.empty(lead, dtype=torch.float32, device=device)
+    if n_groups and group:
+        st = _native.load().lf_asymmetric_codes(x.data_ptr(), _native.dtype_code(x.dtype), n_groups, group, int(bits),
+                                                codes.data_ptr(), scale.data_ptr(), low.data_ptr(),
+                                                _native.current_stream_ptr(device))
+        _native.check(st, "lf_asymmetric_codes")
+    return codes, scale, low
+
+
+def pack_ints(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """LSB-first packing of the last axis into int32 words on the device (reference
+    ``layout.py:21-35``): slot ``j`` goes to word ``j // per`` at bit ``(j % per) * bits``,
+    ``per = 32 // bits``, the last word zero padded.  ``codes`` are non-negative integers."""
+    device = _require_device(codes)
+    n = int(codes.shape[-1])
+    per = 32 // int(bits)
+    out = torch.zeros(*codes.shape[:-1], -(-n // per), dtype=torch.int32, device=device)
+    rows = codes.numel() // n if n else 0
+    if rows:
+        src = codes.to(torch.int32).contiguous()
+        st = _native.load().lf_pack_ints(src.data_ptr(), rows, n, int(bits), out.data_ptr(),
+                                         _native.current_stream_ptr(device))
+        _native.check(st, "lf_pack_ints")
+    return out
+
+
+def unpack_ints(packed: torch.Tensor, count: int, bits: int) -> torch.Tensor:
+    """The first ``count`` slots of each row of packed int32 words (reference
+    ``layout.py:38-46``), on the device; ``[..., words] -> [..., count]`` int32."""
+    device = _require_device(packed)
+    n_words = int(packed.shape[-1])
+    out = torch.zeros(*packed.shape[:-1], int(count), dtype=torch.int32, device=device)
+    rows = packed.numel() // n_words if n_words else 0
+    if count and rows:
+        src = packed.to(torch.int32).contiguous()
+        st = _native.load().lf_unpack_ints(src.data_ptr(), rows, n_words, int(count), int(bits), out.data_ptr(),
+                                           _native.current_stream_ptr(device))
+        _native.check(st, "lf_unpack_ints")
+    elif count and not n_words:
+        raise IndexError(f"cannot unpack {count} slots from rows of zero words")
+    return out
 
 
 def _require_device(*tensors: torch.Tensor) -> torch.device:
@@ -105,7 +172,7 @@ def make_layer_struct(table: dict, table_dev: dict, *, batch: int, n_kv: int, he
     s.batch, s.n_kv, s.head_dim = batch, n_kv, head_dim
     s.cap_tokens, s.cap_kgroups = cap_tokens, cap_kgroups
     s.page_size, s.k_group, s.v_group, s.bit_v = page_size, k_group, v_group, bit_v
-    s.v_words = head_dim * bit_v // 32 if bit_v < 16 else 0
+    s.v_words = value_words(head_dim, bit_v) if bit_v < 16 else 0
     s.v_groups = head_dim // v_group if bit_v < 16 else 0
     return s
 
@@ -140,7 +207,7 @@ def _quantize_page(key: torch.Tensor, value: torch.Tensor, table: dict, k_group:
     k_min = [torch.zeros(heads, widths[t], groups, dtype=torch.float16, device=device) for t in range(3)]
     k_value16 = torch.zeros(heads, tokens, widths[3], dtype=torch.float16, device=device)
     if bit_v < 16:
-        v = {"code": torch.zeros(heads, tokens, dim * bit_v // 32, dtype=torch.int32, device=device),
+        v = {"code": torch.zeros(heads, tokens, value_words(dim, bit_v), dtype=torch.int32, device=device),
              "scale": torch.zeros(heads, tokens, dim // v_group, dtype=torch.float16, device=device),
              "min": torch.zeros(heads, tokens, dim // v_group, dtype=torch.float16, device=device)}
         vv = dict(v_code=v["code"], v_scale=v["scale"], v_min=v["min"])

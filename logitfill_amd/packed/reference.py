@@ -20,6 +20,8 @@ from __future__ import annotations
 import ctypes
 import functools
 import os
+import warnings
+from collections import Counter
 
 import numpy as np
 import torch
@@ -29,24 +31,20 @@ from logitfill_amd.packed.cache import env_int
 
 
 def repeat_kv(states: torch.Tensor, repeats: int) -> torch.Tensor:
-    """``reference.py:10-15``: kv head h feeds query heads h*r .. h*r+r-1."""
-    if repeats == 1:
-        return states
-    batch, heads, tokens, dim = states.shape
-    states = states[:, :, None].expand(batch, heads, repeats, tokens, dim)
-    return states.reshape(batch, heads * repeats, tokens, dim)
+    """GQA head expansion (``reference.py:10-15``): ``[B, n_kv, T, D] -> [B, n_kv * repeats, T, D]``
+    with query head ``i`` reading kv head ``i // repeats``."""
+    return states if repeats == 1 else torch.repeat_interleave(states, repeats, dim=1)
 
 
 def _causal_mask(query_len: int, key_len: int, device) -> torch.Tensor | None:
-    """``reference.py:18-27``: float mask for queries aligned to the right edge of the keys."""
+    """Additive float mask of ``query_len`` queries that are the last ``query_len`` of
+    ``key_len`` keys (``reference.py:18-27``): query ``i`` sees keys ``0 .. key_len -
+    query_len + i``; None for one query."""
     if query_len == 1:
         return None
-    mask = torch.zeros(query_len, key_len, dtype=torch.float32, device=device)
-    for index in range(query_len):
-        visible = key_len - query_len + index + 1
-        if visible < key_len:
-            mask[index, visible:] = float("-inf")
-    return mask
+    last_visible = torch.arange(query_len, device=device)[:, None] + (key_len - query_len)
+    hidden = torch.arange(key_len, device=device)[None, :] > last_visible
+    return torch.zeros(query_len, key_len, device=device).masked_fill(hidden, float("-inf"))
 
 
 def reference_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
@@ -254,17 +252,58 @@ def _kernel_attention(manager, layer_idx: int, query: torch.Tensor, key_new: tor
     return out.view(B, n_q, q_len, D)
 
 
-# Query rows per kv head the multi-token kernel path serves ((n_q / n_kv) * q_len).
+# Query rows per kv head the decode kernels serve ((n_q / n_kv) * q_len).
 MAX_ROWS_PER_KV_HEAD = 16
+
+# Calls that took the dense dequantise-then-attend path because the decode kernels do not
+# serve their shape, by reason (read by tests and benchmarks; see ``packed_attention``).
+DENSE_FALLBACKS: Counter = Counter()
+_WARNED: set = set()
+
+
+def kernel_unsupported_reason(manager, q_len: int = 1) -> str | None:
+    """Why ``lf_decode_attention`` would not serve this manager's shape, or None when it does
+    (the checks of the C entry point: int2 Values as the reference kernel requires,
+    ``reference.py:62``; head_dim a power of two in 8..512; at most 16 query rows per kv head;
+    at most 64 Value groups; the general kernel's LDS within 160 KB)."""
+    D = int(manager.head_dim)
+    if manager.bit_v != 2:
+        return f"bit_v={manager.bit_v} (the decode kernels take int2 Values)"
+    if D < 8 or D > 512 or D & (D - 1):
+        return f"head_dim={D} (the decode kernels take powers of two in 8..512)"
+    rows = manager.n_q // manager.n_kv * int(q_len)
+    if rows > MAX_ROWS_PER_KV_HEAD:
+        return f"{rows} query rows per kv head (at most {MAX_ROWS_PER_KV_HEAD})"
+    vg = D // int(manager.v_group_size)
+    if vg > 64:
+        return f"{vg} Value groups per token (at most 64)"
+    slots = max(sum(layer.widths) for layer in manager.layers) if manager.layers else D
+    lds = 4 * (16 * D + 16 * 64 + 2 * 64 * vg + 64 * -(-D // 16) + 16 * slots)
+    if lds > 160 * 1024:
+        return f"{lds} bytes of LDS for the general kernel (at most 160 KB)"
+    return None
 
 
 def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
                      value_new: torch.Tensor, scaling: float) -> torch.Tensor:
-    """``reference.py:112-116``: ``query [B, n_q, q_len, D]`` -> ``[B, n_q, q_len, D]``."""
+    """``reference.py:112-116``: ``query [B, n_q, q_len, D]`` -> ``[B, n_q, q_len, D]``.
+
+    Shapes the decode kernels serve run the HIP split-K decode.  Others take the dense
+    dequantise-then-attend path on the device, as the reference falls back to its dense path
+    (``reference.py:62-68,105-108``) -- but not silently: each fallback is counted in
+    ``DENSE_FALLBACKS``, warned about once per reason, and raises instead when the environment
+    sets ``LOGITFILL_AMD_STRICT=1``.
+    """
     if not query.is_cuda:
         raise RuntimeError("logitfill_amd runs on ROCm devices only (there is no CPU path)")
-    q_len = int(query.shape[-2])
-    rows = manager.n_q // manager.n_kv * q_len
-    if manager.bit_v == 2 and (q_len == 1 or rows <= MAX_ROWS_PER_KV_HEAD):
+    reason = kernel_unsupported_reason(manager, int(query.shape[-2]))
+    if reason is None:
         return _kernel_attention(manager, layer_idx, query, key_new, value_new, scaling)
+    if os.environ.get("LOGITFILL_AMD_STRICT", "") == "1":
+        raise _native.LFError(_native.LF_E_UNSUPPORTED, reason, "packed_attention")
+    DENSE_FALLBACKS[reason] += 1
+    if reason not in _WARNED:
+        _WARNED.add(reason)
+        warnings.warn(f"packed_attention: {reason}; running the dense dequantise-then-attend path on the device",
+                      RuntimeWarning, stacklevel=2)
     return reference_attention(manager, layer_idx, query, key_new, value_new, scaling)

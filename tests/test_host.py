@@ -62,7 +62,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
         assert name in _native._SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.lf_abi_version() == 5
+    assert lib.lf_abi_version() == 6
     assert b"gfx950" in lib.lf_build_info()
 
 
@@ -160,3 +160,25 @@ def test_argument_validation_rejects_before_launch():
     assert lib.lf_decode_attention(layer, None, None) == -2
     assert lib.lf_dequantize(layer, 0, 4, None, None, None) == -1
     assert lib.lf_dense_decode(None, None, None, 1, 1, 1, 128, 1, 0, 0, 0, 1.0, None, 64, None, 0, None) == -1
+
+
+def test_layout_helper_validation_rejects_before_launch():
+    """The device layout helpers check sizes on the host; nothing is launched here."""
+    lib = _native.load()
+    assert lib.lf_pack_ints(None, 1, 4, 3, None, None) == -2          # 3 does not divide 32
+    assert lib.lf_pack_ints(None, 0, 4, 2, None, None) == 0           # empty: nothing to do
+    assert lib.lf_pack_ints(None, 1, 4, 2, None, None) == -1
+    assert lib.lf_unpack_ints(None, 1, 1, 17, 2, None, None) == -2    # 17 slots > 1 word x 16
+    assert lib.lf_unpack_ints(None, 1, 1, 16, 2, None, None) == -1
+    assert lib.lf_asymmetric_codes(None, 7, 1, 4, 2, None, None, None, None) == -5
+    assert lib.lf_asymmetric_codes(None, 0, 1, 4, 0, None, None, None, None) == -2
+    assert lib.lf_asymmetric_codes(None, 0, 0, 4, 2, None, None, None, None) == 0
+
+
+def test_padded_value_words_accepted():
+    """Value rows whose width is not a word multiple are padded (reference layout.py:27-29),
+    and the layer check wants ceil(head_dim * bit_v / 32) words: a D 8 int2 layer has one."""
+    from logitfill_amd.packed.layout import value_words
+
+    assert value_words(8, 2) == 1 and value_words(128, 2) == 8 and value_words(24, 4) == 3
+    assert value_words(100, 8) == 25 and value_words(12, 8) == 3

@@ -69,3 +69,82 @@ def test_decoder_wiring_reproduces_the_model():
         multi = model(input_ids=ids[:, 27:], position_ids=pos, use_cache=False).logits[0]
     detach_packed(model)
     assert torch.allclose(multi, want[27:], atol=1e-4, rtol=1e-4)
+
+
+class _ExactCacheWithLength(_ExactCache):
+    """The exact cache plus the manager's ``seq_len`` (the last layer's length, as the
+    reference manager updates it at the last layer's commit)."""
+
+    @property
+    def seq_len(self):
+        return self.layer_length(len(self.layers) - 1)
+
+
+def _small_model():
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512,
+                      rope_theta=10000.0, attn_implementation="eager")
+    torch.manual_seed(0)
+    return Qwen2ForCausalLM(cfg).float().eval()
+
+
+def test_logitfill_cache_shim_on_installed_transformers():
+    """LogitFillCache (reference packed/cache.py:149-183) constructs on transformers 5.x and
+    answers lengths and mask sizes from the manager; writes and beam search are refused."""
+    from logitfill_amd.packed.cache import LogitFillCache
+
+    cache = _ExactCacheWithLength(2, 2, 64)
+    hf = LogitFillCache(cache)
+    assert hf.get_seq_length() == 0 and hf.get_mask_sizes(5, 0) == (5, 0)
+    cache.commit(0, torch.zeros(1, 2, 7, 64), torch.zeros(1, 2, 7, 64))
+    cache.commit(1, torch.zeros(1, 2, 7, 64), torch.zeros(1, 2, 7, 64))
+    assert hf.get_seq_length() == 7 and hf.get_query_offset() == 7
+    assert hf.get_mask_sizes(1, 0) == (8, 0)
+    assert hf.get_mask_sizes(torch.arange(3), 0) == (10, 0)  # transformers 4.x passes cache positions
+    assert not hf.is_compileable and hf.get_max_length() == -1
+    try:
+        hf.update(None, None, 0)
+        raise AssertionError("update must raise")
+    except RuntimeError:
+        pass
+    try:
+        hf.reorder_cache(torch.arange(1))
+        raise AssertionError("reorder_cache must raise")
+    except NotImplementedError:
+        pass
+    hf.reset()
+    assert hf.get_seq_length() == 0
+
+
+def test_generate_through_logitfill_cache_matches_plain_generate():
+    """``model.generate(..., past_key_values=LogitFillCache(manager))`` -- the reference
+    adapter's ``make_cache`` path (deepseek_qwen.py:141-146) -- decodes the same greedy tokens
+    as the unmodified model without a cache, and PackedDecoder(hf_cache=True) gives the same
+    logits as PackedDecoder with explicit positions."""
+    from logitfill_amd.packed.cache import LogitFillCache
+    from logitfill_amd.qwen2 import attach_packed
+
+    model = _small_model()
+    ids = torch.randint(0, 256, (1, 20), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        want = model.generate(ids, max_new_tokens=8, do_sample=False, use_cache=False)
+    cache = _ExactCacheWithLength(2, 2, 64)
+    attach_packed(model, cache, _exact_attention)
+    with torch.no_grad():
+        got = model.generate(ids, max_new_tokens=8, do_sample=False, past_key_values=LogitFillCache(cache),
+                             use_cache=True)
+    detach_packed(model)
+    assert torch.equal(got, want)
+    assert cache.layer_length(0) == 27  # prompt + 7 committed decode inputs
+
+    runs = []
+    for hf_cache in (False, True):
+        dec = PackedDecoder(model, _ExactCacheWithLength(2, 2, 64), _exact_attention, hf_cache=hf_cache)
+        steps = [dec.prefill(ids)]
+        for t in range(5):
+            steps.append(dec.step(want[0, 20 + t]))
+        detach_packed(model)
+        runs.append(torch.cat(steps))
+    assert torch.allclose(runs[0], runs[1], atol=1e-5, rtol=1e-5)
