@@ -28,36 +28,38 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     const int nw = blockDim.x / kWave;
 
     if (count <= kFastItems) {
-        // Every thread (one per channel) loads all items' (m, l) -- the same addresses across
-        // the workgroup -- and its channel's o, all before the first use: one load latency.
-        float m[kFastItems], l[kFastItems], o[kFastItems];
+        // Every thread loads all items' (m, l) -- the same addresses across the workgroup --
+        // and its channels' o, all before the first use: one load latency per channel pass.
+        float m[kFastItems], l[kFastItems];
 #pragma unroll
         for (int k = 0; k < kFastItems; ++k) {
             m[k] = -__builtin_inff();
             l[k] = 0.f;
-            o[k] = 0.f;
             if (k < count) {
                 const float* r = part_rec(p, first + k, h, i);
                 m[k] = r[D];
                 l[k] = r[D + 1];
-                if (tid < D) o[k] = r[tid];
             }
         }
-        float M = m[0];
+        for (int c = tid; c < D; c += blockDim.x) {
+            float o[kFastItems];
 #pragma unroll
-        for (int k = 1; k < kFastItems; ++k) M = fmaxf(M, m[k]);
-        float lsum = 0.f, osum = 0.f;
-        if (M != -__builtin_inff()) {
+            for (int k = 0; k < kFastItems; ++k) o[k] = k < count ? part_rec(p, first + k, h, i)[c] : 0.f;
+            float M = m[0];
 #pragma unroll
-            for (int k = 0; k < kFastItems; ++k) {
-                const float wk = __builtin_amdgcn_exp2f(m[k] - M);  // 0 for the items past count
-                lsum = fmaf(wk, l[k], lsum);
-                osum = fmaf(wk, o[k], osum);
+            for (int k = 1; k < kFastItems; ++k) M = fmaxf(M, m[k]);
+            float lsum = 0.f, osum = 0.f;
+            if (M != -__builtin_inff()) {
+#pragma unroll
+                for (int k = 0; k < kFastItems; ++k) {
+                    const float wk = __builtin_amdgcn_exp2f(m[k] - M);  // 0 for the items past count
+                    lsum = fmaf(wk, l[k], lsum);
+                    osum = fmaf(wk, o[k], osum);
+                }
             }
-        }
-        if (tid < D)
-            store_from_f32(p.A.out, (static_cast<int64_t>(b) * p.A.n_q + h * g + i) * D + tid, p.A.out_dtype,
+            store_from_f32(p.A.out, (static_cast<int64_t>(b) * p.A.n_q + h * g + i) * D + c, p.A.out_dtype,
                            lsum > 0.f ? osum / lsum : 0.f);
+        }
         return;
     }
 

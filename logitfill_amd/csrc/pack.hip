@@ -86,7 +86,9 @@ __device__ __forceinline__ uint32_t group_code(float x, float lo, float s, int q
     return static_cast<uint32_t>(fminf(fmaxf(q, 0.0f), static_cast<float>(qmax)));
 }
 
-template <typename T, bool IsHalf>
+// ``Staged``: the page is copied to LDS first; otherwise (pages too large for LDS next to the
+// code rows) every element is read from global memory where it is used.
+template <typename T, bool IsHalf, bool Staged>
 __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a) {
     const lf_packed_layer& L = a.L;
     const int job = blockIdx.x;
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
     extern __shared__ __align__(16) unsigned char smem[];
     T* page_lds = reinterpret_cast<T*>(smem);
     const int cw = a.cw;
-    uint8_t* codes = smem + static_cast<size_t>(P) * ld * sizeof(T);     // [P][cw]
+    uint8_t* codes = smem + (Staged ? static_cast<size_t>(P) * ld * sizeof(T) : 0);  // [P][cw]
     int8_t* tier_of = reinterpret_cast<int8_t*>(codes + P * cw);         // [D]
     int16_t* local_of = reinterpret_cast<int16_t*>(tier_of + ((D + 1) & ~1));  // [D]
 
@@ -127,7 +129,10 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
 
     // ---- Key page ----
     const T* ksrc = static_cast<const T*>(a.k_src) + b * a.sb + h * a.sh + tok0 * a.st;
-    stage_page<T>(page_lds, ld, ksrc, a.st, P, D, a.vec16 != 0);
+    const T* vsrc = static_cast<const T*>(a.v_src) + b * a.sb + h * a.sh + tok0 * a.st;
+    const T* cur = ksrc;  // the page the accessor below reads
+    auto at = [&](int tau, int c) -> T { return Staged ? page_lds[tau * ld + c] : cur[tau * a.st + c]; };
+    if (Staged) stage_page<T>(page_lds, ld, ksrc, a.st, P, D, a.vec16 != 0);
     __syncthreads();
 
     const int kg = L.k_group;
@@ -149,7 +154,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
         float lo = __builtin_inff(), hi = -__builtin_inff();
         if (quant) {
             for (int tau = beg; tau < end; ++tau) {
-                const float x = elem_f32<T, IsHalf>(page_lds[tau * ld + c]);
+                const float x = elem_f32<T, IsHalf>(at(tau, c));
                 lo = fminf(lo, x);
                 hi = fmaxf(hi, x);
             }
@@ -161,7 +166,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
             const int j = local_of[c];
             uint8_t* crow = codes + koff[t] + j;
             for (int tau = beg; tau < end; ++tau) {
-                const float x = elem_f32<T, IsHalf>(page_lds[tau * ld + c]);
+                const float x = elem_f32<T, IsHalf>(at(tau, c));
                 crow[tau * cw] = static_cast<uint8_t>(group_code(x, lo, s, qmax));
             }
             if (half == 0) {
@@ -216,8 +221,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
             uint16_t v = 0;
             if (j < cnt) {
                 const int c = L.tier_index[3][h * w16 + j];
-                if constexpr (IsHalf) v = static_cast<uint16_t>(page_lds[tau * ld + c]);
-                else v = f32_to_f16(elem_f32<T, IsHalf>(page_lds[tau * ld + c]));
+                if constexpr (IsHalf) v = static_cast<uint16_t>(at(tau, c));
+                else v = f32_to_f16(elem_f32<T, IsHalf>(at(tau, c)));
             }
             out[idx] = v;
         }
@@ -225,8 +230,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
     __syncthreads();
 
     // ---- Value page (layout.py:115-129) ----
-    const T* vsrc = static_cast<const T*>(a.v_src) + b * a.sb + h * a.sh + tok0 * a.st;
-    stage_page<T>(page_lds, ld, vsrc, a.st, P, D, a.vec16 != 0);
+    cur = vsrc;
+    if (Staged) stage_page<T>(page_lds, ld, vsrc, a.st, P, D, a.vec16 != 0);
     __syncthreads();
 
     if (L.bit_v >= 16) {
@@ -234,8 +239,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
         for (int idx = threadIdx.x; idx < P * D; idx += kPackThreads) {
             const int tau = idx / D;
             const int c = idx % D;
-            if constexpr (IsHalf) out[idx] = static_cast<uint16_t>(page_lds[tau * ld + c]);
-            else out[idx] = f32_to_f16(elem_f32<T, IsHalf>(page_lds[tau * ld + c]));
+            if constexpr (IsHalf) out[idx] = static_cast<uint16_t>(at(tau, c));
+            else out[idx] = f32_to_f16(elem_f32<T, IsHalf>(at(tau, c)));
         }
         return;
     }
@@ -255,7 +260,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
         float lo = __builtin_inff(), hi = -__builtin_inff();
         if (live) {
             for (int c = beg; c < end; ++c) {
-                const float x = elem_f32<T, IsHalf>(page_lds[tau * ld + c]);
+                const float x = elem_f32<T, IsHalf>(at(tau, c));
                 lo = fminf(lo, x);
                 hi = fmaxf(hi, x);
             }
@@ -265,7 +270,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
         if (live) {
             const float s = group_scale(hi, lo, vqmax);
             for (int c = beg; c < end; ++c) {
-                const float x = elem_f32<T, IsHalf>(page_lds[tau * ld + c]);
+                const float x = elem_f32<T, IsHalf>(at(tau, c));
                 codes[tau * cw + c] = static_cast<uint8_t>(group_code(x, lo, s, vqmax));
             }
             if (half == 0) {
@@ -670,18 +675,26 @@ int pack_code_row(const lf_packed_layer& L) {
     return wsum > L.head_dim ? wsum : L.head_dim;
 }
 
-size_t pack_lds_bytes(const lf_packed_layer& L, int elem) {
+// Dynamic LDS of the generic kernel: the staged page (when ``staged``), the code rows and the
+// per-channel tier maps.
+size_t pack_lds_bytes(const lf_packed_layer& L, int elem, bool staged) {
     const int D = L.head_dim;
     const int ld = D + (elem == 2 ? 2 : 1);
-    return static_cast<size_t>(L.page_size) * ld * elem +
+    return (staged ? static_cast<size_t>(L.page_size) * ld * elem : 0) +
            static_cast<size_t>(L.page_size) * pack_code_row(L) + ((D + 1) & ~1) + 2 * D + 16;
 }
 
 template <typename T, bool IsHalf>
-int launch_one(const PackJobArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-    const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&pack_pages_kernel<T, IsHalf>), lds);
+int launch_one(const PackJobArgs& a, dim3 grid, int elem, hipStream_t stream) {
+    const bool staged = pack_lds_bytes(a.L, elem, true) <= 160 * 1024;
+    const size_t lds = pack_lds_bytes(a.L, elem, staged);
+    if (lds > 160 * 1024) return LF_E_SHAPE;
+    const void* fn = staged ? reinterpret_cast<const void*>(&pack_pages_kernel<T, IsHalf, true>)
+                            : reinterpret_cast<const void*>(&pack_pages_kernel<T, IsHalf, false>);
+    const int rc = allow_dynamic_lds(fn, lds);
     if (rc != LF_OK) return rc;
-    hipLaunchKernelGGL((pack_pages_kernel<T, IsHalf>), grid, dim3(kPackThreads), lds, stream, a);
+    if (staged) hipLaunchKernelGGL((pack_pages_kernel<T, IsHalf, true>), grid, dim3(kPackThreads), lds, stream, a);
+    else hipLaunchKernelGGL((pack_pages_kernel<T, IsHalf, false>), grid, dim3(kPackThreads), lds, stream, a);
     return LF_OK;
 }
 
@@ -719,12 +732,10 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
             return err == hipSuccess ? LF_OK : static_cast<int>(err);
         }
     }
-    const size_t lds = pack_lds_bytes(L, elem);
-    if (lds > 160 * 1024) return LF_E_SHAPE;
     int rc;
-    if (src_dtype == LF_BF16) rc = launch_one<uint16_t, false>(a, grid, lds, stream);
-    else if (src_dtype == LF_FP16) rc = launch_one<uint16_t, true>(a, grid, lds, stream);
-    else if (src_dtype == LF_FP32) rc = launch_one<float, false>(a, grid, lds, stream);
+    if (src_dtype == LF_BF16) rc = launch_one<uint16_t, false>(a, grid, elem, stream);
+    else if (src_dtype == LF_FP16) rc = launch_one<uint16_t, true>(a, grid, elem, stream);
+    else if (src_dtype == LF_FP32) rc = launch_one<float, false>(a, grid, elem, stream);
     else return LF_E_DTYPE;
     if (rc != LF_OK) return rc;
     const hipError_t err = hipGetLastError();
