@@ -10,9 +10,10 @@
  * Conventions
  *  - Plain C: device pointers, sizes and strides only; no torch types.
  *  - The caller owns every buffer, including outputs and workspaces; the
- *    library never allocates device memory and keeps no mutable global state
- *    (no static variables written after load), so every entry point is
- *    re-entrant and may be called from several host threads at once.
+ *    library never allocates device memory.  Its only mutable global state is
+ *    the per-device address of the scratch array of
+ *    lf_decode_attention_noalloc, looked up once per device under a lock; every
+ *    entry point is re-entrant and may be called from several host threads.
  *  - ``stream`` is a hipStream_t passed as ``void*`` (NULL = default stream).
  *    Nothing synchronises inside; all work is enqueued on ``stream``.
  *  - Return value: 0 = success; negative = argument/shape error (LF_E_*),
@@ -203,6 +204,22 @@ int64_t lf_decode_workspace_bytes(int32_t n_q, int32_t head_dim, int32_t n_work)
  * dense path, reference.py:105-108).
  */
 int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* args, void* stream);
+
+/*
+ * Decode attention that allocates nothing (no counterpart in the reference): for callers
+ * that cannot allocate device memory -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  Same arguments, checks, kernels and results as
+ * lf_decode_attention, except that the split-K partials go to a file-scope device array of
+ * LF_NOALLOC_SCRATCH_BYTES per GPU (held from library load until the process ends) and the
+ * args' workspace / workspace_bytes are ignored.  A call whose partials
+ * (lf_decode_workspace_bytes(n_q * q_len, head_dim, n_work)) exceed that size returns
+ * LF_E_WORKSPACE and enqueues nothing.  The current HIP device must be the device of
+ * ``stream`` and of every buffer.  All calls on one GPU share its array, and it keeps the
+ * last call's partials: calls that overlap on one GPU (other streams or host threads) race.
+ */
+#define LF_NOALLOC_SCRATCH_BYTES (16u << 20)
+int32_t lf_decode_attention_noalloc(const lf_packed_layer* layer, const lf_decode_args* args, void* stream);
+int64_t lf_noalloc_scratch_bytes(void);
 
 /*
  * Dense fp32 dequantisation of sequence b's first ``tokens`` history tokens

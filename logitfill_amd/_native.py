@@ -108,6 +108,8 @@ _SIGNATURES = {
                                       c_void_p]),
     "lf_pack_ints": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p]),
     "lf_unpack_ints": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
+    "lf_decode_attention_noalloc": (c_int32, [POINTER(PackedLayer), POINTER(DecodeArgs), c_void_p]),
+    "lf_noalloc_scratch_bytes": (c_int64, []),
 }
 
 ABI_VERSION = 6

@@ -70,6 +70,61 @@ int32_t check_layer(const lf_packed_layer* L, bool need_k = true, bool need_v = 
 
 }  // namespace
 
+namespace lf {
+
+// Checks shared by the decode entry points, then the launch with ``workspace`` (at least
+// ``workspace_bytes``) as the split-K partials.  The args' own workspace fields are not read.
+int32_t decode_checked(const lf_packed_layer* layer, const lf_decode_args* args, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+    const int32_t st = check_layer(layer);
+    if (st != LF_OK) return st;
+    if (!args) return LF_E_NULL;
+    const lf_decode_args& A = *args;
+    if (!A.query || !A.out || !A.work || !A.seq_work || !workspace || !A.tail_len) return LF_E_NULL;
+    if ((A.k_new == nullptr) != (A.v_new == nullptr)) return LF_E_NULL;
+    if (!valid_dtype(A.q_dtype) || !valid_dtype(A.out_dtype) || !valid_dtype(A.tail_dtype)) return LF_E_DTYPE;
+    if (A.k_new && !valid_dtype(A.new_dtype)) return LF_E_DTYPE;
+    if (A.n_q <= 0 || A.n_q % layer->n_kv != 0) return LF_E_SHAPE;
+    if (A.q_len < 0) return LF_E_SHAPE;
+    const int q_len = A.q_len > 1 ? A.q_len : 1;
+    // q_len new tokens: the kernels serve n_q * q_len query rows (row = head * q_len + token)
+    const int64_t rows = static_cast<int64_t>(A.n_q) * q_len;
+    if (rows > (1 << 20)) return LF_E_SHAPE;
+    const int g = static_cast<int>(rows / layer->n_kv);
+    if (g > 16) return LF_E_UNSUPPORTED;
+    if (layer->bit_v != 2) return LF_E_UNSUPPORTED;  // as reference.py:62
+    const int D = layer->head_dim;
+    if (D < 8 || D > 512 || (D & (D - 1)) != 0) return LF_E_UNSUPPORTED;
+    if (layer->v_groups > 64) return LF_E_UNSUPPORTED;
+    if (A.tail_cap < 0 || A.tail_cap > layer->page_size) return LF_E_SHAPE;
+    if (A.tail_cap > 0 && (!A.tail_k || !A.tail_v)) return LF_E_NULL;
+    if (A.n_work <= 0) return LF_E_SHAPE;
+    if (workspace_bytes < lf_decode_workspace_bytes(static_cast<int32_t>(rows), D, A.n_work)) return LF_E_WORKSPACE;
+    if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
+    if (q_len > 1 && A.kernel == 2) return LF_E_UNSUPPORTED;  // the MFMA kernel takes one token
+
+    DecodeParams p;
+    p.L = *layer;
+    p.A = A;
+    p.A.n_q = static_cast<int32_t>(rows);
+    p.A.workspace = workspace;
+    p.A.workspace_bytes = workspace_bytes;
+    p.g = g;
+    p.q_len = q_len;
+    p.qscale = A.scaling * kLog2e;
+    p.part = static_cast<float*>(workspace);
+    p.dense_splits = 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (A.kernel != 1 && q_len == 1) {
+        bool handled = false;
+        const int r = launch_decode_mfma(p, s, &handled);
+        if (handled || A.kernel == 2) return handled ? r : LF_E_UNSUPPORTED;
+    }
+    return launch_decode_valu(p, s);
+}
+
+}  // namespace lf
+
 extern "C" {
 
 int32_t lf_abi_version(void) { return LF_ABI_VERSION; }
@@ -159,50 +214,8 @@ int64_t lf_decode_workspace_bytes(int32_t n_q, int32_t head_dim, int32_t n_work)
 }
 
 int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* args, void* stream) {
-    const int32_t st = check_layer(layer);
-    if (st != LF_OK) return st;
-    if (!args) return LF_E_NULL;
-    const lf_decode_args& A = *args;
-    if (!A.query || !A.out || !A.work || !A.seq_work || !A.workspace || !A.tail_len) return LF_E_NULL;
-    if ((A.k_new == nullptr) != (A.v_new == nullptr)) return LF_E_NULL;
-    if (!valid_dtype(A.q_dtype) || !valid_dtype(A.out_dtype) || !valid_dtype(A.tail_dtype)) return LF_E_DTYPE;
-    if (A.k_new && !valid_dtype(A.new_dtype)) return LF_E_DTYPE;
-    if (A.n_q <= 0 || A.n_q % layer->n_kv != 0) return LF_E_SHAPE;
-    if (A.q_len < 0) return LF_E_SHAPE;
-    const int q_len = A.q_len > 1 ? A.q_len : 1;
-    // q_len new tokens: the kernels serve n_q * q_len query rows (row = head * q_len + token)
-    const int64_t rows = static_cast<int64_t>(A.n_q) * q_len;
-    if (rows > (1 << 20)) return LF_E_SHAPE;
-    const int g = static_cast<int>(rows / layer->n_kv);
-    if (g > 16) return LF_E_UNSUPPORTED;
-    if (layer->bit_v != 2) return LF_E_UNSUPPORTED;  // as reference.py:62
-    const int D = layer->head_dim;
-    if (D < 8 || D > 512 || (D & (D - 1)) != 0) return LF_E_UNSUPPORTED;
-    if (layer->v_groups > 64) return LF_E_UNSUPPORTED;
-    if (A.tail_cap < 0 || A.tail_cap > layer->page_size) return LF_E_SHAPE;
-    if (A.tail_cap > 0 && (!A.tail_k || !A.tail_v)) return LF_E_NULL;
-    if (A.n_work <= 0) return LF_E_SHAPE;
-    if (A.workspace_bytes < lf_decode_workspace_bytes(static_cast<int32_t>(rows), D, A.n_work))
-        return LF_E_WORKSPACE;
-    if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
-    if (q_len > 1 && A.kernel == 2) return LF_E_UNSUPPORTED;  // the MFMA kernel takes one token
-
-    lf::DecodeParams p;
-    p.L = *layer;
-    p.A = A;
-    p.A.n_q = static_cast<int32_t>(rows);
-    p.g = g;
-    p.q_len = q_len;
-    p.qscale = A.scaling * lf::kLog2e;
-    p.part = static_cast<float*>(A.workspace);
-    p.dense_splits = 0;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (A.kernel != 1 && q_len == 1) {
-        bool handled = false;
-        const int r = lf::launch_decode_mfma(p, s, &handled);
-        if (handled || A.kernel == 2) return handled ? r : LF_E_UNSUPPORTED;
-    }
-    return lf::launch_decode_valu(p, s);
+    return lf::decode_checked(layer, args, args ? args->workspace : nullptr, args ? args->workspace_bytes : 0,
+                              stream);
 }
 
 int32_t lf_dequantize(const lf_packed_layer* layer, int32_t b, int32_t tokens, float* k_out, float* v_out,

@@ -171,14 +171,16 @@ def kernel_choice() -> int:
 
 
 def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new, scaling: float,
-                out: torch.Tensor, kernel: int | None = None, pages_per_split: int | None = None) -> None:
+                out: torch.Tensor, kernel: int | None = None, pages_per_split: int | None = None,
+                noalloc: bool = False) -> None:
     """Enqueue the fused decode kernel for layer ``layer_idx`` writing ``out``.
 
     One new token: ``query/out [B, n_q, D]``, ``key_new/value_new [B, n_kv, D]`` or None.
     ``q_len`` new tokens: ``query/out [B, n_q, q_len, D]``, ``key_new/value_new
     [B, n_kv, q_len, D]``; query token j sees the history, the tail and new tokens 0..j
     (reference ``reference.py:18-27,48``).  Everything is enqueued on the current stream;
-    nothing synchronises.
+    nothing synchronises.  ``noalloc`` calls ``lf_decode_attention_noalloc`` (the partials in
+    the library's per-GPU scratch array instead of the manager's workspace).
     """
     layer = manager.layers[layer_idx]
     layer.flush()  # deferred residual pages of this layer, if any
@@ -201,7 +203,7 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
         layer.decode_plan = plan
     lib = _native.load()
     nbytes = lib.lf_decode_workspace_bytes(manager.n_q * q_len, layer.head_dim, plan.n_work)
-    ws = manager.workspace(nbytes)
+    ws = None if noalloc else manager.workspace(nbytes)
     tail_k, tail_v = layer.tail_buffers()
     a = _native.DecodeArgs()
     a.query = query.data_ptr()
@@ -228,12 +230,17 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     a.work = plan.work.data_ptr()
     a.n_work = plan.n_work
     a.seq_work = plan.seq_work.data_ptr()
-    a.workspace = ws.data_ptr()
-    a.workspace_bytes = ws.numel()
+    a.workspace = 0 if ws is None else ws.data_ptr()
+    a.workspace_bytes = 0 if ws is None else ws.numel()
     a.kernel = kernel
     a.q_len = q_len
-    st = lib.lf_decode_attention(layer.layer_struct(), a, _native.current_stream_ptr(layer.device))
-    _native.check(st, "lf_decode_attention")
+    stream = _native.current_stream_ptr(layer.device)
+    if noalloc:
+        st = lib.lf_decode_attention_noalloc(layer.layer_struct(), a, stream)
+        _native.check(st, "lf_decode_attention_noalloc")
+    else:
+        st = lib.lf_decode_attention(layer.layer_struct(), a, stream)
+        _native.check(st, "lf_decode_attention")
 
 
 def _kernel_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
