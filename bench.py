@@ -44,6 +44,8 @@ def parse_args():
     p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the other decode configs (c2 at target 3.0, c1, c4) reported beside the headline")
+    p.add_argument("--compress-only", action="store_true",
+                   help="only time the config-3 page compress (one JSON line; for profiling runs)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                    help="only run a plain device-to-device copy of BYTES (3 times) and exit: the reference "
                         "kernel that scales the PMC byte counters (FETCH_SIZE / WRITE_SIZE)")
@@ -306,6 +308,27 @@ def time_compress(target_bit, steps, warmup):
     return us, us_layer, page_heads, read, written
 
 
+def host_cpu():
+    """(threads for the CPU baseline, logical CPUs of the host, CPU model).  The threads are
+    the CPUs this process may run on, capped by OMP_NUM_THREADS when the environment sets it
+    (the GPU box gives each job a share of its cores that way)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    threads = max(1, min(avail, int(cap))) if cap and cap.isdigit() else max(1, avail)
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return threads, os.cpu_count() or 1, model
+
+
 def cpu_baseline(cfg, n_seqs):
     """The oracle's dense path (dequantise whole history, concatenate, repeat_kv, fp32
     softmax attention) on one layer for ``n_seqs`` sequences, scaled to the batch."""
@@ -319,9 +342,10 @@ def cpu_baseline(cfg, n_seqs):
     B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
     pages_b, resid_b, tb = seq_lengths(cfg)
     pages, resid = pages_b[0], resid_b[0]
-    cores = max(1, min(16, os.cpu_count() or 1))
+    threads, host_cpus, model = host_cpu()
     times = []
-    with threadpool_limits(limits=cores):
+    t_leg = time.perf_counter()
+    with threadpool_limits(limits=threads):
         for s in range(n_seqs):
             d = synth.make_layer(1, n_q, n_kv, D, pages * 128 + resid, tb, seed=1000 + s)
             key = d.key[0].float().numpy()
@@ -338,17 +362,78 @@ def cpu_baseline(cfg, n_seqs):
                 runs.append(time.perf_counter() - t0)
             times.append(float(np.median(runs)))
     per_seq = float(np.mean(times))
-    return {"value": round(per_seq * B * 1e6, 1), "unit": "us/step/layer", "cores": cores, "kind": "port",
+    return {"value": round(per_seq * B * 1e6, 1), "unit": "us/step/layer", "cores": threads, "kind": "port",
+            "host_cpus": host_cpus, "cpu_model": model, "wall_s": round(time.perf_counter() - t_leg, 1),
+            "per_run_s": round(per_seq, 4),
             "sample": f"1 layer x {n_seqs} of {B} sequences at the full shape ({pages} pages + {resid} "
                       f"residual + 1), median of 3 after 1 warm-up, scaled x{B // n_seqs if n_seqs else 0} "
-                      "to the batch; numpy float32 (BLAS threads = cores)"}
+                      f"to the batch; numpy float32 with {threads} BLAS threads"}
+
+
+def cpu_baseline_compress(target_bit, n_pages=16):
+    """The oracle's page packer (quantize_key_page + quantize_value_page, reference
+    layout.py:71-129) on ``n_pages`` config-3 page-heads of 4 kv heads (one layer's page for
+    n_pages / 4 sequences), median of 3 after 1 warm-up.  Returns page-heads per second."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from logitfill_amd import synth
+    from oracle import layout as ol
+
+    threads, host_cpus, model = host_cpu()
+    t_leg = time.perf_counter()
+    seqs = max(1, n_pages // 4)
+    d = synth.make_layer(seqs, 28, 4, 128, 128, target_bit, seed=0)
+    table = ol.layer_table(d.levels)
+    pages_k = [d.key[b].float().numpy() for b in range(seqs)]
+    pages_v = [d.value[b].float().numpy() for b in range(seqs)]
+
+    def run():
+        for k, v in zip(pages_k, pages_v):
+            ol.quantize_key_page(k, table, 128)
+            ol.quantize_value_page(v, 2, 128)
+
+    with threadpool_limits(limits=threads):
+        run()
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            runs.append(time.perf_counter() - t0)
+    per_pass = float(np.median(runs))
+    page_heads = 4 * seqs
+    return {"value": round(page_heads / per_pass, 1), "unit": "page-heads/s", "cores": threads, "kind": "port",
+            "host_cpus": host_cpus, "cpu_model": model, "wall_s": round(time.perf_counter() - t_leg, 1),
+            "sample": f"{page_heads} page-heads (4 kv heads x {seqs} sequences, one 128-token page each, "
+                      f"target_bit {target_bit}), median of 3 after 1 warm-up; numpy float32"}
+
+
+def compress_record(steps=10, warmup=2):
+    comp = {}
+    for tb in (2.5, 3.0, 4.0):
+        us_c, us_c_layer, ph, rd, wr = time_compress(tb, steps, warmup)
+        comp[f"target_{tb}"] = {"us_per_pass": round(us_c, 1), "page_heads": ph,
+                                "pages_per_s": round(ph / us_c * 1e6), "gbs": round((rd + wr) / us_c / 1e3, 1),
+                                "hbm_frac": round((rd + wr) / us_c / 1e3 / HBM_PEAK_GBS, 4),
+                                "bytes_read": rd, "bytes_written": wr,
+                                "us_per_pass_one_launch_per_layer": round(us_c_layer, 1)}
+    return {"what": "BASELINE config 3: 64 sequences x 1 page x 4 kv heads x 28 layers, bf16 K/V from the "
+                    "config-0 distributions; us_per_pass = one lf_pack_pages_multi launch for the 28 layers (a "
+                    "deferring manager's end-of-step flush), us_per_pass_one_launch_per_layer = 28 lf_pack_pages "
+                    "launches; pages_per_s counts page-heads; GB/s = bf16 pages read + packed bytes written",
+            **comp}
+
+
+ARITHMETIC = ("bf16 query/residual/output; packed int2/int4/int8 codes and fp16 tier values from HBM; "
+              "scores and probability x Value products on the matrix cores with fp16 hi+lo operands; "
+              "fp32 accumulation and softmax")
 
 
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of this "
-              "path is a design note, not a built component", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the path on one GPU "
+              "(its multi-GPU sharding is a design note)", file=sys.stderr)
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -357,16 +442,24 @@ def main():
 
     from logitfill_amd import _native, synth
 
+    legs = {}
+    if args.compress_only:
+        t0 = time.perf_counter()
+        rec = compress_record(args.steps, args.warmup)
+        legs["compress"] = round(time.perf_counter() - t0, 2)
+        print(json.dumps({"compress_c3": rec, "leg_wall_s": legs}), flush=True)
+        return
     cfg = dict(synth.CONFIGS[args.config])
     layers = args.layers or cfg["layers"]
     dev = torch.device("cuda", 0)
     kernel = {"auto": _native.KERNEL_AUTO, "valu": _native.KERNEL_VALU, "mfma": _native.KERNEL_MFMA}[args.kernel]
     print(f"[bench] building {layers} layers of {args.config} and timing ...", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
     us_layer, bytes_launch, pay_launch, wall_ms = decode_point(cfg, layers, args.steps, args.warmup, kernel,
                                                                args.pages_per_split, dev)
+    legs["decode"] = round(time.perf_counter() - t0, 2)
     ms_step = us_layer * layers / 1e3
     B, n_q, n_kv, D = cfg["batch"], cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
-    tot_bytes = bytes_launch * layers
     pay_bytes = pay_launch * layers
     launch_s = us_layer / 1e6
     achieved = bytes_launch / launch_s / 1e9
@@ -381,7 +474,8 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
+        "dtype": "bf16",
+        "arithmetic": ARITHMETIC,
         "data": "synthetic (seeded logitfill_amd.synth: K~N(0,1)*LogNormal channel scale + outliers, V,Q~N)",
         "config": {"workload": f"{args.config}: packed decode attention, {layers} layers x batch {B}, "
                                f"{n_q}q/{n_kv}kv heads, D {D}, {context_text(cfg)}, target_bit {cfg['target_bit']}",
@@ -393,11 +487,15 @@ def main():
         "wall_ms_per_step": round(wall_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(args.config) if args.layers in (None, cfg["layers"]) else None},
+                     "traffic": measured_traffic(args.config) if args.layers in (None, cfg["layers"]) else None,
+                     "timed": "HIP events on the launch stream around every layer's decode kernel + split "
+                              "merge; achieved = algorithmic bytes per layer-step / that time"},
     }
     if not args.no_dense and cfg["pages"] is not None:
         print("[bench] bf16 dense comparator ...", file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
         dense_us, dense_bytes = time_dense(cfg, max(args.steps, 10), args.warmup)
+        legs["dense"] = round(time.perf_counter() - t0, 2)
         result["dense_bf16"] = {
             "what": "lf_dense_decode: BF16 dense split-K MFMA decode over the uncompressed K/V cache of the "
                     "same shape (history + residual + new token), synthetic bf16 data",
@@ -410,27 +508,18 @@ def main():
         }
     if not args.no_compress:
         print("[bench] page compress (config 3) ...", file=sys.stderr, flush=True)
-        comp = {}
-        for tb in (2.5, 3.0, 4.0):
-            us_c, us_c_layer, ph, rd, wr = time_compress(tb, 10, 2)
-            comp[f"target_{tb}"] = {"us_per_pass": round(us_c, 1), "page_heads": ph,
-                                    "pages_per_s": round(ph / us_c * 1e6), "gbs": round((rd + wr) / us_c / 1e3, 1),
-                                    "hbm_frac": round((rd + wr) / us_c / 1e3 / HBM_PEAK_GBS, 4),
-                                    "bytes_read": rd, "bytes_written": wr,
-                                    "us_per_pass_one_launch_per_layer": round(us_c_layer, 1)}
-        result["compress_c3"] = {
-            "what": "BASELINE config 3: 64 sequences x 1 page x 4 kv heads x 28 layers, bf16 K/V from the "
-                    "config-0 distributions; us_per_pass = one lf_pack_pages_multi launch for the 28 layers (a "
-                    "deferring manager's end-of-step flush), us_per_pass_one_launch_per_layer = 28 lf_pack_pages "
-                    "launches; pages_per_s counts page-heads",
-            **comp}
+        t0 = time.perf_counter()
+        result["compress_c3"] = compress_record()
+        legs["compress"] = round(time.perf_counter() - t0, 2)
     if not args.no_extra and args.config == "c2" and args.layers is None:
         extra = {}
         for name, n_layers in (("c2_k4", None), ("c1", None), ("c4", 8)):
             c = dict(synth.CONFIGS[name])
             nl = n_layers or c["layers"]
             print(f"[bench] {name} ({nl} layers) ...", file=sys.stderr, flush=True)
+            t0 = time.perf_counter()
             us_x, bytes_x, pay_x, _ = decode_point(c, nl, 10, 2, kernel, None, dev)
+            legs[name] = round(time.perf_counter() - t0, 2)
             extra[name] = {"workload": f"{c['layers']}-layer model shape timed on {nl} distinct layers, batch "
                                        f"{c['batch']}, {c['n_q']}q/{c['n_kv']}kv heads, {context_text(c)}, "
                                        f"target_bit {c['target_bit']}",
@@ -441,7 +530,14 @@ def main():
         result["other_configs"] = extra
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seqs)
+        legs["cpu_baseline"] = round(time.perf_counter() - t0, 2)
+        if not args.no_compress:
+            t0 = time.perf_counter()
+            result["cpu_baseline_compress"] = cpu_baseline_compress(2.5)
+            legs["cpu_baseline_compress"] = round(time.perf_counter() - t0, 2)
+    result["leg_wall_s"] = legs
     print(json.dumps(result), flush=True)
 
 

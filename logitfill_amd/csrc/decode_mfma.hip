@@ -51,6 +51,7 @@ constexpr int kD = 128;
 constexpr int kPage = 128;
 constexpr int kMaxDma = 8;    // 16-byte DMA instructions per wave per page (<= 2048 chunks)
 constexpr int kMaxKsDma = 4;  // 4-byte Key scale/min DMA instructions per wave per page
+constexpr int kMaxKSteps = 16; // K-steps of a page: at most 4 per tier (128 channels)
 constexpr float kLazyRescale = 8.f;  // log2-domain headroom before the running max moves
 constexpr int kRawbVs = 0;    // rest buffer: Value scale [128] fp16
 constexpr int kRawbVm = 256;  //              Value min [128] fp16
@@ -81,7 +82,6 @@ struct MfmaLayout {
     int ck_v16;          // prepared: [128][w16p] fp16 Key fp16 tier, zero padded (after Qs), one spare dword
     int ck_bytes;
     int off_qperm;       // [nb][8 heads][8] fp32: q * scaling*log2e per slot (0 for padding)
-    int off_tt;          // int16 tier table of this kv head (ranks -> channel ids), tiers back to back
     int off_small;       // alpha [waves][8], wave m/l/mid [waves][3][8]
     int slot_bytes;      // one page slot: Key-code buffer, then rest buffer
     int off_ck;          // the prepared buffer
@@ -773,41 +773,68 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         const uint32_t raw_lds = lds_addr(smem) + y.off_raw;  // LDS address of page slot 0
         dma_page(ds, raw_lds, z, pbeg, wave);
 
-        // ---- q (scaled into the log2 domain) and this head's tier table ----
-        int16_t* tt = reinterpret_cast<int16_t*>(smem + y.off_tt);
-        int tt_off[4];
-        tt_off[0] = 0;
-        for (int t = 1; t < 4; ++t) tt_off[t] = tt_off[t - 1] + L.k_width[t - 1];
-        load_q(p, b, h, qlin, tid);
-        for (int e = tid; e < tt_off[3] + L.k_width[3]; e += kThreads) {
-            const int t = e >= tt_off[3] ? 3 : e >= tt_off[2] ? 2 : e >= tt_off[1] ? 1 : 0;
-            const int j = e - sel4(tt_off, t);
-            tt[e] = j < sel4(L.tier_count, t)[h] ? static_cast<int16_t>(sel4(L.tier_index, t)[h * sel4(L.k_width, t) + j])
-                                                 : int16_t(-1);
-        }
-        __syncthreads();
-        // q permuted into slot order (0 for padding slots and heads >= g), integer tiers only.
-        // The fp16 tier's Qs is this q (hi / lo) on every page: set once in the prepared buffer,
-        // as are the zero Qs rows of heads >= g in the integer tiers.
-        for (int e = tid; e < y.nb * 64; e += kThreads) {
-            const int gb = e >> 6, n = (e >> 3) & 7, pos = e & 7;
-            const int tier = gb >= 4 * y.kfirst[3] ? 3 : gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
+        // ---- q permuted into slot order ----
+        // K-step i of the layout holds blocks 4i .. 4i+3, one per wave: wave w's lane (n, pos)
+        // takes slot pos of block 4i + w for head n.  The slot's channel comes from the tier
+        // table in global memory (no LDS staging) and q is gathered from global memory the
+        // same way, so the whole set-up is two rounds of loads that overlap the first page's
+        // DMA; nothing here waits for that DMA (the page loop's first barrier does).  Integer
+        // tiers go to qperm (0 for padding slots and heads >= g); the fp16 tier's Qs (plain q,
+        // hi / lo) is written once into the prepared buffer, which no page rewrites.
+        {
+            // Thread tid owns block gb = tid / 4 (K-step gb / 4) for heads 2 (tid % 4) and
+            // 2 (tid % 4) + 1, all 8 slot positions: the slots' channels come from the tier table
+            // in global memory and q is gathered from global memory -- two rounds of loads that
+            // overlap the first page's DMA (nothing here waits for it; the page loop's first
+            // barrier does).  Integer tiers go to qperm (0 for padding slots and heads >= g);
+            // the fp16 tier's Qs (plain q, hi / lo) goes into the prepared buffer, which no page
+            // rewrites; Qs rows of heads >= g start at 0.
+            const int ks = z.kst0 + z.kst1 + z.kst2 + z.kst3;
+            const int gb = tid >> 2, n0 = 2 * (tid & 3);
+            const int i = gb >> 2;
+            const bool own = i < ks;
+            const int tier = i >= z.kf3 ? 3 : i >= z.kf2 ? 2 : i >= z.kf1 ? 1 : 0;
             const int lb = gb - 4 * sel4(y.kfirst, tier);
-            float v = 0.f;
-            if (block_live(L, tier, lb)) {
+            const bool live = own && block_live(L, tier, lb);
+            const int width = sel4(L.k_width, tier);
+            const int32_t* tix = sel4(L.tier_index, tier);
+            const int count = live ? sel4(L.tier_count, tier)[h] : 0;
+            int chan[8];
+#pragma unroll
+            for (int pos = 0; pos < 8; ++pos) {
                 const int j = block_slot(tier, lb, pos);
-                if (j < sel4(L.k_width, tier)) {
-                    const int c = tt[sel4(tt_off, tier) + j];
-                    if (c >= 0) v = qlin[n * kD + c];
-                }
+                chan[pos] = live && j < count ? tix[h * width + j] : -1;
             }
-            if (gb < y.nb_int) qperm[e] = v;
-            if (gb >= y.nb_int || n >= g) {
-                const _Float16 hv = static_cast<_Float16>(v);
-                const _Float16 lv = static_cast<_Float16>(v - static_cast<float>(hv));
-                _Float16* qs = reinterpret_cast<_Float16*>(ck + kCkQs);
-                qs[(gb * 16 + n) * 8 + pos] = hv;
-                qs[(gb * 16 + 8 + n) * 8 + pos] = lv;
+            float qv[2][8];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int n = n0 + r;
+                const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD;
+#pragma unroll
+                for (int pos = 0; pos < 8; ++pos)
+                    qv[r][pos] = chan[pos] >= 0 && n < g ? load_as_f32(A.query, qrow + chan[pos], A.q_dtype) * p.qscale : 0.f;
+            }
+            if (own) {
+                _Float16* qs16 = reinterpret_cast<_Float16*>(ck + kCkQs);
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const int n = n0 + r;
+                    if (i < z.kf3) {
+                        float4* dst = reinterpret_cast<float4*>(qperm + (gb * 8 + n) * 8);
+                        dst[0] = float4{qv[r][0], qv[r][1], qv[r][2], qv[r][3]};
+                        dst[1] = float4{qv[r][4], qv[r][5], qv[r][6], qv[r][7]};
+                    }
+                    if (i >= z.kf3 || n >= g) {
+                        half8 hi, lo;
+#pragma unroll
+                        for (int pos = 0; pos < 8; ++pos) {
+                            hi[pos] = static_cast<_Float16>(qv[r][pos]);
+                            lo[pos] = static_cast<_Float16>(qv[r][pos] - static_cast<float>(hi[pos]));
+                        }
+                        *reinterpret_cast<half8*>(qs16 + (gb * 16 + n) * 8) = hi;
+                        *reinterpret_cast<half8*>(qs16 + (gb * 16 + 8 + n) * 8) = lo;
+                    }
+                }
             }
         }
         const int w16 = L.k_width[3];
@@ -1024,51 +1051,102 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         // ---- residual (kind 1, 2): the tail page and the new token (at most page_size tokens) ----
         // VALU: wave w scores tokens 32w..32w+31 (lane % 32 = token, lane / 32 = channel half;
         // q read as float4 from LDS), then accumulates them into channels 2*lane, 2*lane+1.
-        // One pass, so each wave's max is final.  Every global load of a phase is issued
-        // before its first use.
+        // One pass, so each wave's max is final.  For 2-byte residual and new-token rows every
+        // global load goes out in one round, before the tail length is known: q (into LDS),
+        // the tail length, the lane's tail rows read for every row the residual buffer holds
+        // (rows at or past the tail length are then ignored) and the new token's row.
         const int rw = kind == 2 ? wave + kWaves : wave;  // partial slot
-        load_q(p, b, h, qlin, tid);
-        __syncthreads();
-        const int tl = A.tail_len[b];
-        const int n_res = tl + (A.k_new != nullptr ? 1 : 0);
+        const int cap = min(A.tail_cap, kPage);
+        const int64_t bh = static_cast<int64_t>(b) * L.n_kv + h;
         const int t = 32 * wave + (lane & 31);
         const int ch0 = 64 * (lane >> 5);
-        const bool act = t < n_res;
-        float s[8];
+        const bool has_new = A.k_new != nullptr;
+        const bool two_byte = A.tail_dtype != LF_FP32 && (!has_new || A.new_dtype != LF_FP32);
+        load_q(p, b, h, qlin, tid);
+        const int tl = min(max(A.tail_len[b], 0), min(cap, kPage - 1));
+        float kv[64];
+        float v0[32], v1[32];
+        if (two_byte) {
+            uint4 kt[8], kn[8];
+            uint32_t vt[32], vn = 0;
+            const uint16_t* tk = static_cast<const uint16_t*>(A.tail_k) + (bh * A.tail_cap + t) * kD + ch0;
+            const uint16_t* tv = static_cast<const uint16_t*>(A.tail_v) + bh * A.tail_cap * kD + 2 * lane;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s[i] = 0.f;
-        if (act) {
-            const void* kp = t < tl ? A.tail_k : A.k_new;
-            const int kdt = t < tl ? A.tail_dtype : A.new_dtype;
-            const int64_t kbase = (t < tl ? ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap + t) * kD
-                                          : (static_cast<int64_t>(b) * L.n_kv + h) * kD) + ch0;
-            float kv[64];
-            if (kdt != LF_FP32) {
-                uint4 raw[8];
+            for (int u = 0; u < 8; ++u) kt[u] = t < cap ? *reinterpret_cast<const uint4*>(tk + 8 * u) : uint4{0, 0, 0, 0};
 #pragma unroll
-                for (int u = 0; u < 8; ++u) raw[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(kp) + kbase + 8 * u);
+            for (int k = 0; k < 32; ++k)
+                vt[k] = 32 * wave + k < cap ? *reinterpret_cast<const uint32_t*>(tv + static_cast<int64_t>(32 * wave + k) * kD) : 0u;
+            if (has_new) {
+                const uint16_t* nk = static_cast<const uint16_t*>(A.k_new) + bh * kD + ch0;
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const uint16_t x = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
-                        kv[8 * u + k] = kdt == LF_BF16 ? bf16_to_f32(x) : f16_to_f32(x);
-                    }
-                }
+                for (int u = 0; u < 8; ++u) kn[u] = *reinterpret_cast<const uint4*>(nk + 8 * u);
+                vn = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(A.v_new) + bh * kD + 2 * lane);
             } else {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) kn[u] = uint4{0, 0, 0, 0};
+            }
+            // Token t is the lane's tail row when t < tl, the new token when t == tl.
+            const bool from_new = t >= tl;
+            const int kdt = from_new ? A.new_dtype : A.tail_dtype;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint4 r = from_new ? kn[u] : kt[u];
+                const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint16_t x = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+                    kv[8 * u + k] = kdt == LF_BF16 ? bf16_to_f32(x) : f16_to_f32(x);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const int tk2 = 32 * wave + k;
+                const uint32_t r = tk2 < tl ? vt[k] : (tk2 == tl ? vn : 0u);
+                const int dt = tk2 < tl ? A.tail_dtype : A.new_dtype;
+                const uint16_t lo = static_cast<uint16_t>(r & 0xffffu), hi = static_cast<uint16_t>(r >> 16);
+                v0[k] = dt == LF_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+                v1[k] = dt == LF_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+            }
+        } else {
+            // float32 rows: the tail length first, then the rows it selects
+            const bool in_tail = t < tl;
+            const void* kp = in_tail ? A.tail_k : A.k_new;
+            const int kdt = in_tail ? A.tail_dtype : A.new_dtype;
+            const int64_t kbase = (in_tail ? (bh * A.tail_cap + t) * kD : bh * kD) + ch0;
+#pragma unroll
+            for (int i = 0; i < 64; ++i) kv[i] = 0.f;
+            if (t < tl + (has_new ? 1 : 0)) {
 #pragma unroll
                 for (int u = 0; u < 8; ++u) load8_as_f32(kp, kbase + 8 * u, kdt, kv + 8 * u);
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4* q4 = reinterpret_cast<const float4*>(qlin + i * kD + ch0);
-#pragma unroll
-                for (int c4 = 0; c4 < 16; ++c4) {
-                    const float4 q = q4[c4];
-                    s[i] = fmaf(q.x, kv[4 * c4], fmaf(q.y, kv[4 * c4 + 1], fmaf(q.z, kv[4 * c4 + 2], fmaf(q.w, kv[4 * c4 + 3], s[i]))));
+            for (int k = 0; k < 32; ++k) {
+                const int tk2 = 32 * wave + k;
+                v0[k] = 0.f;
+                v1[k] = 0.f;
+                if (tk2 < tl) {
+                    v0[k] = load_as_f32(A.tail_v, (bh * A.tail_cap + tk2) * kD + 2 * lane, A.tail_dtype);
+                    v1[k] = load_as_f32(A.tail_v, (bh * A.tail_cap + tk2) * kD + 2 * lane + 1, A.tail_dtype);
+                } else if (tk2 == tl && has_new) {
+                    v0[k] = load_as_f32(A.v_new, bh * kD + 2 * lane, A.new_dtype);
+                    v1[k] = load_as_f32(A.v_new, bh * kD + 2 * lane + 1, A.new_dtype);
                 }
             }
+        }
+        const int n_res = tl + (has_new ? 1 : 0);
+        const bool act = t < n_res;
+        __syncthreads();  // q in LDS
+        float s[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4* q4 = reinterpret_cast<const float4*>(qlin + i * kD + ch0);
+            float acc = 0.f;
+#pragma unroll
+            for (int c4 = 0; c4 < 16; ++c4) {
+                const float4 q = q4[c4];
+                acc = fmaf(q.x, kv[4 * c4], fmaf(q.y, kv[4 * c4 + 1], fmaf(q.z, kv[4 * c4 + 2], fmaf(q.w, kv[4 * c4 + 3], acc))));
+            }
+            s[i] = acc;
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) s[i] += __shfl_xor(s[i], 32, kWave);
@@ -1102,46 +1180,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             }
         }
         __builtin_amdgcn_wave_barrier();
-        const int cnt = max(0, min(32, n_res - 32 * wave));
-        const int64_t vrow0 = ((static_cast<int64_t>(b) * L.n_kv + h) * A.tail_cap) * kD;
-        const int64_t vnew = (static_cast<int64_t>(b) * L.n_kv + h) * kD;
-        float v0[32], v1[32];
-        if (A.tail_dtype != LF_FP32 && (A.v_new == nullptr || A.new_dtype != LF_FP32)) {
-            // 2-byte Values: one dword (channels 2*lane, 2*lane+1) per token, addresses chosen
-            // without branches so all 32 loads are in flight together
-            uint32_t raw[32];
-#pragma unroll
-            for (int k = 0; k < 32; ++k) {
-                const int tk = 32 * wave + k;
-                const bool in_tail = tk < tl;
-                const uint16_t* base = static_cast<const uint16_t*>(in_tail ? A.tail_v : A.v_new);
-                const int64_t idx = (in_tail ? vrow0 + static_cast<int64_t>(tk) * kD : vnew) + 2 * lane;
-                raw[k] = k < cnt ? *reinterpret_cast<const uint32_t*>(base + idx) : 0u;
-            }
-#pragma unroll
-            for (int k = 0; k < 32; ++k) {
-                const int dt = 32 * wave + k < tl ? A.tail_dtype : A.new_dtype;
-                const uint16_t lo = static_cast<uint16_t>(raw[k] & 0xffffu), hi = static_cast<uint16_t>(raw[k] >> 16);
-                v0[k] = dt == LF_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
-                v1[k] = dt == LF_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 32; ++k) {
-                const int tk = 32 * wave + k;
-                v0[k] = 0.f;
-                v1[k] = 0.f;
-                if (k < cnt) {
-                    if (tk < tl) {
-                        v0[k] = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tk) * kD + 2 * lane, A.tail_dtype);
-                        v1[k] = load_as_f32(A.tail_v, vrow0 + static_cast<int64_t>(tk) * kD + 2 * lane + 1, A.tail_dtype);
-                    } else {
-                        v0[k] = load_as_f32(A.v_new, vnew + 2 * lane, A.new_dtype);
-                        v1[k] = load_as_f32(A.v_new, vnew + 2 * lane + 1, A.new_dtype);
-                    }
-                }
-            }
-        }
         float acc[2][8];
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
@@ -1211,6 +1249,7 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
         y.kfirst[t] = ks;
         ks += y.kst[t];
     }
+    if (ks > kMaxKSteps) return false;
     y.nb = 4 * ks;
     y.nb_int = 4 * (y.kst[0] + y.kst[1] + y.kst[2]);
     y.w16p = round_up(L.k_width[3], 8);
@@ -1239,8 +1278,6 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     int off = 0;
     y.off_qperm = off;
     off += y.nb_int * 64 * 4;
-    y.off_tt = off;
-    off += round_up(2 * (L.k_width[0] + L.k_width[1] + L.k_width[2] + L.k_width[3]), 16);
     y.off_small = off;
     off += (kWaves * 8 + 2 * kWaves * 3 * 8) * 4;  // alpha, wave partial statistics
     off = round_up(off, 16);
@@ -1262,7 +1299,10 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
     MfmaParams mp;
     mp.p = p;
     mp.k = UnpackBits{0x00C000C0u, 0x03000300u, 0x003C003Cu, 0x03C003C0u, 0x4C004C00u, 0x44004400u, 0x5C005C00u};
-    if (!plan_layout(p.L, p.g, mp.y)) {
+    // The residual pass reads 16-byte Key chunks and 4-byte Value pairs of the tail and new rows.
+    const bool rows_aligned = (p.A.tail_cap == 0 || (aligned(p.A.tail_k, 16) && aligned(p.A.tail_v, 4))) &&
+                              (!p.A.k_new || (aligned(p.A.k_new, 16) && aligned(p.A.v_new, 4)));
+    if (!rows_aligned || !plan_layout(p.L, p.g, mp.y)) {
         *handled = false;
         return LF_OK;
     }

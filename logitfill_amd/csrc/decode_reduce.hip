@@ -12,7 +12,8 @@ namespace lf {
 namespace {
 
 constexpr int kReduceLds = 2048;  // items whose weights are kept in LDS (more: recomputed per channel)
-constexpr int kFastItems = 16;    // up to this many items: one round of loads per thread, no LDS
+constexpr int kFastItems = 32;    // up to this many items: one round of loads per thread, no LDS
+                                  // (at most the 64 lanes of a wave)
 
 __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     __shared__ float w[kReduceLds];
@@ -28,37 +29,39 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     const int nw = blockDim.x / kWave;
 
     if (count <= kFastItems) {
-        // Every thread loads all items' (m, l) -- the same addresses across the workgroup --
-        // and its channels' o, all before the first use: one load latency per channel pass.
-        float m[kFastItems], l[kFastItems];
-#pragma unroll
-        for (int k = 0; k < kFastItems; ++k) {
-            m[k] = -__builtin_inff();
-            l[k] = 0.f;
-            if (k < count) {
-                const float* r = part_rec(p, first + k, h, i);
-                m[k] = r[D];
-                l[k] = r[D + 1];
-            }
+        // One round of loads: lane k of each wave loads item k's (m, l); every thread loads its
+        // channels' o of every item.  Each wave then forms the weights in-lane (max and sum by
+        // wave reductions) and broadcasts weight k from lane k -- no LDS, no barrier.
+        const int lane = tid & (kWave - 1);
+        float mk = -__builtin_inff(), lk = 0.f;
+        if (lane < count) {
+            const float* r = part_rec(p, first + lane, h, i);
+            mk = r[D];
+            lk = r[D + 1];
         }
-        for (int c = tid; c < D; c += blockDim.x) {
-            float o[kFastItems];
+        const int c0 = tid;
+        float o[kFastItems];
 #pragma unroll
-            for (int k = 0; k < kFastItems; ++k) o[k] = k < count ? part_rec(p, first + k, h, i)[c] : 0.f;
-            float M = m[0];
+        for (int k = 0; k < kFastItems; ++k) o[k] = k < count && c0 < D ? part_rec(p, first + k, h, i)[c0] : 0.f;
+        const float M = wave_max(mk);
+        const float wk = M == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(mk - M);  // 0 past count
+        const float lsum = wave_sum(wk * lk);
+        float osum = 0.f;
 #pragma unroll
-            for (int k = 1; k < kFastItems; ++k) M = fmaxf(M, m[k]);
-            float lsum = 0.f, osum = 0.f;
-            if (M != -__builtin_inff()) {
+        for (int k = 0; k < kFastItems; ++k) osum = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), o[k], osum);
+        if (c0 < D)
+            store_from_f32(p.A.out, (static_cast<int64_t>(b) * p.A.n_q + h * g + i) * D + c0, p.A.out_dtype,
+                           lsum > 0.f ? osum / lsum : 0.f);
+        // channels past the first blockDim.x (head_dim 512): the same with the weights kept
+        for (int c = c0 + blockDim.x; c < D; c += blockDim.x) {
+            float acc = 0.f;
 #pragma unroll
-                for (int k = 0; k < kFastItems; ++k) {
-                    const float wk = __builtin_amdgcn_exp2f(m[k] - M);  // 0 for the items past count
-                    lsum = fmaf(wk, l[k], lsum);
-                    osum = fmaf(wk, o[k], osum);
-                }
+            for (int k = 0; k < kFastItems; ++k) {
+                const float ok = k < count ? part_rec(p, first + k, h, i)[c] : 0.f;
+                acc = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)), ok, acc);
             }
             store_from_f32(p.A.out, (static_cast<int64_t>(b) * p.A.n_q + h * g + i) * D + c, p.A.out_dtype,
-                           lsum > 0.f ? osum / lsum : 0.f);
+                           lsum > 0.f ? acc / lsum : 0.f);
         }
         return;
     }
