@@ -44,6 +44,7 @@ def parse_args():
     p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the other decode configs (c2 at target 3.0, c1, c4) reported beside the headline")
+    p.add_argument("--no-step", action="store_true", help="skip the full decode-step timing (attention + commit)")
     p.add_argument("--compress-only", action="store_true",
                    help="only time the config-3 page compress (one JSON line; for profiling runs)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -101,7 +102,7 @@ def algorithmic_bytes(widths, words, n_kv, n_q, D, H, R1, k_group=128, v_group=1
     return total, n_kv * H * payload_tok
 
 
-def build_state(cfg, layers, dev):
+def build_state(cfg, layers, dev, capacity_pages=None):
     import torch
 
     from logitfill_amd import synth
@@ -111,7 +112,7 @@ def build_state(cfg, layers, dev):
     pages, resid, tb = seq_lengths(cfg)
     levels = [synth.sample_tier_levels(n_kv, D, tb, seed=layer) for layer in range(layers)]
     mgr = PackedKVManager(levels, n_q, n_kv, D, 128, 128, 128, 2, dev, batch_size=B,
-                          capacity_tokens=max(pages) * 128)
+                          capacity_tokens=(capacity_pages or max(pages)) * 128)
     inputs = []
     T = max(pages) * 128 + 128  # every sequence's residual slice below is 127 tokens long
     for layer in range(layers):
@@ -197,6 +198,96 @@ def decode_point(cfg, layers, steps, warmup, kernel, pages_per_split, dev):
     del mgr, inputs
     torch.cuda.empty_cache()
     return ms_step * 1e3 / layers, tot / layers, pay / layers, wall_ms
+
+
+def time_real_step(cfg, layers, steps, dev):
+    """A full decode step through the drop-in API, as a model's attention layers drive it
+    (reference qwen2_attention.py:234-255): for every layer ``packed_attention`` over the packed
+    history, the residual page and the new token, then ``commit`` of the new token; after the
+    last layer ``flush_pending`` packs every layer's completed page in one launch (the manager
+    defers flushes).  The residual starts ``steps // 2`` tokens short of a full page, so the
+    timed steps cross one page boundary (a flush and a new decode plan).  Returns (GPU us per
+    step from HIP events on the stream, host wall us per step, enqueue-only host us per step,
+    steps, pages flushed per layer)."""
+    import torch
+
+    from logitfill_amd.packed.reference import packed_attention
+
+    B = cfg["batch"]
+    pages, _, _ = seq_lengths(cfg)
+    resid = [128 - steps // 2] * B
+    c = dict(cfg, residual=resid[0])
+    mgr, inputs = build_state(c, layers, dev, capacity_pages=max(pages) + 2)
+    mgr.defer_flush = True
+    scaling = mgr.head_dim ** -0.5
+    ins = [(q[:, :, None], kn[:, :, None], vn[:, :, None]) for q, kn, vn in inputs]
+
+    def one_step():
+        for layer, (q, kn, vn) in enumerate(ins):
+            packed_attention(mgr, layer, q, kn, vn, scaling)
+            mgr.commit(layer, kn, vn)
+        mgr.flush_pending()
+
+    one_step()  # warm-up: plans, workspace, pinned staging buffers
+    torch.cuda.synchronize(dev)
+    hist0 = mgr.layers[0].hist_len
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps - 1):
+        one_step()
+    end.record(stream)
+    t_enq = time.perf_counter() - t0
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    flushed = (mgr.layers[0].hist_len - hist0) // 128
+    n = steps - 1
+    del mgr, inputs, ins
+    torch.cuda.empty_cache()
+    return start.elapsed_time(end) * 1e3 / n, wall * 1e6 / n, t_enq * 1e6 / n, n, flushed
+
+
+def time_graph_step(cfg, layers, replays, dev):
+    """The same decode step (every layer's packed_attention, then the one-token commit, which
+    appends on the device) captured once in a HIP graph and replayed ``replays`` times, as a
+    serving loop launches it; the residual starts at 20 tokens so no replay fills a page.
+    Returns GPU us per step (HIP events around the replays)."""
+    import torch
+
+    from logitfill_amd.packed.reference import packed_attention
+
+    c = dict(cfg, residual=20)
+    mgr, inputs = build_state(c, layers, dev)
+    scaling = mgr.head_dim ** -0.5
+    ins = [(q[:, :, None], kn[:, :, None], vn[:, :, None]) for q, kn, vn in inputs]
+
+    def one_step():
+        for layer, (q, kn, vn) in enumerate(ins):
+            packed_attention(mgr, layer, q, kn, vn, scaling)
+            mgr.commit(layer, kn, vn)
+
+    one_step()
+    torch.cuda.synchronize(dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            one_step()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    del graph, mgr, inputs, ins
+    torch.cuda.empty_cache()
+    return start.elapsed_time(end) * 1e3 / replays
 
 
 def time_dense(cfg, steps, warmup):
@@ -528,6 +619,25 @@ def main():
                            "hbm_frac": round(bytes_x / us_x / 1e3 / HBM_PEAK_GBS, 4),
                            "payload_gbs": round(pay_x / us_x / 1e3, 1)}
         result["other_configs"] = extra
+    if not args.no_step and args.layers is None:
+        for name in (args.config, "c1") if args.config != "c1" else (args.config,):
+            c = dict(synth.CONFIGS[name])
+            print(f"[bench] real decode step ({name}) ...", file=sys.stderr, flush=True)
+            t0 = time.perf_counter()
+            gpu_us, wall_us, enq_us, n, flushed = time_real_step(c, c["layers"], 40, dev)
+            legs[f"step_{name}"] = round(time.perf_counter() - t0, 2)
+            result.setdefault("decode_step", {})[name] = {
+                "what": f"{c['layers']} layers x (packed_attention + commit) + flush_pending per step, batch "
+                        f"{c['batch']}, {c['n_q']}q/{c['n_kv']}kv, {c['pages']} pages + a residual that fills a page "
+                        "mid-run (deferred flush: one lf_pack_pages_multi launch for all layers), drop-in API",
+                "us_per_step": round(gpu_us, 1), "us_per_layer": round(gpu_us / c["layers"], 2),
+                "host_wall_us_per_step": round(wall_us, 1), "host_enqueue_us_per_step": round(enq_us, 1),
+                "steps": n, "pages_flushed_per_layer": flushed}
+            t0 = time.perf_counter()
+            g_us = time_graph_step(c, c["layers"], 60, dev)
+            legs[f"graph_step_{name}"] = round(time.perf_counter() - t0, 2)
+            result["decode_step"][name]["graph_us_per_step"] = round(g_us, 1)
+            result["decode_step"][name]["graph_us_per_layer"] = round(g_us / c["layers"], 2)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         t0 = time.perf_counter()

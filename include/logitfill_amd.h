@@ -247,6 +247,20 @@ int32_t lf_dense_decode(const void* query, const void* k, const void* v,
                         void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Single-token append to the residual pages (the one-token commit of a decode step;
+ * reference src/logitfill/packed/cache.py:48-62 while the page is not full).  For every
+ * sequence b: the new Key and Value rows k_new / v_new [batch][n_kv][head_dim] (dtype
+ * ``new_dtype``) are written, converted to ``tail_dtype``, as row tail_len[b] of tail_k / tail_v
+ * [batch][n_kv][tail_cap][head_dim], and the DEVICE int32 tail_len[b] is advanced by one.  A
+ * sequence whose residual page is already full (tail_len[b] >= tail_cap) is left unchanged:
+ * full pages are packed (lf_pack_pages) and their length reset before the next append.  The
+ * write position never leaves the device, so a decode step that appends needs no host copy.
+ */
+int32_t lf_append_token(void* tail_k, void* tail_v, int32_t tail_dtype, int32_t tail_cap, int32_t* tail_len,
+                        const void* k_new, const void* v_new, int32_t new_dtype, int32_t batch, int32_t n_kv,
+                        int32_t head_dim, void* stream);
+
+/*
  * Layout helpers on the device (building blocks of the page packers, for callers of the
  * reference's layout module).  All arrays are contiguous device memory.
  *

@@ -109,6 +109,8 @@ _SIGNATURES = {
     "lf_pack_ints": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p]),
     "lf_unpack_ints": (c_int32, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "lf_decode_attention_noalloc": (c_int32, [POINTER(PackedLayer), POINTER(DecodeArgs), c_void_p]),
+    "lf_append_token": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
+                                  c_int32, c_int32, c_int32, c_void_p]),
     "lf_noalloc_scratch_bytes": (c_int64, []),
 }
 
@@ -160,3 +162,21 @@ def current_stream_ptr(device) -> int:
     import torch
 
     return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def upload(data, dtype, device):
+    """Copy host data (a sequence of numbers, or raw bytes for ``torch.uint8``) to a new device
+    tensor without synchronising the host: the data is staged in pinned host memory and copied
+    asynchronously on the current stream.  torch's pinned-memory allocator keeps the staging
+    block until that copy has run, so the caller may reuse or drop its data at once."""
+    import torch
+
+    if isinstance(data, (bytes, bytearray, memoryview)):
+        host = torch.frombuffer(bytearray(data), dtype=torch.uint8)
+    else:
+        host = torch.as_tensor(data, dtype=dtype)
+    staged = torch.empty(host.shape, dtype=host.dtype, pin_memory=True)
+    staged.copy_(host)
+    out = torch.empty(host.shape, dtype=host.dtype, device=device)
+    out.copy_(staged, non_blocking=True)
+    return out

@@ -24,6 +24,9 @@ int launch_asymmetric_codes(const void* x, int dtype, int64_t n_groups, int grou
 int launch_pack_ints(const int32_t* codes, int64_t rows, int n, int bits, int32_t* words, hipStream_t stream);
 int launch_unpack_ints(const int32_t* words, int64_t rows, int n_words, int count, int bits, int32_t* codes,
                        hipStream_t stream);
+int launch_append_token(void* tail_k, void* tail_v, int tail_dtype, int tail_cap, int32_t* tail_len,
+                        const void* k_new, const void* v_new, int new_dtype, int batch, int n_kv, int head_dim,
+                        hipStream_t stream);
 }  // namespace lf
 
 namespace {
@@ -247,6 +250,16 @@ int32_t lf_dense_decode(const void* query, const void* k, const void* v, int32_t
     return lf::launch_dense_decode(query, k, v, batch, n_q, n_kv, head_dim, tokens, kv_stride_b, kv_stride_h,
                                    kv_stride_t, scaling, out, tokens_per_split, workspace,
                                    static_cast<hipStream_t>(stream));
+}
+
+int32_t lf_append_token(void* tail_k, void* tail_v, int32_t tail_dtype, int32_t tail_cap, int32_t* tail_len,
+                        const void* k_new, const void* v_new, int32_t new_dtype, int32_t batch, int32_t n_kv,
+                        int32_t head_dim, void* stream) {
+    if (!valid_dtype(tail_dtype) || !valid_dtype(new_dtype)) return LF_E_DTYPE;
+    if (batch <= 0 || n_kv <= 0 || head_dim <= 0 || tail_cap <= 0) return LF_E_SHAPE;
+    if (!tail_k || !tail_v || !tail_len || !k_new || !v_new) return LF_E_NULL;
+    return lf::launch_append_token(tail_k, tail_v, tail_dtype, tail_cap, tail_len, k_new, v_new, new_dtype, batch,
+                                   n_kv, head_dim, static_cast<hipStream_t>(stream));
 }
 
 int32_t lf_asymmetric_codes(const void* x, int32_t dtype, int64_t n_groups, int32_t group, int32_t bits,

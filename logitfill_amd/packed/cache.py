@@ -207,12 +207,10 @@ class _LayerStore:
         return self._tail_k, self._tail_v
 
     def tail_len_device(self) -> torch.Tensor:
-        """int32 ``[B]`` residual lengths on the device (uploaded when they changed)."""
-        if self._tail_len_dev is None:
-            self._tail_len_dev = torch.zeros(self.batch, dtype=torch.int32, device=self.device)
-            self._tail_dirty = True
-        if self._tail_dirty:
-            self._tail_len_dev.copy_(torch.tensor(self.tail_lens, dtype=torch.int32), non_blocking=False)
+        """int32 ``[B]`` residual lengths on the device, re-uploaded (asynchronously, from pinned
+        memory, on the current stream) after they change."""
+        if self._tail_dirty or self._tail_len_dev is None:
+            self._tail_len_dev = _native.upload(self.tail_lens, torch.int32, self.device)
             self._tail_dirty = False
         return self._tail_len_dev
 
@@ -248,13 +246,18 @@ class _LayerStore:
             raise ValueError(f"expected [{self.batch}, {self.n_kv}, T, {self.head_dim}], got {tuple(key.shape)}")
         if not key.is_cuda or not value.is_cuda:
             raise RuntimeError("logitfill_amd keeps the packed cache on a ROCm device (there is no CPU path)")
+        P = self.page_size
+        if (T == 1 and lengths is None and self._tail_k is not None and not self._pending
+                and max(self.tail_lens) + 1 < P and key.dtype == value.dtype
+                and key.is_contiguous() and value.is_contiguous()):
+            self._append_one(key, value)
+            return
         lens = [T] * B if lengths is None else [int(x) for x in lengths]
         if len(lens) != B or min(lens) < 0 or max(lens) > T:
             raise ValueError("lengths must give 0 <= length <= T for every sequence")
         if max(lens) == 0:
             return
         self.flush()
-        P = self.page_size
         if self._tail_k is None:
             self._tail_k = torch.zeros(B, H, P, D, dtype=key.dtype, device=self.device)
             self._tail_v = torch.zeros(B, H, P, D, dtype=value.dtype, device=self.device)
@@ -296,7 +299,7 @@ class _LayerStore:
                 self._tail_k[:, :, tl:tl + n1].copy_(key[:, :, :n1])
                 self._tail_v[:, :, tl:tl + n1].copy_(value[:, :, :n1])
             else:
-                idx = torch.tensor(bs, device=self.device)
+                idx = _native.upload(bs, torch.int64, self.device)
                 self._tail_k[idx, :, tl:tl + n1] = key[idx, :, :n1]
                 self._tail_v[idx, :, tl:tl + n1] = value[idx, :, :n1]
         # 2) pack full pages in place -- or, for a deferring store on a step that only completes
@@ -322,6 +325,19 @@ class _LayerStore:
         self.hist_lens = [p * P for p in hist_pages]
         self.tail_lens = new_tail
         self._tail_dirty = True
+
+    def _append_one(self, key: torch.Tensor, value: torch.Tensor) -> None:
+        """One token per sequence into residual pages that stay below full: ``lf_append_token``
+        writes the rows at the device-side lengths and advances them, so nothing is uploaded;
+        the host copy of the lengths advances in step."""
+        tail_len = self.tail_len_device()
+        tk, tv = self._tail_k, self._tail_v
+        st = _native.load().lf_append_token(
+            tk.data_ptr(), tv.data_ptr(), _native.dtype_code(tk.dtype), int(tk.shape[2]), tail_len.data_ptr(),
+            key.data_ptr(), value.data_ptr(), _native.dtype_code(key.dtype), self.batch, self.n_kv, self.head_dim,
+            _native.current_stream_ptr(self.device))
+        _native.check(st, "lf_append_token")
+        self.tail_lens = [t + 1 for t in self.tail_lens]
 
     @property
     def pending(self) -> list[tuple[int, int]]:
@@ -351,7 +367,7 @@ class _LayerStore:
             v_src = v_src.contiguous()
         if k_src.stride() != v_src.stride():
             k_src, v_src = k_src.contiguous(), v_src.contiguous()
-        jobs_dev = torch.tensor(jobs, dtype=torch.int32).to(self.device)
+        jobs_dev = _native.upload([v for job in jobs for v in job], torch.int32, self.device)
         st = _native.load().lf_pack_pages(
             self.layer_struct(), k_src.data_ptr(), v_src.data_ptr(), _native.dtype_code(k_src.dtype),
             k_src.stride(0), k_src.stride(1), k_src.stride(2), jobs_dev.data_ptr(), len(jobs),
@@ -477,10 +493,10 @@ class PackedKVManager:
             srcs[i] = _native.PackSource(tk.data_ptr(), tv.data_ptr(), tk.stride(0), tk.stride(1), tk.stride(2))
         st = _native.LF_E_UNSUPPORTED if len(dtypes) != 1 else None
         if st is None:
-            dev_structs = torch.frombuffer(bytearray(structs), dtype=torch.uint8).to(self.device)
-            dev_srcs = torch.frombuffer(bytearray(srcs), dtype=torch.uint8).to(self.device)
+            dev_structs = _native.upload(bytes(structs), torch.uint8, self.device)
+            dev_srcs = _native.upload(bytes(srcs), torch.uint8, self.device)
             jobs = [(i, b, 0, page) for i, layer in enumerate(todo) for b, page in layer._pending]
-            jobs_dev = torch.tensor(jobs, dtype=torch.int32).to(self.device)
+            jobs_dev = _native.upload([v for job in jobs for v in job], torch.int32, self.device)
             st = _native.load().lf_pack_pages_multi(
                 dev_structs.data_ptr(), structs, dev_srcs.data_ptr(), srcs, n, _native.dtype_code(dtypes.pop()),
                 jobs_dev.data_ptr(), len(jobs), _native.current_stream_ptr(self.device))

@@ -150,8 +150,8 @@ class DecodePlan:
             _native.check(n, "lf_plan_decode")
         self.key = (tuple(hist_pages), pages_per_split, residual_pages)
         self.n_work = int(n)
-        self.work = torch.tensor(list(work)[: 4 * n], dtype=torch.int32).to(device)
-        self.seq_work = torch.tensor(list(seq), dtype=torch.int32).to(device)
+        self.work = _native.upload(list(work)[: 4 * n], torch.int32, device)
+        self.seq_work = _native.upload(list(seq), torch.int32, device)
         self.pages_per_split = pages_per_split
 
 
@@ -303,7 +303,11 @@ def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torc
     """
     if not query.is_cuda:
         raise RuntimeError("logitfill_amd runs on ROCm devices only (there is no CPU path)")
-    reason = kernel_unsupported_reason(manager, int(query.shape[-2]))
+    q_len = int(query.shape[-2])
+    cache = manager.__dict__.setdefault("_lf_kernel_reason", {})  # the shape is fixed per manager
+    if q_len not in cache:
+        cache[q_len] = kernel_unsupported_reason(manager, q_len)
+    reason = cache[q_len]
     if reason is None:
         return _kernel_attention(manager, layer_idx, query, key_new, value_new, scaling)
     if os.environ.get("LOGITFILL_AMD_STRICT", "") == "1":

@@ -14,7 +14,7 @@ import torch
 from logitfill_amd import _native, synth
 from logitfill_amd.packed import PackedKVManager
 from logitfill_amd.packed.reference import packed_attention
-from tests.helpers import assert_history_equal, f32, oracle_store
+from tests.helpers import assert_decode_close, assert_history_equal, f32, oracle_store
 
 pytestmark = pytest.mark.gpu
 
@@ -156,3 +156,98 @@ def test_pack_pages_multi_rejects_other_shapes(gpu):
     for lay in m.layers:
         assert_history_equal(lay, 0, store)
     assert np.all([lay.pending == [] for lay in m.layers])
+
+
+@pytest.mark.parametrize("defer", [False, True])
+def test_device_append_path_matches_oracle(gpu, defer):
+    """One contiguous token per sequence per step -- the model's decode commit -- goes through
+    lf_append_token (rows written at the device-side residual lengths, which it advances; no
+    upload).  Batch 3 with ragged prefills, 140 steps across page flushes: every sequence's
+    history and residual equal the oracle store's, the device lengths equal the host's, and a
+    decode at the end matches the oracle (reference cache.py:48-90, reference.py:30-56)."""
+    from logitfill_amd.packed.reference import packed_attention
+    from oracle import attention as oatt
+
+    n_q, n_kv, D, B, steps = 4, 2, 128, 3, 140
+    lens = [120, 7, 64]
+    ds = [synth.make_layer(1, n_q, n_kv, D, 300, 2.5, seed=60 + b) for b in range(B)]
+    levels = ds[0].levels
+    m = PackedKVManager([levels], n_q, n_kv, D, 128, 128, 128, 2, gpu, batch_size=B, defer_flush=defer)
+    k0 = torch.zeros(B, n_kv, max(lens), D, dtype=torch.bfloat16)
+    v0 = torch.zeros_like(k0)
+    for b in range(B):
+        k0[b, :, :lens[b]] = ds[b].key[0, :, :lens[b]]
+        v0[b, :, :lens[b]] = ds[b].value[0, :, :lens[b]]
+    m.commit(0, k0.to(gpu), v0.to(gpu), lengths=lens)
+    keys = torch.stack([d.key[0] for d in ds])       # [B, n_kv, 300, D]
+    values = torch.stack([d.value[0] for d in ds])
+    appended = 0
+    for s in range(steps):
+        kt = torch.stack([keys[b, :, lens[b] + s] for b in range(B)])[:, :, None].contiguous().to(gpu)
+        vt = torch.stack([values[b, :, lens[b] + s] for b in range(B)])[:, :, None].contiguous().to(gpu)
+        before = list(m.layers[0].tail_lens)
+        m.commit(0, kt, vt)
+        if defer:
+            m.flush_pending()
+        appended += int(max(before) + 1 < 128 and not m.layers[0].pending)
+    layer = m.layers[0]
+    assert appended > 100  # most steps took the device append path
+    assert layer.tail_len_device().cpu().tolist() == layer.tail_lens
+    for b in range(B):
+        n = lens[b] + steps
+        store = oracle_store(levels, f32(keys[b, :, :n]), f32(values[b, :, :n]))
+        assert_history_equal(layer, b, store)
+    q = torch.randn(B, n_q, 1, D, generator=torch.Generator().manual_seed(3)).bfloat16().to(gpu) * D ** -0.5
+    kn = torch.randn(B, n_kv, 1, D, generator=torch.Generator().manual_seed(4)).bfloat16().to(gpu)
+    vn = torch.randn(B, n_kv, 1, D, generator=torch.Generator().manual_seed(5)).bfloat16().to(gpu)
+    out = packed_attention(m, 0, q, kn, vn, D ** -0.5)
+    for b in range(B):
+        n = lens[b] + steps
+        store = oracle_store(levels, f32(keys[b, :, :n]), f32(values[b, :, :n]))
+        ref = oatt.reference_attention(store, f32(q[b]), f32(kn[b]), f32(vn[b]), D ** -0.5, n_q, n_kv)
+        assert_decode_close(out[b, :, 0], ref[:, 0])
+
+
+def test_decode_step_replays_from_a_hip_graph(gpu):
+    """A decode step -- every layer's packed_attention then a one-token commit through
+    lf_append_token -- captured once in a HIP graph and replayed: each replay appends one more
+    token (positions live on the device) and its outputs equal, bit for bit, those of an eager
+    twin manager stepped with the same inputs; the program's own eager work and
+    synchronisations run between the replays."""
+    n_q, n_kv, D, B, L = 8, 2, 128, 2, 3
+    ds = [synth.make_layer(B, n_q, n_kv, D, 5 * 128 + 20, 2.5, seed=90 + i) for i in range(L)]
+    levels = [d.levels for d in ds]
+    mgrs = [PackedKVManager(levels, n_q, n_kv, D, 128, 128, 128, 2, gpu, batch_size=B) for _ in range(2)]
+    for m in mgrs:
+        for i, d in enumerate(ds):
+            m.commit(i, d.key.to(gpu), d.value.to(gpu))
+    ins = [(d.query[:, :, None].contiguous().to(gpu), d.key_new[:, :, None].contiguous().to(gpu),
+            d.value_new[:, :, None].contiguous().to(gpu)) for d in ds]
+
+    def step(m):
+        outs = []
+        for i, (q, kn, vn) in enumerate(ins):
+            outs.append(packed_attention(m, i, q, kn, vn, D ** -0.5))
+            m.commit(i, kn, vn)
+        return outs
+
+    eager, graphed = mgrs
+    step(graphed)          # warm-up outside capture: plans, workspace, device lengths
+    step(eager)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            captured = step(graphed)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for r in range(5):
+        g.replay()
+        want = step(eager)
+        torch.cuda.synchronize()
+        for i in range(L):
+            assert torch.equal(captured[i], want[i]), (r, i)
+        tl = graphed.layers[0].tail_len_device().cpu().tolist()
+        assert tl == eager.layers[0].tail_lens, (r, tl)
