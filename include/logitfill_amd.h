@@ -96,7 +96,8 @@ const char* lf_status_string(int32_t status);
  * history concatenation of _LayerStore._flush
  * (reference src/logitfill/packed/layout.py:71-129, cache.py:64-81).
  *
- * Packs ``n_jobs`` pages.  ``jobs`` is a DEVICE int32 array [n_jobs][3] of
+ * Packs ``n_jobs`` pages (at most 2^21 per call, else LF_E_SHAPE).  ``jobs``
+ * is a DEVICE int32 array [n_jobs][3] of
  * (b, src_token0, dst_page): the page is rows src_token0 .. src_token0 +
  * page_size - 1 of sequence b of ``k_src``/``v_src`` (element strides
  * src_stride_b/h/t, channel stride 1, dtype ``src_dtype``) and is written as
@@ -130,7 +131,8 @@ typedef struct lf_pack_source {
  * (layer, b, src_token0, dst_page).  Every layer must have the same n_kv and
  * take the fast shape (head_dim = page_size = k_group = v_group = 128,
  * bit_v 2, 16-byte aligned rows of a 2-byte dtype, even cap_tokens, 4-byte
- * aligned v_scale / v_min); otherwise LF_E_UNSUPPORTED and nothing runs.
+ * aligned v_scale / v_min, 8-byte aligned v_code); otherwise LF_E_UNSUPPORTED
+ * and nothing runs.  At most 2^21 jobs per call, else LF_E_SHAPE.
  */
 int32_t lf_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_layer* layers_host,
                             const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int32_t n_layers,

@@ -149,13 +149,17 @@ const char* lf_status_string(int32_t status) {
     return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown status";
 }
 
+// Two 512-thread workgroups per page and kv head: the grid's x extent (2 n_jobs workgroups)
+// stays far below the 2^32 work-items of a dimension.
+constexpr int32_t kMaxPackJobs = 1 << 21;
+
 int32_t lf_pack_pages(const lf_packed_layer* layer, const void* k_src, const void* v_src, int32_t src_dtype,
                       int64_t src_stride_b, int64_t src_stride_h, int64_t src_stride_t,
                       const int32_t* jobs, int32_t n_jobs, void* stream) {
     const int32_t st = check_layer(layer);
     if (st != LF_OK) return st;
     if (!valid_dtype(src_dtype)) return LF_E_DTYPE;
-    if (n_jobs < 0) return LF_E_SHAPE;
+    if (n_jobs < 0 || n_jobs > kMaxPackJobs) return LF_E_SHAPE;
     if (n_jobs == 0) return LF_OK;
     if (!k_src || !v_src || !jobs) return LF_E_NULL;
     if (layer->page_size > 1024 || layer->head_dim > 512) return LF_E_SHAPE;
@@ -166,7 +170,7 @@ int32_t lf_pack_pages(const lf_packed_layer* layer, const void* k_src, const voi
 int32_t lf_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_layer* layers_host,
                             const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int32_t n_layers,
                             int32_t src_dtype, const int32_t* jobs, int32_t n_jobs, void* stream) {
-    if (n_layers < 0 || n_jobs < 0) return LF_E_SHAPE;
+    if (n_layers < 0 || n_jobs < 0 || n_jobs > kMaxPackJobs) return LF_E_SHAPE;
     if (n_jobs == 0 || n_layers == 0) return n_jobs == 0 ? LF_OK : LF_E_SHAPE;
     if (!layers_dev || !layers_host || !srcs_dev || !srcs_host || !jobs) return LF_E_NULL;
     if (!valid_dtype(src_dtype)) return LF_E_DTYPE;

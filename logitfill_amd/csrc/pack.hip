@@ -304,10 +304,12 @@ int pack_code_row(const lf_packed_layer& L);
 // ---------------------------------------------------------------------------------------
 // Fast path for the common shape: page = Key group = Value group = head_dim = 128, int2
 // Values, 2-byte inputs with 16-byte aligned rows.  Two workgroups of 512 threads per page and
-// kv head (blockIdx.z 0: Key page, 1: Value page), about 39 KB of LDS for a Key workgroup, so
-// four share a CU; per element the division uses a correctly rounded reciprocal of the group
-// scale and one Markstein correction (see div_rn), branch-free.  The phases are listed at
-// pack_fast_page.  Each integer tier has a 16-byte aligned segment of a token's code row (in
+// kv head (blockIdx.z 0: Key page, 1: Value page -- all Key pages are dispatched first: mixing
+// the VALU-bound Key pages with the memory-bound Value pages measured slower, in alternate
+// single blocks and in runs of 8), about 40 KB of LDS, so four share a CU (56 KB and two for the
+// widest tier mixes).  Per element the division uses a correctly rounded reciprocal of the group
+// scale and one Markstein correction (div_rn); groups whose scale is not clamped above take the
+// clamp-free magic_code.  The phases are listed at pack_fast_page.  Each integer tier has a 16-byte aligned segment of a token's code row (in
 // slot order), so a word's 16 / 8 / 4 code bytes are one LDS read.
 // ---------------------------------------------------------------------------------------
 constexpr int kFastThreads = 512;
@@ -316,21 +318,104 @@ constexpr int kFastLd = 130;  // halves per staged row
 
 // a / s rounded to nearest even from y = RN(1/s) (Markstein: q0 = RN(a*y) is within an ulp of
 // a/s, the residual a - q0*s is exact by FMA, and RN(q0 + r*y) is the correctly rounded
-// quotient when no step overflows or underflows).  a >= 0 here and a <= s * qmax unless s was
-// clamped to 1e5 (then a / s <= 3.5e33), so a * y cannot overflow for finite a; a quotient
-// below the normal range rounds to code 0 either way.  a = +inf (a range overflowing float)
-// gives +inf, as IEEE division does.
+// quotient when no step overflows or underflows).  ``a`` is clamped to FLT_MAX first: only a
+// range that overflows float makes it +inf, and then s is clamped to 1e5, so the clamped
+// quotient (>= 3.4e33) still clamps to qmax, as inf / s does; otherwise a <= s * qmax (s not
+// clamped or clamped to 1e-5) or y = 1e-5, and a * y cannot overflow.  A quotient below the
+// normal range rounds to code 0 either way.  (A CPU check of 40 M random, tie and overflow
+// cases against IEEE division found no difference.)
 __device__ __forceinline__ float div_rn(float a, float s, float y) {
+    a = fminf(a, 3.40282347e38f);
     const float q0 = a * y;
     const float r = fmaf(-q0, s, a);
-    const float q = fmaf(r, y, q0);
-    return a == __builtin_inff() ? a : q;
+    return fmaf(r, y, q0);
 }
 
-// code = clamp(rint((x - lo) / s), 0, qmax) with div_rn.
+// RN((hi - lo) / qmax) by div_rn on the constant inv = RN(1 / qmax), qmax one of 3, 15, 255: a
+// range of +inf becomes FLT_MAX, whose quotient lies far above the clamp, as inf / qmax does.
+// The group scale is clamp(raw, 1e-5, 1e5) (layout.py:16); in the subnormal range the clamp to
+// 1e-5 hides the last bit.  (Checked on the CPU against IEEE division for 60 M ranges of every
+// magnitude: no difference.)
+__device__ __forceinline__ float raw_scale(float hi, float lo, float qmax, float inv) {
+    return div_rn(hi - lo, qmax, inv);
+}
+__device__ __forceinline__ float clamp_scale(float raw) { return fminf(fmaxf(raw, 1e-5f), 1e5f); }
+
+// code = clamp(rint((x - lo) / s), 0, qmax) with div_rn: the path for groups whose unclamped
+// scale exceeds 1e5 (ranges above 1e5 qmax, infinite ones included).
 __device__ __forceinline__ uint32_t fast_code(float x, float lo, float s, float y, float qmax) {
     const float q = __builtin_rintf(div_rn(x - lo, s, y));
     return static_cast<uint32_t>(__builtin_amdgcn_fmed3f(q, 0.0f, qmax));
+}
+
+// The common path, for groups whose unclamped scale r = RN(range / qmax) is at most 1e5: then
+// s = max(r, 1e-5) >= range / qmax (1 - 2^-24), a = RN(x - lo) lies in [0, range], so a / s is
+// at most qmax (1 + 2^-23) and its rint at most qmax -- the clamp cannot bind and nothing
+// overflows.  The correctly rounded quotient plus 2^23 rounds to an integer, half to even, in
+// the low mantissa bits: bits(q + 2^23) = 0x4B000000 + rint(q) for 0 <= q < 2^23, so the low
+// byte is the code.  (A CPU check of 4 M groups of 32 values at every magnitude, ties and
+// ranges around the 1e5 qmax boundary included, found no difference from the IEEE formula.)
+__device__ __forceinline__ uint32_t magic_code(float x, float lo, float s, float y) {
+    const float a = x - lo;
+    const float q0 = a * y;
+    const float r = fmaf(-q0, s, a);
+    return __float_as_uint(fmaf(r, y, q0) + 8388608.0f);
+}
+
+// Sum over a 16-code word of the 0x4B000000 that each magic_code carries, shifted as its code
+// is: a word built by adding magic codes shifted by 2 i, minus this, holds the codes.
+constexpr uint32_t value_word_bias() {
+    uint32_t s = 0;
+    for (int i = 0; i < 16; ++i) s += 0x4B000000u << (2 * i);
+    return s;
+}
+
+// min / max of three without the v_max_f32 x, x, x that the compiler puts before fminf / fmaxf
+// of a value it cannot prove canonical (bf16 bits moved into a float's high half).  Quieting a
+// signalling NaN is all that step does, and a NaN in a group is outside the packer's contract
+// (the reference's own scale becomes NaN).
+__device__ __forceinline__ float min3_raw(float a, float b, float c) {
+    float d;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
+// The value of lane l ^ 1 / l ^ 2 (DPP quad_perm [1,0,3,2] / [2,3,0,1]).
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
+// The two 16-bit elements of a dword as floats (element 0 in the low half).
+template <bool IsHalf>
+__device__ __forceinline__ void pair_f32(uint32_t d, float& e0, float& e1) {
+    if constexpr (IsHalf) {
+        e0 = f16_to_f32(static_cast<uint16_t>(d & 0xffffu));
+        e1 = f16_to_f32(static_cast<uint16_t>(d >> 16));
+    } else {
+        e0 = __uint_as_float(d << 16);
+        e1 = __uint_as_float(d & 0xffff0000u);
+    }
+}
+
+// lo / hi of 32 values by 16 min3 / max3 each.
+__device__ __forceinline__ void minmax32(const float (&v)[32], float& lo, float& hi) {
+    lo = min3_raw(v[0], v[1], v[2]);
+    hi = max3_raw(v[0], v[1], v[2]);
+#pragma unroll
+    for (int i = 3; i < 31; i += 2) {
+        lo = min3_raw(lo, v[i], v[i + 1]);
+        hi = max3_raw(hi, v[i], v[i + 1]);
+    }
+    lo = min3_raw(lo, v[31], v[31]);
+    hi = max3_raw(hi, v[31], v[31]);
 }
 
 // Byte-per-code LDS row of the fast path: tier t's slots start at seg[t] (16-byte aligned).
@@ -366,122 +451,173 @@ __device__ __forceinline__ uint32_t word_int4(uint2 b) {
     return __builtin_amdgcn_perm(t1, t0, 0x06040200u);
 }
 
-// Values of one token row: thread (token tk, channels 16 w + 0..15) holds its 32 bytes in ``r``
-// and produces one code word (layout.py:115-129); the token's min/max comes from its 8 lanes
-// (lanes 8k .. 8k + 7 of one wave) by lane exchange.
+// Value page (layout.py:115-129): one quad per token row, lane w holding channels 32 w .. 32 w +
+// 31 of token tid / 4; the row's min / max by two quad exchanges; lane w writes code words 2 w
+// and 2 w + 1.  The page's 128 fp16 scales and mins are contiguous: gathered in LDS, each array
+// leaves as one 256-byte store (token pairs; the row offset is even and the arrays 4-byte
+// aligned, which the launcher checks).
 template <bool IsHalf>
-__device__ __forceinline__ void pack_value_row(const lf_packed_layer& L, const uint4 (&r)[2], int b, int h,
-                                               int64_t dst_tok, int w, uint16_t& sc16, uint16_t& lo16) {
-    const uint32_t pr[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
-    float v[16];
-    float lo = __builtin_inff(), hi = -__builtin_inff();
+__device__ __forceinline__ void pack_value_page(const lf_packed_layer& L, const uint16_t* src, int64_t st, int b,
+                                                int h, int64_t dst_tok0, unsigned char* smem) {
+    const int tid = threadIdx.x;
+    const int tk = tid >> 2, w = tid & 3;
+    uint4 r[4];
+    {
+        const uint4* a = reinterpret_cast<const uint4*>(src + tk * st + 32 * w);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        v[2 * i] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] & 0xffffu));
-        v[2 * i + 1] = elem_f32<uint16_t, IsHalf>(static_cast<uint16_t>(pr[i] >> 16));
-        lo = fminf(lo, fminf(v[2 * i], v[2 * i + 1]));
-        hi = fmaxf(hi, fmaxf(v[2 * i], v[2 * i + 1]));
+        for (int i = 0; i < 4; ++i) r[i] = a[i];
     }
+    float v[32];
 #pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        lo = fminf(lo, __shfl_xor(lo, off, kWave));
-        hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
+    for (int i = 0; i < 4; ++i) {
+        pair_f32<IsHalf>(r[i].x, v[8 * i + 0], v[8 * i + 1]);
+        pair_f32<IsHalf>(r[i].y, v[8 * i + 2], v[8 * i + 3]);
+        pair_f32<IsHalf>(r[i].z, v[8 * i + 4], v[8 * i + 5]);
+        pair_f32<IsHalf>(r[i].w, v[8 * i + 6], v[8 * i + 7]);
     }
-    const float sc = group_scale(hi, lo, 3);
+    float lo, hi;
+    minmax32(v, lo, hi);
+    lo = min3_raw(lo, quad_xor1(lo), lo);
+    hi = max3_raw(hi, quad_xor1(hi), hi);
+    lo = min3_raw(lo, quad_xor2(lo), lo);
+    hi = max3_raw(hi, quad_xor2(hi), hi);
+    const float raw = raw_scale(hi, lo, 3.0f, 1.0f / 3.0f);
+    const float sc = clamp_scale(raw);
     const float y = 1.0f / sc;
-    uint32_t word = 0;
+    uint32_t wd[2];
+    if (raw <= 1e5f) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) word |= fast_code(v[i], lo, sc, y, 3.0f) << (2 * i);
-    const int64_t trow = tok_row(L, b, h, dst_tok);
-    L.v_code[trow * 8 + w] = static_cast<int32_t>(word);
-    sc16 = f32_to_f16(sc);
-    lo16 = f32_to_f16(lo);
+        for (int j = 0; j < 2; ++j) {
+            uint32_t acc = 0u - value_word_bias();
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc += magic_code(v[16 * j + i], lo, sc, y) << (2 * i);
+            wd[j] = acc;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t acc = 0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc |= fast_code(v[16 * j + i], lo, sc, y, 3.0f) << (2 * i);
+            wd[j] = acc;
+        }
+    }
+    reinterpret_cast<uint2*>(L.v_code + tok_row(L, b, h, dst_tok0 + tk) * 8)[w] = make_uint2(wd[0], wd[1]);
+    uint16_t* vsm = reinterpret_cast<uint16_t*>(smem);  // [2][128]: scale, min
+    if (w == 0) {
+        vsm[tk] = f32_to_f16(sc);
+        vsm[128 + tk] = f32_to_f16(lo);
+    }
+    __syncthreads();
+    if (tid < 128) {
+        uint16_t* dst = (tid < 64 ? L.v_scale : L.v_min) + tok_row(L, b, h, dst_tok0);
+        reinterpret_cast<uint32_t*>(dst)[tid & 63] = reinterpret_cast<const uint32_t*>(vsm)[tid];
+    }
 }
 
-// LDS layout of the Key workgroup: the staged page (rows padded to 130 halves), partial
-// min/max, the fp16-tier values, the channel map; the code rows reuse the page once phase 1
-// has read it (or sit after the rest when they do not fit there).
+// Code rows of the Key workgroup: one row of ``Ld`` bytes per token, Ld a compile-time constant
+// so that phase 3's 32 byte stores per thread address by immediate offsets.  272 (17 x 16 bytes:
+// consecutive rows start 4 banks apart) holds every tier mix whose int tiers' 16-byte aligned
+// segments fit (all of the bench's), 400 the widest possible (3 x 128).
+constexpr int kCodeLdNarrow = 272;
+constexpr int kCodeLdWide = 400;
+static_assert(kFastLd * 2 <= kCodeLdNarrow, "the staged page lies within the code rows");
+
+__device__ __host__ inline int code_ld(const lf_packed_layer& L) {
+    return code_segs(L).seg[3] <= kCodeLdNarrow ? kCodeLdNarrow : kCodeLdWide;
+}
+
+// LDS layout of the Key workgroup: the code rows (the staged page, rows padded to 130 halves,
+// lies in their first 33 KB until phase 1 has read it), partial min/max, the channel map, the
+// fp16 tier's channels.
 struct FastLds {
-    int pmm, f16, cpos, tidx, codes, total;
+    int pmm, cpos, tidx, total;
 };
 
-__device__ __host__ inline FastLds fast_lds(const lf_packed_layer& L) {
+__device__ __host__ inline FastLds fast_lds(int ld, int w16) {
     FastLds f;
-    const int page = kFastP * kFastLd * 2;
-    f.pmm = page;                                        // [4][128] float2
-    f.f16 = f.pmm + 4 * 128 * 8;                         // [128][w16] fp16
-    f.cpos = f.f16 + ((kFastP * L.k_width[3] * 2 + 15) & ~15);  // [128] int16
+    f.pmm = kFastP * ld;                                 // after [128][ld] code bytes (ld % 16 == 0)
+    f.cpos = f.pmm + 4 * 128 * 8;                        // [4][128] float2 -> [128] int16
     f.tidx = f.cpos + 128 * 2;                           // [w16] int16
-    const int end = f.tidx + ((L.k_width[3] * 2 + 15) & ~15);
-    const int cbytes = kFastP * code_segs(L).seg[3];
-    f.codes = cbytes <= page ? 0 : end;
-    f.total = (cbytes <= page ? end : end + cbytes) + 16;
+    f.total = f.tidx + ((w16 * 2 + 15) & ~15) + 16;
     return f;
 }
 
-// One page of one kv head (blockIdx.y) of layer ``L``: the Key page (blockIdx.z == 0) or the
-// Value page.  Source rows tok0 .. tok0 + 127 of sequence b (element strides sb, sh, st) are
+// Words of one integer tier (Bits 2, 4 or 8) of the Key page (layout.py:21-35, :94-97): with
+// T = 512 / kw rows per pass, thread tid < T kw takes word w = tid % kw of rows tid / kw, + T,
+// ...; word r kw + w of the page block is then tid, + T kw, ..., so consecutive threads store
+// consecutive dwords and every store instruction covers whole lines.  Each word comes from
+// 16 / 8 / 4 code bytes of its token's row; slots at or beyond the tier's count for this head
+// are masked to 0 (layout.py:84-85).  tid / kw = (int)((tid + 0.5) * (1 / kw)) in fp32 is exact
+// for tid < 512, kw <= 512 (checked exhaustively).
+template <int Bits, int Ld>
+__device__ __forceinline__ void tier_words(const uint8_t* codes, int seg, int kw, int cnt, int32_t* out, int tid) {
+    if (kw == 0) return;
+    constexpr int kPer = 32 / Bits;
+    const int T = kFastThreads / kw;
+    if (tid >= T * kw) return;
+    const int r0 = static_cast<int>((static_cast<float>(tid) + 0.5f) * (1.0f / static_cast<float>(kw)));
+    const int w = tid - r0 * kw;
+    const int nv = min(max(cnt - kPer * w, 0), kPer);
+    const uint32_t keep = nv >= kPer ? 0xffffffffu : (1u << (Bits * nv)) - 1u;
+    const uint8_t* src = codes + r0 * Ld + seg + kPer * w;
+    int32_t* dst = out + tid;
+    for (int r = r0; r < kFastP; r += T) {
+        uint32_t word;
+        if constexpr (Bits == 2) {
+            uint4 cb = *reinterpret_cast<const uint4*>(src);
+            cb.x &= 0x03030303u; cb.y &= 0x03030303u; cb.z &= 0x03030303u; cb.w &= 0x03030303u;
+            word = word_int2(cb);
+        } else if constexpr (Bits == 4) {
+            uint2 cb = *reinterpret_cast<const uint2*>(src);
+            cb.x &= 0x0f0f0f0fu; cb.y &= 0x0f0f0f0fu;
+            word = word_int4(cb);
+        } else {
+            word = *reinterpret_cast<const uint32_t*>(src);
+        }
+        *dst = static_cast<int32_t>(word & keep);
+        src += T * Ld;
+        dst += T * kw;
+    }
+}
+
+// One page of one kv head (blockIdx.y) of layer ``L``: the Key page or (``value``) the Value
+// page.  Source rows tok0 .. tok0 + 127 of sequence b (element strides sb, sh, st) are
 // written as page ``page`` of sequence b.  512 threads: four workgroups share a CU.
-//   Value page  thread (token tid / 8 and + 64, 16 channels) reads its row slices from global
-//               memory directly: no LDS
+//   Value page  quad per token row (tid / 4), 32 channels per lane, read from global memory
+//               directly (LDS only gathers the page's scales and mins)
 //   Key page    stage (page -> LDS, tier tables -> channel map); phase 1: thread (channel
-//               tid % 128, tokens 32 (tid / 128) + 0..31) min/max, fp16-tier values to LDS;
-//               phases 2, 3: the channel's scale and its 32 codes into byte rows over the
-//               page; phase 4: thread (token tid / 4, q) assembles words q, q + 4, ... of the
-//               token's integer tiers from 16 / 8 / 4 code bytes and copies the fp16 tier
-template <bool IsHalf>
+//               tid % 128, tokens 32 (tid / 128) + 0..31) min/max, the fp16 tier copied from
+//               the staged page; phases 2, 3: the channel's scale and its 32 codes into byte
+//               rows over the page; phase 4: the tiers' words (tier_words)
+template <bool IsHalf, int Ld>
 __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const void* k_src, const void* v_src,
-                                               int64_t sb, int64_t sh, int64_t st, int b, int64_t tok0, int page) {
+                                               int64_t sb, int64_t sh, int64_t st, int b, int64_t tok0, int page,
+                                               bool value) {
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
     const int64_t dst_tok0 = static_cast<int64_t>(page) * kFastP;
     constexpr int D = 128;
     extern __shared__ __align__(16) unsigned char smem[];
 
-    if (blockIdx.z != 0) {
-        // ---- Values: both rows' slices in flight before the first use ----
-        const uint16_t* src = static_cast<const uint16_t*>(v_src) + b * sb + h * sh + tok0 * st;
-        const int tk = tid >> 3, w = tid & 7;
-        uint4 r0[2], r1[2];
-        {
-            const uint4* a0 = reinterpret_cast<const uint4*>(src + tk * st + 16 * w);
-            const uint4* a1 = reinterpret_cast<const uint4*>(src + (tk + 64) * st + 16 * w);
-            r0[0] = a0[0]; r0[1] = a0[1]; r1[0] = a1[0]; r1[1] = a1[1];
-        }
-        uint16_t s0, m0, s1, m1;
-        pack_value_row<IsHalf>(L, r0, b, h, dst_tok0 + tk, w, s0, m0);
-        pack_value_row<IsHalf>(L, r1, b, h, dst_tok0 + tk + 64, w, s1, m1);
-        // the page's 128 fp16 scales and mins are contiguous: gathered in LDS, each array leaves
-        // as one 256-byte store (token pairs; the row offset is even and the arrays 4-byte
-        // aligned, which the launcher checks)
-        uint16_t* vsm = reinterpret_cast<uint16_t*>(smem);  // [2][128]: scale, min
-        if (w == 0) {
-            vsm[tk] = s0;
-            vsm[tk + 64] = s1;
-            vsm[128 + tk] = m0;
-            vsm[128 + tk + 64] = m1;
-        }
-        __syncthreads();
-        if (tid < 128) {
-            uint16_t* dst = (tid < 64 ? L.v_scale : L.v_min) + tok_row(L, b, h, dst_tok0);
-            reinterpret_cast<uint32_t*>(dst)[tid & 63] = reinterpret_cast<const uint32_t*>(vsm)[tid];
-        }
+    if (value) {
+        pack_value_page<IsHalf>(L, static_cast<const uint16_t*>(v_src) + b * sb + h * sh + tok0 * st, st, b, h,
+                                dst_tok0, smem);
         return;
     }
 
-    const FastLds fl = fast_lds(L);
-    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                  // [128][130]
+    const FastLds fl = fast_lds(Ld, L.k_width[3]);
+    uint8_t* codes = smem;                                                  // [128][Ld] code bytes
+    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                  // [128][130]: the page, read
+                                                                            // before the codes replace it
     float2* pmm = reinterpret_cast<float2*>(smem + fl.pmm);                // [4][128] partial (lo, hi)
-    uint16_t* f16v = reinterpret_cast<uint16_t*>(smem + fl.f16);           // [128][w16] fp16 tier
     int16_t* cpos = reinterpret_cast<int16_t*>(smem + fl.cpos);            // [128] code byte of a channel,
                                                                             // -1 - rank for the fp16 tier
-    uint8_t* codes = smem + fl.codes;                                      // [128][cw] code bytes
-    const CodeSegs cs = code_segs(L);
-    const int cw = cs.seg[3];
+    int16_t* tidx = reinterpret_cast<int16_t*>(smem + fl.tidx);            // [w16] channel of an fp16 slot
+    const CodeSegs cs = code_segs(L);  // cs.seg[3] <= Ld (the launcher's choice of Ld)
 
     const int w0 = L.k_width[0], w1 = L.k_width[1], w2 = L.k_width[2], w16 = L.k_width[3];
     const int koff1 = w0, koff2 = w0 + w1, nslots = w0 + w1 + w2, wall = nslots + w16;
-
     // ---- stage the page and this head's tier tables (layout.py:49-68): all their global loads
     // go out before the first wait ----
     {
@@ -514,6 +650,7 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
             const int j = tid - (t == 3 ? nslots : t == 2 ? koff2 : t == 1 ? koff1 : 0);
             if (j < my_cnt) {
                 cpos[my_idx] = static_cast<int16_t>(t == 3 ? -1 - j : (t == 2 ? cs.seg[2] : t == 1 ? cs.seg[1] : 0) + j);
+                if (t == 3) tidx[j] = static_cast<int16_t>(my_idx);
             } else if (t < 3) {
                 const int width = t == 2 ? w2 : t == 1 ? w1 : w0;
                 const int64_t o = kgrp_idx(L, b, h, width, j, page);
@@ -531,18 +668,22 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     const int pos = cpos[c];
     float x[32];
     {
-        float lo = __builtin_inff(), hi = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            x[i] = elem_f32<uint16_t, IsHalf>(kpage[(32 * ck + i) * kFastLd + c]);
-            lo = fminf(lo, x[i]);
-            hi = fmaxf(hi, x[i]);
-        }
+        for (int i = 0; i < 32; ++i) x[i] = elem_f32<uint16_t, IsHalf>(kpage[(32 * ck + i) * kFastLd + c]);
+        float lo, hi;
+        minmax32(x, lo, hi);
         pmm[ck * D + c] = float2{lo, hi};
-        if (pos < 0) {  // fp16 tier (layout.py:101-111): exact for fp16 input, RNE for bf16
-            const int j = -1 - pos;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) f16v[(32 * ck + i) * w16 + j] = f32_to_f16(x[i]);
+    }
+    // fp16 tier (layout.py:101-111; exact for fp16 input, RNE for bf16) straight from the staged
+    // page, element i = (token i / w16, slot i % w16) in memory order; padding slots are 0
+    if (w16 > 0) {
+        const int cnt = L.tier_count[3][h];
+        const float rk = 1.0f / static_cast<float>(w16);
+        uint16_t* out = L.k_value16 + tok_row(L, b, h, dst_tok0) * w16;
+        for (int i = tid; i < kFastP * w16; i += kFastThreads) {
+            const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), j = i - tau * w16;
+            out[i] = j < cnt ? f32_to_f16(elem_f32<uint16_t, IsHalf>(kpage[tau * kFastLd + tidx[j]]))
+                             : static_cast<uint16_t>(0);
         }
     }
     __syncthreads();  // the page is dead: the code rows may overwrite it
@@ -550,16 +691,13 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     // ---- phases 2, 3: the channel's group scale (layout.py:12-18) and its 32 codes; bytes of
     // slots no channel writes are masked when the words are assembled ----
     if (pos >= 0) {
-        float lo = __builtin_inff(), hi = -__builtin_inff();
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float2 m = pmm[k * D + c];
-            lo = fminf(lo, m.x);
-            hi = fmaxf(hi, m.y);
-        }
+        const float2 m0 = pmm[c], m1 = pmm[D + c], m2 = pmm[2 * D + c], m3 = pmm[3 * D + c];
+        const float lo = min3_raw(min3_raw(m0.x, m1.x, m2.x), m3.x, m3.x);
+        const float hi = max3_raw(max3_raw(m0.y, m1.y, m2.y), m3.y, m3.y);
         const int t = pos >= cs.seg[2] ? 2 : pos >= cs.seg[1] ? 1 : 0;
-        const int qm = t == 2 ? 255 : t == 1 ? 15 : 3;
-        const float sc = group_scale(hi, lo, qm);
+        const float qmax = t == 2 ? 255.0f : t == 1 ? 15.0f : 3.0f;
+        const float raw = raw_scale(hi, lo, qmax, t == 2 ? 1.0f / 255.0f : t == 1 ? 1.0f / 15.0f : 1.0f / 3.0f);
+        const float sc = clamp_scale(raw);
         const float y = 1.0f / sc;
         if (ck == 0) {
             const int j = pos - (t == 2 ? cs.seg[2] : t == 1 ? cs.seg[1] : 0);
@@ -570,78 +708,30 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
             ks[o] = f32_to_f16(sc);
             km[o] = f32_to_f16(lo);
         }
-        const float qmax = static_cast<float>(qm);
-        uint8_t* crow = codes + (32 * ck) * cw + pos;
+        uint8_t* crow = codes + (32 * ck) * Ld + pos;
+        if (raw <= 1e5f) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) crow[i * cw] = static_cast<uint8_t>(fast_code(x[i], lo, sc, y, qmax));
+            for (int i = 0; i < 32; ++i) crow[i * Ld] = static_cast<uint8_t>(magic_code(x[i], lo, sc, y));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) crow[i * Ld] = static_cast<uint8_t>(fast_code(x[i], lo, sc, y, qmax));
+        }
     }
     __syncthreads();
 
-    // ---- phase 4: LSB-first words (layout.py:21-35, :94-97), one loop per tier; fp16 tier.
-    // Word i of a tier's page block is (token i / kw, word i % kw): the page's rows are
-    // contiguous, so consecutive threads store consecutive dwords and every store instruction
-    // covers whole lines (a row-per-thread-group order leaves each line part-written by several
-    // instructions).  i / kw = (int)((i + 0.5) * (1 / kw)) in fp32 is exact for i < 128 kw,
-    // kw <= 64 (checked exhaustively) ----
-    {
-        const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
-        const int c0 = w0 ? L.tier_count[0][h] : 0;
-        const int c1 = w1 ? L.tier_count[1][h] : 0;
-        const int c2 = w2 ? L.tier_count[2][h] : 0;
-        const int64_t row0 = tok_row(L, b, h, dst_tok0);
-        const int n0 = kFastP * kw0, n1 = kFastP * kw1, n2 = kFastP * kw2;
-        {
-            const float rk = 1.0f / static_cast<float>(kw0);
-            int32_t* out = L.k_code[0] + row0 * kw0;
-            for (int i = tid; i < n0; i += kFastThreads) {
-                const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), w = i - tau * kw0;
-                uint4 cb = *reinterpret_cast<const uint4*>(codes + tau * cw + 16 * w);
-                cb.x &= 0x03030303u; cb.y &= 0x03030303u; cb.z &= 0x03030303u; cb.w &= 0x03030303u;
-                const int nv = min(max(c0 - 16 * w, 0), 16);
-                const uint32_t keep = nv >= 16 ? 0xffffffffu : (1u << (2 * nv)) - 1u;
-                out[i] = static_cast<int32_t>(word_int2(cb) & keep);
-            }
-        }
-        {
-            const float rk = 1.0f / static_cast<float>(kw1);
-            int32_t* out = L.k_code[1] + row0 * kw1;
-            for (int i = (tid - n0) & (kFastThreads - 1); i < n1; i += kFastThreads) {
-                const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), w = i - tau * kw1;
-                uint2 cb = *reinterpret_cast<const uint2*>(codes + tau * cw + cs.seg[1] + 8 * w);
-                cb.x &= 0x0f0f0f0fu; cb.y &= 0x0f0f0f0fu;
-                const int nv = min(max(c1 - 8 * w, 0), 8);
-                const uint32_t keep = nv >= 8 ? 0xffffffffu : (1u << (4 * nv)) - 1u;
-                out[i] = static_cast<int32_t>(word_int4(cb) & keep);
-            }
-        }
-        {
-            const float rk = 1.0f / static_cast<float>(kw2);
-            int32_t* out = L.k_code[2] + row0 * kw2;
-            for (int i = (tid - n0 - n1) & (kFastThreads - 1); i < n2; i += kFastThreads) {
-                const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), w = i - tau * kw2;
-                const uint32_t cb = *reinterpret_cast<const uint32_t*>(codes + tau * cw + cs.seg[2] + 4 * w);
-                const int nv = min(max(c2 - 4 * w, 0), 4);
-                const uint32_t keep = nv >= 4 ? 0xffffffffu : (1u << (8 * nv)) - 1u;
-                out[i] = static_cast<int32_t>(cb & keep);
-            }
-        }
-        if (w16 > 0) {
-            const int cnt = L.tier_count[3][h];
-            const float rk = 1.0f / static_cast<float>(w16);
-            uint16_t* out = L.k_value16 + row0 * w16;
-            for (int i = (tid - n0 - n1 - n2) & (kFastThreads - 1); i < kFastP * w16; i += kFastThreads) {
-                const int j = i - w16 * static_cast<int>((static_cast<float>(i) + 0.5f) * rk);
-                out[i] = j < cnt ? f16v[i] : static_cast<uint16_t>(0);
-            }
-        }
-    }
+    // ---- phase 4: the integer tiers' words ----
+    const int64_t row0 = tok_row(L, b, h, dst_tok0);
+    const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
+    tier_words<2, Ld>(codes, 0, kw0, w0 ? L.tier_count[0][h] : 0, L.k_code[0] + row0 * kw0, tid);
+    tier_words<4, Ld>(codes, cs.seg[1], kw1, w1 ? L.tier_count[1][h] : 0, L.k_code[1] + row0 * kw1, tid);
+    tier_words<8, Ld>(codes, cs.seg[2], kw2, w2 ? L.tier_count[2][h] : 0, L.k_code[2] + row0 * kw2, tid);
 }
 
-template <bool IsHalf>
+template <bool IsHalf, int Ld>
 __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) {
     const int job = blockIdx.x;
-    pack_fast_page<IsHalf>(a.L, a.k_src, a.v_src, a.sb, a.sh, a.st, a.jobs[3 * job + 0], a.jobs[3 * job + 1],
-                           a.jobs[3 * job + 2]);
+    pack_fast_page<IsHalf, Ld>(a.L, a.k_src, a.v_src, a.sb, a.sh, a.st, a.jobs[3 * job + 0], a.jobs[3 * job + 1],
+                           a.jobs[3 * job + 2], blockIdx.z != 0);
 }
 
 // Several layers' pages in one launch: job = (layer, b, src_token0, dst_page); the layer's
@@ -652,23 +742,55 @@ struct PackMultiArgs {
     const int32_t* jobs;
 };
 
-template <bool IsHalf>
+template <bool IsHalf, int Ld>
 __global__ __launch_bounds__(kFastThreads) void pack_fast_multi_kernel(PackMultiArgs m) {
     const int job = blockIdx.x;
     const int layer = __builtin_amdgcn_readfirstlane(m.jobs[4 * job + 0]);
     const lf_packed_layer& L = m.layers[layer];
     const lf_pack_source& S = m.srcs[layer];
-    pack_fast_page<IsHalf>(L, S.k, S.v, S.stride_b, S.stride_h, S.stride_t, m.jobs[4 * job + 1], m.jobs[4 * job + 2],
-                           m.jobs[4 * job + 3]);
+    pack_fast_page<IsHalf, Ld>(L, S.k, S.v, S.stride_b, S.stride_h, S.stride_t, m.jobs[4 * job + 1], m.jobs[4 * job + 2],
+                           m.jobs[4 * job + 3], blockIdx.z != 0);
 }
 
-bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16) {
-    return vec16 && src_dtype != LF_FP32 && L.head_dim == 128 && L.page_size == kFastP && L.k_group == kFastP &&
+// ``st``: the source's token stride in elements (the Key page is read through a buffer resource
+// whose byte offsets, up to 127 st 2 + 256, must stay below 2^31).
+bool pack_fast_ok(const lf_packed_layer& L, int src_dtype, bool vec16, int64_t st) {
+    return vec16 && src_dtype != LF_FP32 && st > 0 && st <= (1 << 22) && L.head_dim == 128 && L.page_size == kFastP && L.k_group == kFastP &&
            L.v_group == 128 && L.bit_v == 2 && L.v_groups == 1 && L.v_words == 8 && L.cap_tokens % 2 == 0 &&
-           (reinterpret_cast<uintptr_t>(L.v_scale) & 3) == 0 && (reinterpret_cast<uintptr_t>(L.v_min) & 3) == 0;
+           (reinterpret_cast<uintptr_t>(L.v_scale) & 3) == 0 && (reinterpret_cast<uintptr_t>(L.v_min) & 3) == 0 &&
+           (reinterpret_cast<uintptr_t>(L.v_code) & 7) == 0;
 }
 
-size_t pack_fast_lds_bytes(const lf_packed_layer& L) { return static_cast<size_t>(fast_lds(L).total); }
+size_t pack_fast_lds_bytes(int ld, int w16) { return static_cast<size_t>(fast_lds(ld, w16).total); }
+
+// One fast-path launch of kernel ``K`` (pack_fast_kernel or pack_fast_multi_kernel instances for
+// bf16 / fp16 sources) with ``lds`` bytes of dynamic LDS.
+template <typename Args>
+int launch_fast(const void* fn_bf16, const void* fn_f16, void (*k_bf16)(Args), void (*k_f16)(Args), bool half,
+                dim3 grid, size_t lds, const Args& args, hipStream_t stream) {
+    const int rc = allow_dynamic_lds(half ? fn_f16 : fn_bf16, lds);
+    if (rc != LF_OK) return rc;
+    if (half) hipLaunchKernelGGL(k_f16, grid, dim3(kFastThreads), lds, stream, args);
+    else hipLaunchKernelGGL(k_bf16, grid, dim3(kFastThreads), lds, stream, args);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? LF_OK : static_cast<int>(err);
+}
+
+template <int Ld>
+int launch_fast_single(const PackJobArgs& a, bool half, dim3 grid, size_t lds, hipStream_t stream) {
+    return launch_fast<PackJobArgs>(reinterpret_cast<const void*>(&pack_fast_kernel<false, Ld>),
+                                    reinterpret_cast<const void*>(&pack_fast_kernel<true, Ld>),
+                                    pack_fast_kernel<false, Ld>, pack_fast_kernel<true, Ld>, half, grid, lds, a,
+                                    stream);
+}
+
+template <int Ld>
+int launch_fast_multi(const PackMultiArgs& m, bool half, dim3 grid, size_t lds, hipStream_t stream) {
+    return launch_fast<PackMultiArgs>(reinterpret_cast<const void*>(&pack_fast_multi_kernel<false, Ld>),
+                                      reinterpret_cast<const void*>(&pack_fast_multi_kernel<true, Ld>),
+                                      pack_fast_multi_kernel<false, Ld>, pack_fast_multi_kernel<true, Ld>, half, grid,
+                                      lds, m, stream);
+}
 
 int pack_code_row(const lf_packed_layer& L) {
     const int wsum = L.k_width[0] + L.k_width[1] + L.k_width[2];
@@ -717,20 +839,13 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
               ((st * elem) % 16 == 0);
     a.cw = pack_code_row(L);
     dim3 grid(n_jobs, L.n_kv);
-    if (pack_fast_ok(L, src_dtype, a.vec16 != 0)) {
-        const size_t lds = pack_fast_lds_bytes(L);
-        if (lds <= 160 * 1024) {
-            const int half = src_dtype == LF_FP16;
-            const void* fn = half ? reinterpret_cast<const void*>(&pack_fast_kernel<true>)
-                                  : reinterpret_cast<const void*>(&pack_fast_kernel<false>);
-            const int rc = allow_dynamic_lds(fn, lds);
-            if (rc != LF_OK) return rc;
-            const dim3 grid2(n_jobs, L.n_kv, 2);  // z: Key page, Value page
-            if (half) hipLaunchKernelGGL(pack_fast_kernel<true>, grid2, dim3(kFastThreads), lds, stream, a);
-            else hipLaunchKernelGGL(pack_fast_kernel<false>, grid2, dim3(kFastThreads), lds, stream, a);
-            const hipError_t err = hipGetLastError();
-            return err == hipSuccess ? LF_OK : static_cast<int>(err);
-        }
+    if (pack_fast_ok(L, src_dtype, a.vec16 != 0, st)) {
+        const int ld = code_ld(L);
+        const size_t lds = pack_fast_lds_bytes(ld, L.k_width[3]);
+        const bool half = src_dtype == LF_FP16;
+        const dim3 grid2(n_jobs, L.n_kv, 2);  // z: Key page, Value page
+        return ld == kCodeLdNarrow ? launch_fast_single<kCodeLdNarrow>(a, half, grid2, lds, stream)
+                                   : launch_fast_single<kCodeLdWide>(a, half, grid2, lds, stream);
     }
     int rc;
     if (src_dtype == LF_BF16) rc = launch_one<uint16_t, false>(a, grid, elem, stream);
@@ -746,7 +861,7 @@ int launch_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_l
                             const lf_pack_source* srcs_dev, const lf_pack_source* srcs_host, int n_layers,
                             int src_dtype, const int32_t* jobs, int n_jobs, hipStream_t stream) {
     if (src_dtype == LF_FP32) return LF_E_UNSUPPORTED;
-    size_t lds = 0;
+    int ld = kCodeLdNarrow;
     for (int i = 0; i < n_layers; ++i) {
         const lf_packed_layer& L = layers_host[i];
         const lf_pack_source& S = srcs_host[i];
@@ -754,22 +869,19 @@ int launch_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_l
         const uintptr_t kp = reinterpret_cast<uintptr_t>(S.k), vp = reinterpret_cast<uintptr_t>(S.v);
         const bool vec16 = ((kp | vp) % 16 == 0) && ((S.stride_b * 2) % 16 == 0) && ((S.stride_h * 2) % 16 == 0) &&
                            ((S.stride_t * 2) % 16 == 0);
-        if (!pack_fast_ok(L, src_dtype, vec16)) return LF_E_UNSUPPORTED;
-        const size_t l = pack_fast_lds_bytes(L);
+        if (!pack_fast_ok(L, src_dtype, vec16, S.stride_t)) return LF_E_UNSUPPORTED;
+        if (code_ld(L) == kCodeLdWide) ld = kCodeLdWide;
+    }
+    size_t lds = 0;
+    for (int i = 0; i < n_layers; ++i) {
+        const size_t l = pack_fast_lds_bytes(ld, layers_host[i].k_width[3]);
         lds = l > lds ? l : lds;
     }
-    if (lds > 160 * 1024) return LF_E_SHAPE;
-    const int half = src_dtype == LF_FP16;
-    const void* fn = half ? reinterpret_cast<const void*>(&pack_fast_multi_kernel<true>)
-                          : reinterpret_cast<const void*>(&pack_fast_multi_kernel<false>);
-    const int rc = allow_dynamic_lds(fn, lds);
-    if (rc != LF_OK) return rc;
+    const bool half = src_dtype == LF_FP16;
     PackMultiArgs m{layers_dev, srcs_dev, jobs};
     const dim3 grid(n_jobs, layers_host[0].n_kv, 2);  // z: Key page, Value page
-    if (half) hipLaunchKernelGGL(pack_fast_multi_kernel<true>, grid, dim3(kFastThreads), lds, stream, m);
-    else hipLaunchKernelGGL(pack_fast_multi_kernel<false>, grid, dim3(kFastThreads), lds, stream, m);
-    const hipError_t err = hipGetLastError();
-    return err == hipSuccess ? LF_OK : static_cast<int>(err);
+    return ld == kCodeLdNarrow ? launch_fast_multi<kCodeLdNarrow>(m, half, grid, lds, stream)
+                               : launch_fast_multi<kCodeLdWide>(m, half, grid, lds, stream);
 }
 
 }  // namespace lf
