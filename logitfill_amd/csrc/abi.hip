@@ -149,8 +149,8 @@ const char* lf_status_string(int32_t status) {
     return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown status";
 }
 
-// Two 512-thread workgroups per page and kv head: the grid's x extent (2 n_jobs workgroups)
-// stays far below the 2^32 work-items of a dimension.
+// Page jobs are the grid's x dimension (n_jobs workgroups of up to 512 threads): 2^21 jobs keep
+// its work-items far below the 2^32 of a dimension.
 constexpr int32_t kMaxPackJobs = 1 << 21;
 
 int32_t lf_pack_pages(const lf_packed_layer* layer, const void* k_src, const void* v_src, int32_t src_dtype,

@@ -160,7 +160,7 @@ def test_argument_validation_rejects_before_launch():
     assert lib.lf_decode_attention(layer, None, None) == -2
     assert lib.lf_dequantize(layer, 0, 4, None, None, None) == -1
     assert lib.lf_dense_decode(None, None, None, 1, 1, 1, 128, 1, 0, 0, 0, 1.0, None, 64, None, 0, None) == -1
-    # two workgroups per page job: more than 2^21 jobs in one call is refused
+    # more than 2^21 page jobs in one call is refused
     assert lib.lf_pack_pages_multi(None, None, None, None, 1, 0, None, (1 << 21) + 1, None) == -2
     assert lib.lf_pack_pages_multi(None, None, None, None, 1, 0, None, 1 << 21, None) == -1
 
