@@ -94,10 +94,21 @@ def _cu_count(device) -> int:
     return _CU_COUNT[key]
 
 
-# Decode time of one sequence's residual (the BF16 tail page and the new token) in units of
-# packed pages, used to balance the split-K items (measured on the 7B shape: about 14 us
-# against 2.6 us per packed page and workgroup).
-RESIDUAL_PAGES = 5
+# Decode time of one sequence's residual (the BF16 tail page and the new token) in packed
+# pages, for balancing the split-K items: a fixed part (the residual pass's load round, its
+# scores and the merge of its wave partials) and a part that grows with the tail, taken from
+# the batch's longest tail (lf_plan_decode takes one cost for every sequence).  Measured with
+# the cost forced, 28 layers: c2 (100-token tails) 88.2-88.8 us per layer-step at 5-8 pages,
+# 92.2 at 3, 90.1 at 12; c1 (37-token tails, 3-page items) 24.0-24.1 us at every cost from 3
+# up (the residual is then an item of its own) and 30.5 at 1-2.
+RESIDUAL_FIXED_PAGES = 3
+RESIDUAL_TAIL_PAGES = 4  # added for a full 127-token tail
+
+
+def residual_pages(tail_lens) -> int:
+    """Residual cost in pages for the longest of ``tail_lens``: 3 + round(4 * tail / 127)."""
+    t = min(max(max(tail_lens, default=0), 0), 127)
+    return RESIDUAL_FIXED_PAGES + (RESIDUAL_TAIL_PAGES * t + 63) // 127
 
 
 # Fixed cost of one split-K item (query load, page-ring start-up, the partial result's store
@@ -118,8 +129,7 @@ def _pages_per_split(pages: tuple, n_kv: int, residual_pages: int, slots: int) -
     return int(size[int(np.argmin(cost)), 0])                          # ties: fewest items
 
 
-def choose_pages_per_split(hist_pages: list[int], n_kv: int, residual_pages: int = RESIDUAL_PAGES,
-                           device=None) -> int:
+def choose_pages_per_split(hist_pages: list[int], n_kv: int, residual_pages: int, device=None) -> int:
     """Work per split-K item, in pages.  The decode kernel holds two workgroups per CU (the
     slots).  Items of ``total work / slots`` pages fill the slots once when every sequence's
     work (its pages plus its residual) divides evenly; with ragged lengths the per-sequence
@@ -137,8 +147,7 @@ def choose_pages_per_split(hist_pages: list[int], n_kv: int, residual_pages: int
 class DecodePlan:
     """Device work list for one layer's current history lengths (rebuilt when they change)."""
 
-    def __init__(self, hist_pages: list[int], n_kv: int, pages_per_split: int, device,
-                 residual_pages: int = RESIDUAL_PAGES):
+    def __init__(self, hist_pages: list[int], n_kv: int, pages_per_split: int, device, residual_pages: int):
         lib = _native.load()
         batch = len(hist_pages)
         cap = sum(-(-(p + residual_pages) // pages_per_split) for p in hist_pages) + batch
@@ -195,11 +204,12 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     kernel = kernel_choice() if kernel is None else kernel
     P = layer.page_size
     hist_pages = [h // P for h in layer.hist_lens]
+    res_pages = residual_pages(layer.tail_lens)
     if pages_per_split is None:
-        pages_per_split = choose_pages_per_split(hist_pages, layer.n_kv, RESIDUAL_PAGES, layer.device)
+        pages_per_split = choose_pages_per_split(hist_pages, layer.n_kv, res_pages, layer.device)
     plan = layer.decode_plan
-    if plan is None or plan.key != (tuple(hist_pages), pages_per_split, RESIDUAL_PAGES):
-        plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device, RESIDUAL_PAGES)
+    if plan is None or plan.key != (tuple(hist_pages), pages_per_split, res_pages):
+        plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device, res_pages)
         layer.decode_plan = plan
     lib = _native.load()
     nbytes = lib.lf_decode_workspace_bytes(manager.n_q * q_len, layer.head_dim, plan.n_work)

@@ -10,20 +10,21 @@ import heapq
 import pytest
 
 from logitfill_amd import _native, synth
-from logitfill_amd.packed.reference import ITEM_OVERHEAD_PAGES, RESIDUAL_PAGES, choose_pages_per_split
+from logitfill_amd.packed.reference import ITEM_OVERHEAD_PAGES, choose_pages_per_split, residual_pages
 
 SLOTS = 512  # 256 CUs x 2 workgroups
+RES = residual_pages([100])  # the c2 residual's cost (100-token tails)
 
 
-def plan_items(hist_pages, pps):
+def plan_items(hist_pages, pps, res=RES):
     """(b, page0, page1, flags) rows from lf_plan_decode."""
     lib = _native.load()
     B = len(hist_pages)
-    cap = sum(-(-(p + RESIDUAL_PAGES) // pps) for p in hist_pages) + B
+    cap = sum(-(-(p + res) // pps) for p in hist_pages) + B
     hp = (ctypes.c_int32 * B)(*hist_pages)
     work = (ctypes.c_int32 * (4 * cap))()
     seq = (ctypes.c_int32 * (2 * B))()
-    n = lib.lf_plan_decode(hp, B, pps, RESIDUAL_PAGES, work, cap, seq)
+    n = lib.lf_plan_decode(hp, B, pps, res, work, cap, seq)
     assert n > 0
     return [tuple(work[4 * i:4 * i + 4]) for i in range(n)]
 
@@ -32,24 +33,34 @@ def makespan(hist_pages, n_kv, pps):
     """Greedy list schedule of the plan's workgroups on SLOTS slots, in page units."""
     slots = [0.0] * SLOTS
     for b, p0, p1, flags in plan_items(hist_pages, pps):
-        cost = (p1 - p0) + (RESIDUAL_PAGES if flags else 0) + ITEM_OVERHEAD_PAGES
+        cost = (p1 - p0) + (RES if flags else 0) + ITEM_OVERHEAD_PAGES
         for _ in range(n_kv):
             t = heapq.heappop(slots)
             heapq.heappush(slots, t + cost)
     return max(slots)
 
 
-def one_round_size(hist_pages, n_kv):
-    return -(-n_kv * sum(p + RESIDUAL_PAGES for p in hist_pages) // SLOTS)
+def one_round_size(hist_pages, n_kv, res=RES):
+    return -(-n_kv * sum(p + res for p in hist_pages) // SLOTS)
 
 
-@pytest.mark.parametrize("hist_pages,n_kv,expect", [([256] * 16, 4, 33), ([64] * 8, 2, 3)])
-def test_uniform_batches_keep_one_round(hist_pages, n_kv, expect):
+def test_residual_cost_grows_with_the_tail():
+    """3 pages for the residual pass itself plus up to 4 for a full tail, from the longest
+    tail of the batch (known answers, and never below the fixed part)."""
+    assert [residual_pages([t]) for t in (0, 1, 15, 16, 37, 100, 127)] == [3, 3, 3, 4, 4, 6, 7]
+    assert residual_pages([]) == 3 and residual_pages([5, 100, 37]) == 6 and residual_pages([500]) == 7
+    costs = [residual_pages([t]) for t in range(128)]
+    assert costs == sorted(costs)
+
+
+@pytest.mark.parametrize("hist_pages,n_kv,tail,expect", [([256] * 16, 4, 100, 33), ([64] * 8, 2, 37, 3)])
+def test_uniform_batches_keep_one_round(hist_pages, n_kv, tail, expect):
     """c2 and c1: every sequence's work divides into the one-round size; the plan fills the
     slots exactly once."""
-    pps = choose_pages_per_split(hist_pages, n_kv)
-    assert pps == expect == one_round_size(hist_pages, n_kv)
-    assert n_kv * len(plan_items(hist_pages, pps)) <= SLOTS
+    res = residual_pages([tail])
+    pps = choose_pages_per_split(hist_pages, n_kv, res)
+    assert pps == expect == one_round_size(hist_pages, n_kv, res)
+    assert n_kv * len(plan_items(hist_pages, pps, res)) <= SLOTS
 
 
 def test_ragged_batch_avoids_the_second_round():
@@ -60,11 +71,11 @@ def test_ragged_batch_avoids_the_second_round():
     n_kv = 8
     top = one_round_size(pages, n_kv)
     assert n_kv * len(plan_items(pages, top)) > SLOTS
-    pps = choose_pages_per_split(pages, n_kv)
+    pps = choose_pages_per_split(pages, n_kv, RES)
     assert 1 <= pps < top
     chosen, naive = makespan(pages, n_kv, pps), makespan(pages, n_kv, top)
     assert chosen <= 0.75 * naive
-    bound = sum(n_kv * (p + RESIDUAL_PAGES) for p in pages) / SLOTS
+    bound = sum(n_kv * (p + RES) for p in pages) / SLOTS
     assert chosen <= 1.10 * (bound + ITEM_OVERHEAD_PAGES) + pps
 
 
@@ -76,12 +87,12 @@ def test_chosen_size_is_best_of_the_scan_by_simulation():
         n_kv = 8
         top = one_round_size(pages, n_kv)
         best = min(makespan(pages, n_kv, s) for s in range(max(1, top // 4), top + 1))
-        assert makespan(pages, n_kv, choose_pages_per_split(pages, n_kv)) <= 1.05 * best
+        assert makespan(pages, n_kv, choose_pages_per_split(pages, n_kv, RES)) <= 1.05 * best
 
 
 def test_edge_cases(monkeypatch):
-    assert choose_pages_per_split([0], 1) == 1
-    assert choose_pages_per_split([0, 0, 3], 2) >= 1
-    assert choose_pages_per_split([512], 8) == one_round_size([512], 8)
+    assert choose_pages_per_split([0], 1, RES) == 1
+    assert choose_pages_per_split([0, 0, 3], 2, RES) >= 1
+    assert choose_pages_per_split([512], 8, RES) == one_round_size([512], 8)
     monkeypatch.setenv("LOGITFILL_AMD_PAGES_PER_SPLIT", "7")
-    assert choose_pages_per_split([256] * 16, 4) == 7
+    assert choose_pages_per_split([256] * 16, 4, RES) == 7
