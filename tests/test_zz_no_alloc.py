@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from logitfill_amd import _native
-from logitfill_amd.packed.reference import DecodePlan, decode_into
+from logitfill_amd.packed.reference import DecodePlan, decode_into, residual_pages
 from tests.test_gpu_fullsize import _build
 
 pytestmark = pytest.mark.gpu
@@ -59,7 +59,7 @@ def test_noalloc_refuses_partials_beyond_the_array(gpu):
     d, m = _build(gpu, 1, 28, 4, [4], [2], 2.5, seed=34)
     layer = m.layers[0]
     n_work = limit // lib.lf_decode_workspace_bytes(28, 128, 1) + 1       # one item past the limit
-    plan = DecodePlan([4], 4, 1, gpu)
+    plan = DecodePlan([4], 4, 1, gpu, residual_pages([2]))
     a = _native.DecodeArgs()
     a.query, a.q_dtype = d.query.data_ptr(), _native.LF_BF16
     a.out, a.out_dtype = d.query.data_ptr(), _native.LF_BF16
