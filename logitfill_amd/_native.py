@@ -146,22 +146,32 @@ def check(status: int, call: str) -> None:
         raise LFError(status, msg.decode() if msg else "?", call)
 
 
-def dtype_code(dtype) -> int:
-    import torch
+_DTYPE_CODES: dict = {}
 
-    if dtype == torch.bfloat16:
-        return LF_BF16
-    if dtype == torch.float16:
-        return LF_FP16
-    if dtype == torch.float32:
-        return LF_FP32
-    raise TypeError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32")
+
+def dtype_code(dtype) -> int:
+    if not _DTYPE_CODES:
+        import torch
+
+        _DTYPE_CODES.update({torch.bfloat16: LF_BF16, torch.float16: LF_FP16, torch.float32: LF_FP32})
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32") from None
 
 
 def current_stream_ptr(device) -> int:
+    """The raw hipStream_t of the current stream on ``device`` (torch's C accessor when this
+    build has it: no Stream object per call, which the per-layer decode path would pay twice)."""
     import torch
 
-    return int(torch.cuda.current_stream(device).cuda_stream)
+    index = device.index if isinstance(device, torch.device) else device
+    if index is None:
+        index = torch.cuda.current_device()
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return int(raw(index))
+    return int(torch.cuda.current_stream(index).cuda_stream)
 
 
 def upload(data, dtype, device):

@@ -203,47 +203,66 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
         _expect(value_new, (B, manager.n_kv, *tok, D), "value_new")
     kernel = kernel_choice() if kernel is None else kernel
     P = layer.page_size
-    hist_pages = [h // P for h in layer.hist_lens]
+    hist_pages = tuple(h // P for h in layer.hist_lens)
     res_pages = residual_pages(layer.tail_lens)
     if pages_per_split is None:
-        pages_per_split = choose_pages_per_split(hist_pages, layer.n_kv, res_pages, layer.device)
+        # the split size depends on the history, the residual cost and the environment's
+        # override only: chosen again when one of them changes
+        choice_key = (hist_pages, res_pages, os.environ.get("LOGITFILL_AMD_PAGES_PER_SPLIT"))
+        cached = layer.__dict__.get("_lf_split_choice")
+        if cached is None or cached[0] != choice_key:
+            cached = (choice_key, choose_pages_per_split(list(hist_pages), layer.n_kv, res_pages, layer.device))
+            layer.__dict__["_lf_split_choice"] = cached
+        pages_per_split = cached[1]
     plan = layer.decode_plan
-    if plan is None or plan.key != (tuple(hist_pages), pages_per_split, res_pages):
-        plan = DecodePlan(hist_pages, layer.n_kv, pages_per_split, layer.device, res_pages)
+    if plan is None or plan.key != (hist_pages, pages_per_split, res_pages):
+        plan = DecodePlan(list(hist_pages), layer.n_kv, pages_per_split, layer.device, res_pages)
         layer.decode_plan = plan
     lib = _native.load()
     nbytes = lib.lf_decode_workspace_bytes(manager.n_q * q_len, layer.head_dim, plan.n_work)
     ws = None if noalloc else manager.workspace(nbytes)
     tail_k, tail_v = layer.tail_buffers()
-    a = _native.DecodeArgs()
-    a.query = query.data_ptr()
-    a.q_dtype = _native.dtype_code(query.dtype)
-    if key_new is not None:
-        a.k_new = key_new.data_ptr()
-        a.v_new = value_new.data_ptr()
-        a.new_dtype = _native.dtype_code(key_new.dtype)
-        if value_new.dtype != key_new.dtype:
-            raise TypeError("key_new and value_new must share a dtype")
-    if tail_k is not None:
-        a.tail_k = tail_k.data_ptr()
-        a.tail_v = tail_v.data_ptr()
-        a.tail_dtype = _native.dtype_code(tail_k.dtype)
-        a.tail_cap = int(tail_k.shape[2])
+    if key_new is not None and value_new.dtype != key_new.dtype:
+        raise TypeError("key_new and value_new must share a dtype")
+    tail_len = layer.tail_len_device()
+    # Every field but the four per-call tensors is fixed while the plan, the buffers and the
+    # call's settings stay the same: the argument block is kept on the layer and reused.
+    static_key = (plan, None if ws is None else (ws.data_ptr(), ws.numel()),
+                  None if tail_k is None else (tail_k.data_ptr(), tail_v.data_ptr(), tail_k.dtype, int(tail_k.shape[2])),
+                  tail_len.data_ptr(), query.dtype, out.dtype, None if key_new is None else key_new.dtype,
+                  manager.n_q, float(scaling), kernel, q_len)
+    cached_args = layer.__dict__.get("_lf_decode_args")
+    if cached_args is not None and cached_args[0] == static_key:
+        a = cached_args[1]
     else:
-        a.tail_dtype = _native.LF_BF16
-        a.tail_cap = 0
-    a.tail_len = layer.tail_len_device().data_ptr()
+        a = _native.DecodeArgs()
+        a.q_dtype = _native.dtype_code(query.dtype)
+        if key_new is not None:
+            a.new_dtype = _native.dtype_code(key_new.dtype)
+        if tail_k is not None:
+            a.tail_k = tail_k.data_ptr()
+            a.tail_v = tail_v.data_ptr()
+            a.tail_dtype = _native.dtype_code(tail_k.dtype)
+            a.tail_cap = int(tail_k.shape[2])
+        else:
+            a.tail_dtype = _native.LF_BF16
+            a.tail_cap = 0
+        a.tail_len = tail_len.data_ptr()
+        a.out_dtype = _native.dtype_code(out.dtype)
+        a.n_q = manager.n_q
+        a.scaling = float(scaling)
+        a.work = plan.work.data_ptr()
+        a.n_work = plan.n_work
+        a.seq_work = plan.seq_work.data_ptr()
+        a.workspace = 0 if ws is None else ws.data_ptr()
+        a.workspace_bytes = 0 if ws is None else ws.numel()
+        a.kernel = kernel
+        a.q_len = q_len
+        layer.__dict__["_lf_decode_args"] = (static_key, a)
+    a.query = query.data_ptr()
     a.out = out.data_ptr()
-    a.out_dtype = _native.dtype_code(out.dtype)
-    a.n_q = manager.n_q
-    a.scaling = float(scaling)
-    a.work = plan.work.data_ptr()
-    a.n_work = plan.n_work
-    a.seq_work = plan.seq_work.data_ptr()
-    a.workspace = 0 if ws is None else ws.data_ptr()
-    a.workspace_bytes = 0 if ws is None else ws.numel()
-    a.kernel = kernel
-    a.q_len = q_len
+    a.k_new = 0 if key_new is None else key_new.data_ptr()
+    a.v_new = 0 if key_new is None else value_new.data_ptr()
     stream = _native.current_stream_ptr(layer.device)
     if noalloc:
         st = lib.lf_decode_attention_noalloc(layer.layer_struct(), a, stream)
