@@ -312,9 +312,11 @@ int pack_code_row(const lf_packed_layer& L);
 // clamp-free magic_code.  The phases are listed at pack_fast_page.  Each integer tier has a 16-byte aligned segment of a token's code row (in
 // slot order), so a word's 16 / 8 / 4 code bytes are one LDS read.
 // ---------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
 constexpr int kFastThreads = 512;
 constexpr int kFastP = 128;
-constexpr int kFastLd = 130;  // halves per staged row
+constexpr int kFastLd = 128;  // halves per staged row (unpadded: phase 1 reads one row per wave instruction)
 
 // a / s rounded to nearest even from y = RN(1/s) (Markstein: q0 = RN(a*y) is within an ulp of
 // a/s, the residual a - q0*s is exact by FMA, and RN(q0 + r*y) is the correctly rounded
@@ -527,8 +529,8 @@ __device__ __host__ inline int code_ld(const lf_packed_layer& L) {
     return code_segs(L).seg[3] <= kCodeLdNarrow ? kCodeLdNarrow : kCodeLdWide;
 }
 
-// LDS layout of the Key workgroup: the code rows (the staged page, rows padded to 130 halves,
-// lies in their first 33 KB until phase 1 has read it), partial min/max, the channel map, the
+// LDS layout of the Key workgroup: the code rows (the staged page, 128 rows of 256 bytes,
+// lies in their first 32 KB until phase 1 has read it), partial min/max, the channel map, the
 // fp16 tier's channels.
 struct FastLds {
     int pmm, cpos, tidx, total;
@@ -586,7 +588,7 @@ __device__ __forceinline__ void tier_words(const uint8_t* codes, int seg, int kw
 // written as page ``page`` of sequence b.  512 threads: four workgroups share a CU.
 //   Value page  quad per token row (tid / 4), 32 channels per lane, read from global memory
 //               directly (LDS only gathers the page's scales and mins)
-//   Key page    stage (page -> LDS, tier tables -> channel map); phase 1: thread (channel
+//   Key page    stage (page -> LDS by LDS-DMA, tier tables -> channel map); phase 1: thread (channel
 //               tid % 128, tokens 32 (tid / 128) + 0..31) min/max, the fp16 tier copied from
 //               the staged page; phases 2, 3: the channel's scale and its 32 codes into byte
 //               rows over the page; phase 4: the tiers' words (tier_words)
@@ -608,7 +610,7 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
 
     const FastLds fl = fast_lds(Ld, L.k_width[3]);
     uint8_t* codes = smem;                                                  // [128][Ld] code bytes
-    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                  // [128][130]: the page, read
+    uint16_t* kpage = reinterpret_cast<uint16_t*>(smem);                  // [128][128]: the page, read
                                                                             // before the codes replace it
     float2* pmm = reinterpret_cast<float2*>(smem + fl.pmm);                // [4][128] partial (lo, hi)
     int16_t* cpos = reinterpret_cast<int16_t*>(smem + fl.cpos);            // [128] code byte of a channel,
@@ -621,12 +623,24 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     // ---- stage the page and this head's tier tables (layout.py:49-68): all their global loads
     // go out before the first wait ----
     {
-        const uint16_t* src = static_cast<const uint16_t*>(k_src) + b * sb + h * sh + tok0 * st;
-        uint4 kv[4];
+        // The page by LDS-DMA (buffer_load_dwordx4 ... lds): wave w's instruction i moves 1 KB
+        // block k = 4 w + i, rows 4 k .. 4 k + 3, lane l's 16 bytes landing at 1024 k + 16 l.  The
+        // row offset is the scalar soffset (rows are st apart in the source), the lane's part a
+        // VGPR shared by the four instructions; the buffer word 3 0x00020000 (DATA_FORMAT 32)
+        // is the gfx9 value for untyped accesses.  Offsets stay below 2^31 (st <= 2^22, checked
+        // by the launcher).
+        {
+            const uint16_t* src = static_cast<const uint16_t*>(k_src) + b * sb + h * sh + tok0 * st;
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(src), 0, 0x7fffffff, 0x00020000);
+            const int st2 = static_cast<int>(st) * 2;
+            const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+            const int voff = (lane >> 4) * st2 + 16 * (lane & 15);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = tid + kFastThreads * i;  // 16-byte chunk: row idx / 16, column 8 (idx % 16)
-            kv[i] = *reinterpret_cast<const uint4*>(src + (idx >> 4) * st + 8 * (idx & 15));
+            for (int i = 0; i < 4; ++i) {
+                const int k = 4 * wave + i;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(smem + 1024 * k), 16, voff, 4 * k * st2, 0, 0);
+            }
         }
         // slot tid of tier t: its channel and the tier's count for head h (wall <= 512).
         // Constant indices into the layer descriptor only (a lane-dependent one would copy it to
@@ -636,13 +650,6 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
         else if (tid < koff2) { my_idx = L.tier_index[1][h * w1 + tid - koff1]; my_cnt = L.tier_count[1][h]; }
         else if (tid < nslots) { my_idx = L.tier_index[2][h * w2 + tid - koff2]; my_cnt = L.tier_count[2][h]; }
         else if (tid < wall) { my_idx = L.tier_index[3][h * w16 + tid - nslots]; my_cnt = L.tier_count[3][h]; }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = tid + kFastThreads * i;
-            // rows are 260 bytes apart: 4-byte aligned, so four dword stores
-            uint32_t* kd = reinterpret_cast<uint32_t*>(kpage + (idx >> 4) * kFastLd + 8 * (idx & 15));
-            kd[0] = kv[i].x; kd[1] = kv[i].y; kd[2] = kv[i].z; kd[3] = kv[i].w;
-        }
         // channel map: every channel sits in exactly one tier (rank < count), so every entry is
         // written once; padding slots (rank >= count): scale 1.0, min 0.0, code 0 (layout.py:84-85)
         if (tid < wall) {
