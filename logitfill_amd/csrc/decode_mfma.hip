@@ -34,12 +34,15 @@
 // vmin - 4 * vscale enters through sum_t p_t * mid_t.  Value codes are
 // regrouped per page (one dword = one byte column of 4 consecutive tokens) so
 // each lane's 8 codes for one 16-channel tile are two LDS dwords.
+#include <type_traits>
+
 #include "decode_common.hpp"
 
 namespace lf {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
@@ -161,6 +164,7 @@ struct MfmaParams {
     DecodeParams p;
     MfmaLayout y;
     UnpackBits k;
+    int res_mfma;  // residual pass: 0 VALU, 1 bf16 matrix cores, 2 fp16 matrix cores (residual_mfma)
 };
 
 // Tier-local rank of position ``pos`` (0..7) of local block ``lb``.  Register r of a
@@ -721,6 +725,176 @@ __device__ __forceinline__ void score_tiles_fixed(const KTiles& t, const UnpackB
     acc1 = acc[1];
 }
 
+// Residual pass on the matrix cores, for 2-byte tail and new-token rows of one dtype (Bf: bf16,
+// else fp16) with 16-byte aligned rows.  The residual is one dense page: token tt < tl is tail
+// row tt, token tl the new token, tokens past them are masked (rows read for them are the new
+// row, or tail row 0 when there is none, so every value read is a stored one).  Wave w takes
+// tokens 32w..32w+31 as two 16-row tiles:
+//   scores  S^T = K . Qb^T: the A operand (lane: token row n16, channels 32 kb + 8 s .. + 7 of
+//           K-step s) straight from global memory; Qb = the LDS query (q * scaling * log2 e)
+//           split hi (columns 0..7) / lo (columns 8..15), recombined by one DPP add;
+//   values  O = P . V with P = 2^(s - m) split hi (rows 0..7) / lo (rows 8..15): the score
+//           accumulator layout is the A-operand layout; the wave's 32 V rows arrive by LDS-DMA
+//           into its own 8 KB of ``vst`` and each lane gathers its 8 tokens of one channel.
+// One pass per wave (its max is final); the wave's (m, l, o) go to partial slot ``rw`` with a
+// zero midpoint term.  ``vst`` may overlap partial slots other than 0..3: the stores wait for
+// every wave's last V read.
+template <bool Bf>
+__device__ __forceinline__ void residual_mfma(const DecodeParams& p, int b, int h, int rw, int tl, float* qlin,
+                                              float* red, float* wstat, unsigned char* vst, int tid) {
+    using T8 = typename std::conditional<Bf, bf16x8, half8>::type;
+    const lf_decode_args& A = p.A;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n16 = lane & 15, kb = lane >> 4;
+    const bool has_new = A.k_new != nullptr;
+    const int n_res = tl + (has_new ? 1 : 0);
+    const int64_t bh = static_cast<int64_t>(b) * p.L.n_kv + h;
+    const uint16_t* tk = static_cast<const uint16_t*>(A.tail_k) + bh * A.tail_cap * kD;
+    const uint16_t* tv = static_cast<const uint16_t*>(A.tail_v) + bh * A.tail_cap * kD;
+    const uint16_t* fk = has_new ? static_cast<const uint16_t*>(A.k_new) + bh * kD : tk;
+    const uint16_t* fv = has_new ? static_cast<const uint16_t*>(A.v_new) + bh * kD : tv;
+    float O[8][4];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[nt][r] = 0.f;
+    float mx = -__builtin_inff(), lsum = 0.f;
+    if (n_res > 0) {  // uniform over the workgroup
+        // V rows by LDS-DMA: instruction i moves rows 32 w + 4 i .. + 3 (16 lanes per row)
+        const uint32_t vbase = lds_addr(vst) + 8192 * wave;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int tt = 32 * wave + 4 * i + (lane >> 4);
+            const uint16_t* row = tt < tl ? tv + static_cast<int64_t>(tt) * kD : fv;
+            dma16(reinterpret_cast<const unsigned char*>(row + 8 * (lane & 15)), vbase + 1024 * i);
+        }
+        uint4 ka[2][4];
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile) {
+            const int tt = 32 * wave + 16 * tile + n16;
+            const uint4* row = reinterpret_cast<const uint4*>((tt < tl ? tk + static_cast<int64_t>(tt) * kD : fk) + 32 * kb);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) ka[tile][s] = row[s];
+        }
+        load_q(p, b, h, qlin, tid);  // its wait also covers the K and V loads: one round trip
+        __syncthreads();             // q in LDS
+        T8 bq[4];
+        {
+            const float4* q4 = reinterpret_cast<const float4*>(qlin + (n16 & 7) * kD + 32 * kb);
+            const bool lo = n16 >= 8;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const float4 a = q4[2 * s], c = q4[2 * s + 1];
+                const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if constexpr (Bf) {
+                        const __bf16 hi = static_cast<__bf16>(x[j]);
+                        bq[s][j] = lo ? static_cast<__bf16>(x[j] - static_cast<float>(hi)) : hi;
+                    } else {
+                        const _Float16 hi = static_cast<_Float16>(x[j]);
+                        bq[s][j] = lo ? static_cast<_Float16>(x[j] - static_cast<float>(hi)) : hi;
+                    }
+                }
+            }
+        }
+        float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if constexpr (Bf) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[0][s]), bq[s], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[1][s]), bq[s], acc1, 0, 0, 0);
+            } else {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[0][s]), bq[s], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[1][s]), bq[s], acc1, 0, 0, 0);
+            }
+        }
+        // hi + lo columns (lanes n16 < 8: head n16, tokens 4 kb + r of each tile); masked -inf
+        const int tb = 32 * wave + 4 * kb;
+        const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
+        float sv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int xi = __builtin_bit_cast(int, accs[r]);
+            const float sum = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
+            sv[r] = tb + (r & 3) + 16 * (r >> 2) < n_res ? sum : -__builtin_inff();
+        }
+        mx = sv[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+        mx = rows_max(mx);
+        const float moff = mx == -__builtin_inff() ? 0.f : mx;
+        float pp[8], psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            pp[i] = __builtin_amdgcn_exp2f(sv[i] - moff);
+            psum += pp[i];
+        }
+        lsum = rows_sum(psum);
+        // A operand: k = 8 kb + j <-> token 4 kb + j (tile 0, j < 4) / 16 + 4 kb + j - 4 (tile 1);
+        // hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8
+        uint32_t ahi[4], alo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float x0 = pp[2 * j], x1 = pp[2 * j + 1];
+            uint16_t hb[2], lb[2];
+            if constexpr (Bf) {
+                const __bf16 h0 = static_cast<__bf16>(x0), h1 = static_cast<__bf16>(x1);
+                const __bf16 l0 = static_cast<__bf16>(x0 - static_cast<float>(h0)), l1 = static_cast<__bf16>(x1 - static_cast<float>(h1));
+                hb[0] = __builtin_bit_cast(uint16_t, h0); hb[1] = __builtin_bit_cast(uint16_t, h1);
+                lb[0] = __builtin_bit_cast(uint16_t, l0); lb[1] = __builtin_bit_cast(uint16_t, l1);
+            } else {
+                const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
+                const _Float16 l0 = static_cast<_Float16>(x0 - static_cast<float>(h0)), l1 = static_cast<_Float16>(x1 - static_cast<float>(h1));
+                hb[0] = __builtin_bit_cast(uint16_t, h0); hb[1] = __builtin_bit_cast(uint16_t, h1);
+                lb[0] = __builtin_bit_cast(uint16_t, l0); lb[1] = __builtin_bit_cast(uint16_t, l1);
+            }
+            ahi[j] = hb[0] | (static_cast<uint32_t>(hb[1]) << 16);
+            alo[j] = lb[0] | (static_cast<uint32_t>(lb[1]) << 16);
+        }
+        uint4 au;
+        au.x = __builtin_amdgcn_update_dpp(ahi[0], alo[0], 0x118, 0xf, 0xc, false);
+        au.y = __builtin_amdgcn_update_dpp(ahi[1], alo[1], 0x118, 0xf, 0xc, false);
+        au.z = __builtin_amdgcn_update_dpp(ahi[2], alo[2], 0x118, 0xf, 0xc, false);
+        au.w = __builtin_amdgcn_update_dpp(ahi[3], alo[3], 0x118, 0xf, 0xc, false);
+        // this wave's V rows have landed (the barrier above waited for all of its vector memory)
+        const uint16_t* vs = reinterpret_cast<const uint16_t*>(vst + 8192 * wave);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+            const int c = 16 * nt + n16;
+            uint16_t e[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) e[j] = vs[(4 * kb + (j & 3) + 16 * (j >> 2)) * kD + c];
+            const uint4 bu = {e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16),
+                              e[4] | (static_cast<uint32_t>(e[5]) << 16), e[6] | (static_cast<uint32_t>(e[7]) << 16)};
+            float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
+            if constexpr (Bf)
+                o4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, au), __builtin_bit_cast(bf16x8, bu), o4, 0, 0, 0);
+            else
+                o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, au), __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
+            O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
+        }
+        // rows r (hi) + r + 8 (lo): lanes kb < 2 hold heads 4 kb + r
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) O[nt][r] = halves_sum(O[nt][r]);
+    }
+    __syncthreads();  // every wave's V reads are done (vst may overlap partial slots)
+    if (kb < 2) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(rw * 8 + 4 * kb + r) * kD + 16 * nt + n16] = O[nt][r];
+    }
+    if (kb == 0 && n16 < 8) {
+        wstat[(rw * 3 + 0) * 8 + n16] = mx;
+        wstat[(rw * 3 + 1) * 8 + n16] = lsum;
+        wstat[(rw * 3 + 2) * 8 + n16] = 0.f;
+    }
+    __syncthreads();
+}
+
 __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
     const DecodeParams& p = mp.p;
     const MfmaLayout& y = mp.y;
@@ -763,8 +937,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
 
     if (kind != 1) {
         // ---- pages (kind 0, 2) ----
-        // The first page's DMA goes out first; q, the tier table and the permuted q are built
-        // while it is in flight (the DMA target does not overlap q).
         const LoopY z = loop_y(y);
         DmaSrc ds;
         dma_setup(ds, L, y, b, h, pbeg, wave, lane);
@@ -774,21 +946,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         dma_page(ds, raw_lds, z, pbeg, wave);
 
         // ---- q permuted into slot order ----
-        // K-step i of the layout holds blocks 4i .. 4i+3, one per wave: wave w's lane (n, pos)
-        // takes slot pos of block 4i + w for head n.  The slot's channel comes from the tier
-        // table in global memory (no LDS staging) and q is gathered from global memory the
-        // same way, so the whole set-up is two rounds of loads that overlap the first page's
-        // DMA; nothing here waits for that DMA (the page loop's first barrier does).  Integer
-        // tiers go to qperm (0 for padding slots and heads >= g); the fp16 tier's Qs (plain q,
-        // hi / lo) is written once into the prepared buffer, which no page rewrites.
+        // K-step i of the layout holds blocks 4i .. 4i+3.  Thread tid owns block gb = tid / 4
+        // (K-step gb / 4) for heads 2 (tid % 4) and 2 (tid % 4) + 1, all 8 slot positions: the
+        // slots' channels come from the tier table in global memory and q is gathered from
+        // global memory -- two rounds of loads while the first page's DMA is in flight (nothing
+        // here waits for the DMA explicitly; the page loop's first barrier does).  Integer tiers
+        // go to qperm (0 for padding slots and heads >= g); the fp16 tier's Qs (plain q, hi / lo)
+        // goes into the prepared buffer, which no page rewrites; Qs rows of heads >= g start at 0.
+        // (Issuing the DMA from two waves and the set-up from the other two, so that the set-up's
+        // load waits do not cover the DMA, measured slower: c2 92.5 against 90.3 us.)
         {
-            // Thread tid owns block gb = tid / 4 (K-step gb / 4) for heads 2 (tid % 4) and
-            // 2 (tid % 4) + 1, all 8 slot positions: the slots' channels come from the tier table
-            // in global memory and q is gathered from global memory -- two rounds of loads that
-            // overlap the first page's DMA (nothing here waits for it; the page loop's first
-            // barrier does).  Integer tiers go to qperm (0 for padding slots and heads >= g);
-            // the fp16 tier's Qs (plain q, hi / lo) goes into the prepared buffer, which no page
-            // rewrites; Qs rows of heads >= g start at 0.
             const int ks = z.kst0 + z.kst1 + z.kst2 + z.kst3;
             const int gb = tid >> 2, n0 = 2 * (tid & 3);
             const int i = gb >> 2;
@@ -1047,7 +1214,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         }
         __syncthreads();
     }
-    if (kind != 0) {
+    if (kind != 0 && mp.res_mfma != 0) {
+        // ---- residual (kind 1, 2) on the matrix cores; its V staging starts at partial slot 4 ----
+        const int rw = kind == 2 ? wave + kWaves : wave;
+        const int cap = min(A.tail_cap, kPage);
+        const int tl = min(max(A.tail_len[b], 0), min(cap, kPage - 1));
+        unsigned char* vst = reinterpret_cast<unsigned char*>(red + kWaves * 8 * kD);
+        if (mp.res_mfma == 1) residual_mfma<true>(p, b, h, rw, tl, qlin, red, wstat, vst, tid);
+        else residual_mfma<false>(p, b, h, rw, tl, qlin, red, wstat, vst, tid);
+    } else if (kind != 0) {
         // ---- residual (kind 1, 2): the tail page and the new token (at most page_size tokens) ----
         // VALU: wave w scores tokens 32w..32w+31 (lane % 32 = token, lane / 32 = channel half;
         // q read as float4 from LDS), then accumulates them into channels 2*lane, 2*lane+1.
@@ -1286,8 +1461,10 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     y.off_raw = off;
     off += 2 * y.slot_bytes;
     // q [8][128], wave partial outputs [2 * waves][8][128] and residual probabilities
-    // [waves][32][8] alias the prepared buffer and the page slots
-    const int alias_bytes = (8 + 2 * kWaves * 8) * kD * 4 + kWaves * 32 * 8 * 4;
+    // [waves][32][8] alias the prepared buffer and the page slots; so does the matrix-core
+    // residual's V staging [waves][32][128] 2-byte rows from partial slot 4 on
+    const int alias_bytes = std::max((8 + 2 * kWaves * 8) * kD * 4 + kWaves * 32 * 8 * 4,
+                                     (8 + kWaves * 8) * kD * 4 + kWaves * 32 * kD * 2);
     if (off - y.off_ck < alias_bytes) off = y.off_ck + alias_bytes;
     y.lds_bytes = off;
     return y.lds_bytes <= 160 * 1024 - 64;
@@ -1302,6 +1479,14 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
     // The residual pass reads 16-byte Key chunks and 4-byte Value pairs of the tail and new rows.
     const bool rows_aligned = (p.A.tail_cap == 0 || (aligned(p.A.tail_k, 16) && aligned(p.A.tail_v, 4))) &&
                               (!p.A.k_new || (aligned(p.A.k_new, 16) && aligned(p.A.v_new, 4)));
+    // The residual on the matrix cores: 2-byte rows of one dtype, every row 16-byte aligned (the
+    // V rows go to LDS by 16-byte DMA); otherwise the VALU pass.
+    const bool has_tail = p.A.tail_cap > 0, has_new = p.A.k_new != nullptr;
+    const int res_dt = has_tail ? p.A.tail_dtype : p.A.new_dtype;
+    const bool one_dtype = !has_tail || !has_new || p.A.new_dtype == p.A.tail_dtype;
+    const bool rows16 = (!has_tail || (aligned(p.A.tail_k, 16) && aligned(p.A.tail_v, 16))) &&
+                        (!has_new || (aligned(p.A.k_new, 16) && aligned(p.A.v_new, 16)));
+    mp.res_mfma = (has_tail || has_new) && one_dtype && rows16 && res_dt != LF_FP32 ? (res_dt == LF_BF16 ? 1 : 2) : 0;
     if (!rows_aligned || !plan_layout(p.L, p.g, mp.y)) {
         *handled = false;
         return LF_OK;

@@ -96,17 +96,17 @@ def _cu_count(device) -> int:
 
 # Decode time of one sequence's residual (the BF16 tail page and the new token) in packed
 # pages, for balancing the split-K items: a fixed part (the residual pass's load round, its
-# scores and the merge of its wave partials) and a part that grows with the tail, taken from
-# the batch's longest tail (lf_plan_decode takes one cost for every sequence).  Measured with
-# the cost forced, 28 layers: c2 (100-token tails) 88.2-88.8 us per layer-step at 5-8 pages,
-# 92.2 at 3, 90.1 at 12; c1 (37-token tails, 3-page items) 24.0-24.1 us at every cost from 3
-# up (the residual is then an item of its own) and 30.5 at 1-2.
+# matrix-core page and the merge of its wave partials) and a part that grows with the tail, taken
+# from the batch's longest tail (lf_plan_decode takes one cost for every sequence).  Measured with
+# the cost forced, 28 layers: c2 (100-token tails) 88.5-89.0 us per layer-step for 2-8 pages and
+# 90.5 at 1; c1 (37-token tails, 3-page items) 24.2-24.4 us for 2-8 pages, best from 3 up (the
+# residual is then an item of its own).
 RESIDUAL_FIXED_PAGES = 3
-RESIDUAL_TAIL_PAGES = 4  # added for a full 127-token tail
+RESIDUAL_TAIL_PAGES = 1  # added for a tail of 64 tokens or more
 
 
 def residual_pages(tail_lens) -> int:
-    """Residual cost in pages for the longest of ``tail_lens``: 3 + round(4 * tail / 127)."""
+    """Residual cost in pages for the longest of ``tail_lens``: 3 + round(tail / 127)."""
     t = min(max(max(tail_lens, default=0), 0), 127)
     return RESIDUAL_FIXED_PAGES + (RESIDUAL_TAIL_PAGES * t + 63) // 127
 

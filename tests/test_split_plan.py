@@ -45,10 +45,10 @@ def one_round_size(hist_pages, n_kv, res=RES):
 
 
 def test_residual_cost_grows_with_the_tail():
-    """3 pages for the residual pass itself plus up to 4 for a full tail, from the longest
-    tail of the batch (known answers, and never below the fixed part)."""
-    assert [residual_pages([t]) for t in (0, 1, 15, 16, 37, 100, 127)] == [3, 3, 3, 4, 4, 6, 7]
-    assert residual_pages([]) == 3 and residual_pages([5, 100, 37]) == 6 and residual_pages([500]) == 7
+    """3 pages for the residual pass itself plus one for a tail of 64 tokens or more, from the
+    longest tail of the batch (known answers, and never below the fixed part)."""
+    assert [residual_pages([t]) for t in (0, 1, 37, 63, 64, 100, 127)] == [3, 3, 3, 3, 4, 4, 4]
+    assert residual_pages([]) == 3 and residual_pages([5, 100, 37]) == 4 and residual_pages([500]) == 4
     costs = [residual_pages([t]) for t in range(128)]
     assert costs == sorted(costs)
 
