@@ -1,0 +1,78 @@
+"""The split merge of the packed decode (the reduce kernel over the splits' softmax partials)
+against the oracle (reference src/logitfill/packed/reference.py:30-56 over [history ; tail ;
+new]): forced split sizes that give every sequence 1 .. 12 items, and layers decoded back to
+back on one stream whose partials reuse the same workspace addresses."""
+import pytest
+import torch
+
+from logitfill_amd import _native, synth
+from logitfill_amd.packed import PackedKVManager
+from logitfill_amd.packed.reference import decode_into
+from oracle import attention as oatt
+from tests.helpers import assert_decode_close, f32
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def _check_against_oracle(st, d, out, seqs, levels, n_q, n_kv, tail):
+    tk, tv = st.tail_buffers()
+    for b in seqs:
+        hk, hv = st.export_reference(b)
+        hk = {t: {k: v.cpu().numpy() for k, v in x.items()} for t, x in hk.items()} if hk is not None else None
+        hv = {k: v.cpu().numpy() for k, v in hv.items()} if hv is not None else None
+        store = oatt.ExportedHistory(levels, hk, hv, st.hist_lens[b], f32(tk[b, :, :tail]), f32(tv[b, :, :tail]),
+                                     128, 128, 2)
+        ref = oatt.reference_attention(store, f32(d.query[b])[:, None, :], f32(d.key_new[b])[:, None, :],
+                                       f32(d.value_new[b])[:, None, :], D ** -0.5, n_q, n_kv)[:, 0, :]
+        print(f"merge: sequence {b}", flush=True)
+        assert_decode_close(out[b], ref, out_dtype="fp32")
+
+
+def _layer(gpu, B, n_q, n_kv, pages, tail, seed):
+    d = synth.make_layer(B, n_q, n_kv, D, pages * 128 + 128, 2.5, seed=seed, device=gpu)
+    mgr = PackedKVManager([d.levels], n_q, n_kv, D, 128, 128, 128, 2, gpu, batch_size=B,
+                          capacity_tokens=max(pages, 1) * 128)
+    st = mgr.layers[0]
+    if pages:
+        st.fill_pages(d.key, d.value, [pages] * B)
+    st.set_tail(d.key[:, :, pages * 128:pages * 128 + 127], d.value[:, :, pages * 128:pages * 128 + 127], [tail] * B)
+    return d, mgr, st
+
+
+@pytest.mark.parametrize("pps", [1, 3, None])
+def test_split_sizes_merge_to_the_oracle(gpu, pps):
+    """Sequences split into 1-page items (12 + the residual's), 3-page items and the planner's
+    size, the matrix-core kernel; two calls in a row on the same workspace."""
+    B, n_q, n_kv, pages, tail = 4, 28, 4, 12, 45
+    d, mgr, st = _layer(gpu, B, n_q, n_kv, pages, tail, seed=71)
+    out = torch.empty(B, n_q, D, dtype=torch.float32, device=gpu)
+    for _ in range(2):
+        decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=_native.KERNEL_MFMA,
+                    pages_per_split=pps)
+        torch.cuda.synchronize()
+    _check_against_oracle(st, d, out, range(B), d.levels, n_q, n_kv, tail)
+
+
+def test_back_to_back_layers_share_the_workspace(gpu):
+    """Six layers decoded back to back on one stream with no synchronisation between them: each
+    layer's splits write their partials to the same workspace addresses as the layer before
+    (on whatever XCD they land) and each layer's merge must read its own layer's values."""
+    B, n_q, n_kv, pages, tail, n_layers = 6, 28, 4, 9, 30, 6
+    ds = [synth.make_layer(B, n_q, n_kv, D, pages * 128 + 128, 2.5, seed=80 + l, device=gpu) for l in range(n_layers)]
+    mgr = PackedKVManager([d.levels for d in ds], n_q, n_kv, D, 128, 128, 128, 2, gpu, batch_size=B,
+                          capacity_tokens=pages * 128)
+    for l, d in enumerate(ds):
+        st = mgr.layers[l]
+        st.fill_pages(d.key, d.value, [pages] * B)
+        st.set_tail(d.key[:, :, pages * 128:pages * 128 + 127], d.value[:, :, pages * 128:pages * 128 + 127], [tail] * B)
+    outs = [torch.empty(B, n_q, D, dtype=torch.float32, device=gpu) for _ in range(n_layers)]
+    torch.cuda.synchronize()
+    for l, d in enumerate(ds):
+        decode_into(mgr, l, d.query, d.key_new, d.value_new, D ** -0.5, outs[l], kernel=_native.KERNEL_MFMA,
+                    pages_per_split=2)
+    torch.cuda.synchronize()
+    for l, d in enumerate(ds):
+        print(f"merge: layer {l}", flush=True)
+        _check_against_oracle(mgr.layers[l], d, outs[l], [0, B - 1], d.levels, n_q, n_kv, tail)
