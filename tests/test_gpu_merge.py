@@ -55,6 +55,27 @@ def test_split_sizes_merge_to_the_oracle(gpu, pps):
     _check_against_oracle(st, d, out, range(B), d.levels, n_q, n_kv, tail)
 
 
+def test_ragged_items_divisible_by_the_batch(gpu):
+    """Sequences of 9 and 1 pages at 3 pages per item: 4 + 2 items, a total the batch divides
+    although the sequences' counts differ, so only the plan's own (first, count) per sequence
+    merges the right items."""
+    B, n_q, n_kv, tail = 2, 28, 4, 30
+    d = synth.make_layer(B, n_q, n_kv, D, 10 * 128, 2.5, seed=73, device=gpu)
+    mgr = PackedKVManager([d.levels], n_q, n_kv, D, 128, 128, 128, 2, gpu, batch_size=B, capacity_tokens=9 * 128)
+    st = mgr.layers[0]
+    st.fill_pages(d.key, d.value, [9, 1])
+    rk = torch.stack([d.key[b, :, p * 128:p * 128 + 127] for b, p in enumerate([9, 1])])
+    rv = torch.stack([d.value[b, :, p * 128:p * 128 + 127] for b, p in enumerate([9, 1])])
+    st.set_tail(rk, rv, [tail] * B)
+    out = torch.empty(B, n_q, D, dtype=torch.float32, device=gpu)
+    decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=_native.KERNEL_MFMA, pages_per_split=3)
+    torch.cuda.synchronize()
+    plan = st.decode_plan
+    seq = plan.seq_work.cpu().tolist()
+    assert plan.n_work % B == 0 and seq[1] != plan.n_work // B
+    _check_against_oracle(st, d, out, range(B), d.levels, n_q, n_kv, tail)
+
+
 def test_back_to_back_layers_share_the_workspace(gpu):
     """Six layers decoded back to back on one stream with no synchronisation between them: each
     layer's splits write their partials to the same workspace addresses as the layer before
