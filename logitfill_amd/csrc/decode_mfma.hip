@@ -412,9 +412,12 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
 
 // Issue the DMA of page ``page`` into the page slot at LDS address ``slot`` (32-bit): block j
 // of region A lands at 1024 j, block j of region B at rawa_bytes + 1024 j = 1024 (ja + j), so
-// this wave's i-th 16-byte instruction (block wave + 4 i overall) lands at 1024 (wave + 4 i);
-// the slot dwords follow region B at rawa_bytes + rawb_ks.  The sources advance one page.
-__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t slot, const LoopY& z, int page, int wave) {
+// this wave's i-th 16-byte instruction (block wave + 4 i overall) lands at 1024 (wave + 4 i).
+// The Key scale/min slot dwords hold a page pair (p & ~1, p | 1): they are fetched once per
+// pair (``ks``: the item's first page and every even page) into the slot-dword area at LDS
+// address ``ks_dst``, which the pages of the pair share.  The sources advance one page (the
+// slot sources one pair per fetch).
+__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t slot, uint32_t ks_dst, bool ks, const LoopY& z, int wave) {
     // The counts pass through an empty asm so the compiler keeps one compare per instruction
     // instead of hoisting per-instruction conditions out of the page loop.
     int n_chunk = __builtin_amdgcn_readfirstlane(s.n_chunk), n_ks = __builtin_amdgcn_readfirstlane(s.n_ks);
@@ -427,13 +430,13 @@ __device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t slot, const LoopY& 
             s.chunk[i] += s.chunk_stride[i];
         }
     }
-    const uint32_t d4 = slot + z.rawa_bytes + z.rawb_ks + 256 * wave;
-    const uint32_t step = (page & 1) * 4;  // a slot dword holds pages (p & ~1, p | 1)
+    if (!ks) return;
+    const uint32_t d4 = ks_dst + 256 * wave;
 #pragma unroll
     for (int i = 0; i < kMaxKsDma; ++i) {
         if (i < n_ks) {
             dma4(s.ks[i], d4 + kWaves * 256 * i);
-            s.ks[i] += step;
+            s.ks[i] += 4;
         }
     }
 }
@@ -481,8 +484,8 @@ __device__ __forceinline__ F16Map f16_map(const LoopY& z, int w16, int tid) {
 __device__ __forceinline__ float beta_lo_of(int tier) { return tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f; }
 __device__ __forceinline__ float beta_hi_of(int tier) { return tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f; }
 
-__device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, const unsigned char* raw, const float* qperm,
-                                          int g, int tid, int wave, PrepRegs& r) {
+__device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, const unsigned char* raw, const unsigned char* ksb,
+                                          const float* qperm, int g, int tid, int wave, PrepRegs& r) {
     // read k of thread (tg, w) takes token 4 tg + (k + tg) % 4: the 32 lanes of a half wave then
     // hit 32 different banks
     const int tg = tid >> 3, w = tid & 7;
@@ -503,7 +506,7 @@ __device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, cons
     }
     const int lane = tid & 63, n = lane & 7, j = lane >> 3;
     const int nbw = (z.nb_int + 3) >> 2, gb = min(wave * nbw + j, z.nb_int - 1);
-    const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
+    const uint32_t* ksc = reinterpret_cast<const uint32_t*>(ksb);
     qs_fetch(qperm + (gb * 8 + n) * 8, ksc + gb * 8, ksc + z.n_kslots / 2 + gb * 8, r.qs);
 }
 
@@ -517,10 +520,10 @@ __device__ __forceinline__ float qs_block(const LoopY& z, const QsRegs& r, half8
 }
 
 // Finish page ``page``: fetched registers ``r`` (and, for what they do not hold, rest buffer
-// ``raw``) into prepared buffer ``ck`` (all threads).
+// ``raw`` and slot dwords ``ksb``) into prepared buffer ``ck`` (all threads).
 __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, const PrepRegs& r, const unsigned char* raw,
-                                           unsigned char* ck, const float* qperm, int page, int g, int w16, int tid,
-                                           int wave) {
+                                           const unsigned char* ksb, unsigned char* ck, const float* qperm, int page,
+                                           int g, int w16, int tid, int wave) {
     const int lane = tid & 63;
     {
         // Value codes: dwords (group tg, word w, tokens 0..3) -> byte columns.  The reads came
@@ -566,7 +569,7 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
     float bsum = qs_block(z, r.qs, qs, page, min(gb_own, z.nb_int - 1), n);
     if (!(n < g && j < nbw && gb_own < z.nb_int)) bsum = 0.f;
     if (nbw > 8) {
-        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(raw + z.rawb_ks);
+        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(ksb);
         for (int jj = j + 8; jj < nbw; jj += 8) {
             const int gb2 = wave * nbw + jj;
             if (n < g && gb2 < z.nb_int) {
@@ -580,13 +583,6 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
     bsum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, bsum), 0x128, 0xf, 0xf, false));
     bsum = rows_sum(bsum);
     if (lane < 8) reinterpret_cast<float*>(ck + kCkBias)[4 * lane + wave] = bsum;
-}
-
-__device__ __forceinline__ void prepare_page(const LoopY& z, const F16Map& fm, const unsigned char* raw, unsigned char* ck,
-                                             const float* qperm, int page, int g, int w16, int tid, int wave) {
-    PrepRegs r;
-    prep_load(z, fm, raw, qperm, g, tid, wave, r);
-    prep_store(z, fm, r, raw, ck, qperm, page, g, w16, tid, wave);
 }
 
 // q of the workgroup's heads, scaled into the log2 domain, into qlin [8][128] (0 for heads >= g).
@@ -943,7 +939,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         unsigned char* raw0 = smem + y.off_raw;
         unsigned char* ck = smem + y.off_ck;
         const uint32_t raw_lds = lds_addr(smem) + y.off_raw;  // LDS address of page slot 0
-        dma_page(ds, raw_lds, z, pbeg, wave);
+        // slot dwords of pair q / 2 live in the slot-dword area of page slot (q / 2) % 2
+        const int ks_off = z.rawa_bytes + z.rawb_ks;
+        dma_page(ds, raw_lds, raw_lds + ((pbeg >> 1) & 1) * z.slot_bytes + ks_off, true, z, wave);
 
         // ---- q permuted into slot order ----
         // K-step i of the layout holds blocks 4i .. 4i+3.  Thread tid owns block gb = tid / 4
@@ -1021,10 +1019,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             // The preparation reads go out first; page + 1's DMA is issued while they are in
             // flight (a DMA instruction can wait for the address unit, shared by the CU's waves).
             const unsigned char* raw = raw0 + (rel & 1) * z.slot_bytes;
+            const unsigned char* ksb = raw0 + ((page >> 1) & 1) * z.slot_bytes + ks_off;
             PrepRegs pr;
-            prep_load(z, fm, raw + z.rawa_bytes, qperm, g, tid, wave, pr);
-            if (page + 1 < pend) dma_page(ds, raw_lds + ((rel + 1) & 1) * z.slot_bytes, z, page + 1, wave);
-            prep_store(z, fm, pr, raw + z.rawa_bytes, ck, qperm, page, g, w16, tid, wave);
+            prep_load(z, fm, raw + z.rawa_bytes, ksb, qperm, g, tid, wave, pr);
+            if (page + 1 < pend) {
+                const int q = page + 1;
+                dma_page(ds, raw_lds + ((rel + 1) & 1) * z.slot_bytes, raw_lds + ((q >> 1) & 1) * z.slot_bytes + ks_off,
+                         (q & 1) == 0, z, wave);
+            }
+            prep_store(z, fm, pr, raw + z.rawa_bytes, ksb, ck, qperm, page, g, w16, tid, wave);
             lds_barrier();  // page prepared
             // ---- compute page ``page`` from the prepared buffer and its Key codes ----
             const half8* qs = reinterpret_cast<const half8*>(ck + kCkQs);
