@@ -101,7 +101,7 @@ int32_t decode_checked(const lf_packed_layer* layer, const lf_decode_args* args,
     if (layer->v_groups > 64) return LF_E_UNSUPPORTED;
     if (A.tail_cap < 0 || A.tail_cap > layer->page_size) return LF_E_SHAPE;
     if (A.tail_cap > 0 && (!A.tail_k || !A.tail_v)) return LF_E_NULL;
-    if (A.n_work <= 0) return LF_E_SHAPE;
+    if (A.n_work <= 0 || static_cast<int64_t>(A.n_work) * layer->n_kv > 0x7fffffff) return LF_E_SHAPE;
     if (workspace_bytes < lf_decode_workspace_bytes(static_cast<int32_t>(rows), D, A.n_work)) return LF_E_WORKSPACE;
     if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
     if (q_len > 1 && A.kernel == 2) return LF_E_UNSUPPORTED;  // the MFMA kernel takes one token

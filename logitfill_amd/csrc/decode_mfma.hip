@@ -897,8 +897,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const UnpackBits kv = vgpr_bits(mp.k);
     const lf_packed_layer& L = p.L;
     const lf_decode_args& A = p.A;
-    const int item = blockIdx.x;
-    const int h = blockIdx.y;
+    // Item-major: workgroup id = item * n_kv + h, so the work list's order is the dispatch
+    // order (the host's split plan relies on it).
+    const int n_kv = L.n_kv;
+    const int item = blockIdx.x / n_kv;
+    const int h = blockIdx.x - item * n_kv;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1497,7 +1500,7 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
     *handled = true;
     const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&decode_mfma_kernel), mp.y.lds_bytes);
     if (rc != LF_OK) return rc;
-    hipLaunchKernelGGL(decode_mfma_kernel, dim3(p.A.n_work, p.L.n_kv), dim3(kThreads), mp.y.lds_bytes, stream, mp);
+    hipLaunchKernelGGL(decode_mfma_kernel, dim3(p.A.n_work * p.L.n_kv), dim3(kThreads), mp.y.lds_bytes, stream, mp);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);
     return launch_decode_reduce(p, stream);

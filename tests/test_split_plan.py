@@ -10,7 +10,8 @@ import heapq
 import pytest
 
 from logitfill_amd import _native, synth
-from logitfill_amd.packed.reference import ITEM_OVERHEAD_PAGES, choose_pages_per_split, residual_pages
+from logitfill_amd.packed.reference import (ITEM_OVERHEAD_PAGES, LATE_SLOWDOWN, age_split, choose_pages_per_split,
+                                            plan_work, residual_pages)
 
 SLOTS = 512  # 256 CUs x 2 workgroups
 RES = residual_pages([100])  # the c2 residual's cost (100-token tails)
@@ -96,3 +97,58 @@ def test_edge_cases(monkeypatch):
     assert choose_pages_per_split([512], 8, RES) == one_round_size([512], 8)
     monkeypatch.setenv("LOGITFILL_AMD_PAGES_PER_SPLIT", "7")
     assert choose_pages_per_split([256] * 16, 4, RES) == 7
+
+
+def test_plan_work_equals_one_planner_call_for_one_size():
+    """Per-sequence sizes that are all equal give lf_plan_decode's own work list."""
+    pages = [40, 0, 7, 33, 12]
+    work, seq = plan_work(pages, [5] * 5, RES)
+    assert [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)] == plan_items(pages, 5)
+    assert sum(seq[2 * b + 1] for b in range(5)) == len(work) // 4
+
+
+def test_plan_work_runs_of_sizes_cover_every_page():
+    """Mixed sizes: each sequence's items are contiguous from its first, cover its pages once
+    in order, and number ceil((pages + residual) / size)."""
+    pages, sizes = [30, 30, 9, 0, 17], [4, 4, 7, 2, 3]
+    work, seq = plan_work(pages, sizes, RES)
+    items = [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)]
+    for b, (p, z) in enumerate(zip(pages, sizes)):
+        first, count = seq[2 * b], seq[2 * b + 1]
+        mine = items[first:first + count]
+        assert all(it[0] == b for it in mine)
+        assert [it[1] for it in mine][0] == 0 and mine[-1][2] == p
+        assert all(mine[k][2] == mine[k + 1][1] for k in range(count - 1))
+        assert count == (1 if p == 0 else -(-(p + RES) // z))
+
+
+def test_age_split_gives_early_workgroups_the_larger_items():
+    """c2 (16 sequences x 256 pages + a 4-page residual, 4 kv heads, 256 CUs): 8 sequences of
+    7 items and 8 of 9, 128 items = one round of 512 workgroups; the estimated slowest item
+    (x LATE_SLOWDOWN past the first 256 workgroups) beats the uniform 8 x 32.5 pages."""
+    res = residual_pages([100])
+    sizes = age_split([256] * 16, 4, res, 33, 256)
+    assert sizes == [38] * 8 + [29] * 8
+    work, seq = plan_work([256] * 16, sizes, res)
+    n = len(work) // 4
+    assert n == 128 and [seq[2 * b + 1] for b in range(16)] == [7] * 8 + [9] * 8
+
+    def slowest(work):
+        t = 0.0
+        for i in range(len(work) // 4):
+            b, p0, p1, kind = work[4 * i:4 * i + 4]
+            size = (p1 - p0) + (res if kind else 0)
+            t = max(t, size * (LATE_SLOWDOWN if (i + 1) * 4 > 256 else 1.0))
+        return t
+
+    uniform, _ = plan_work([256] * 16, [33] * 16, res)
+    assert slowest(work) < 0.97 * slowest(uniform)
+
+
+def test_age_split_declines_other_batches():
+    """Ragged lengths, a plan short of a full round (c1: 368 of 512 workgroups), more items than
+    one round, one sequence: the uniform split stays."""
+    assert age_split([256, 200] * 8, 4, RES, 33, 256) is None
+    assert age_split([64] * 8, 2, residual_pages([37]), 3, 256) is None
+    assert age_split([256] * 16, 4, RES, 20, 256) is None
+    assert age_split([256], 4, RES, 33, 256) is None
