@@ -66,6 +66,7 @@ constexpr int kCkVmid = 512;    // [128] fp32 vmin - 4 * vscale
 constexpr int kCkBias = 1024;   // [8 heads][4 waves] fp32 page bias partials
 constexpr int kCkVt = 1152;     // [32 groups][36] u32 Value-code byte columns (4 per 8-word row) + 4 pad
 constexpr int kCkQs = kCkVt + 32 * 36 * 4;  // [nb][16][8] fp16 Qs hi (rows 0..7) / lo (rows 8..15)
+static_assert(kCkQs >= 8 * kD * 4, "the item prologue's q [8][128] fp32 lies below the fp16-tier Qs");
 
 struct MfmaLayout {
     int kst[4];          // K-steps per tier (int2: even; K-step s takes half s&1 of 4 words)
@@ -949,11 +950,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         // ---- q permuted into slot order ----
         // K-step i of the layout holds blocks 4i .. 4i+3.  Thread tid owns block gb = tid / 4
         // (K-step gb / 4) for heads 2 (tid % 4) and 2 (tid % 4) + 1, all 8 slot positions: the
-        // slots' channels come from the tier table in global memory and q is gathered from
-        // global memory -- two rounds of loads while the first page's DMA is in flight (nothing
-        // here waits for the DMA explicitly; the page loop's first barrier does).  Integer tiers
-        // go to qperm (0 for padding slots and heads >= g); the fp16 tier's Qs (plain q, hi / lo)
-        // goes into the prepared buffer, which no page rewrites; Qs rows of heads >= g start at 0.
+        // slots' channels come from the tier table in global memory and q of the workgroup's
+        // heads arrives whole, both in one round of loads while the first page's DMA is in
+        // flight (nothing here waits for the DMA explicitly; the page loop's first barrier does):
+        // q goes to qlin [8][128] (the first 4 KB of the prepared buffer), and after a barrier
+        // each thread reads its slots' channels there.  Integer tiers go to qperm (0 for padding
+        // slots and heads >= g); the fp16 tier's Qs (plain q, hi / lo) goes into the prepared
+        // buffer past qlin, which no page rewrites; Qs rows of heads >= g start at 0.
         // (Issuing the DMA from two waves and the set-up from the other two, so that the set-up's
         // load waits do not cover the DMA, measured slower: c2 92.5 against 90.3 us.)
         {
@@ -973,14 +976,29 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 const int j = block_slot(tier, lb, pos);
                 chan[pos] = live && j < count ? tix[h * width + j] : -1;
             }
+            {
+                // q [8][128] of heads h g .. h g + 7: thread tid takes channels 4 (tid % 32) + 0..3
+                // of head tid / 32 (0 for heads >= g)
+                float* qlin = reinterpret_cast<float*>(ck);
+                const int n = tid >> 5, c0 = 4 * (tid & 31);
+                const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD + c0;
+                float4 q4 = {0.f, 0.f, 0.f, 0.f};
+                if (n < g) {
+                    q4.x = load_as_f32(A.query, qrow + 0, A.q_dtype) * p.qscale;
+                    q4.y = load_as_f32(A.query, qrow + 1, A.q_dtype) * p.qscale;
+                    q4.z = load_as_f32(A.query, qrow + 2, A.q_dtype) * p.qscale;
+                    q4.w = load_as_f32(A.query, qrow + 3, A.q_dtype) * p.qscale;
+                }
+                *reinterpret_cast<float4*>(qlin + n * kD + c0) = q4;
+            }
+            __syncthreads();  // qlin complete
+            const float* qlin = reinterpret_cast<const float*>(ck);
             float qv[2][8];
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
                 const int n = n0 + r;
-                const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD;
 #pragma unroll
-                for (int pos = 0; pos < 8; ++pos)
-                    qv[r][pos] = chan[pos] >= 0 && n < g ? load_as_f32(A.query, qrow + chan[pos], A.q_dtype) * p.qscale : 0.f;
+                for (int pos = 0; pos < 8; ++pos) qv[r][pos] = chan[pos] >= 0 && n < g ? qlin[n * kD + chan[pos]] : 0.f;
             }
             if (own) {
                 _Float16* qs16 = reinterpret_cast<_Float16*>(ck + kCkQs);
