@@ -209,32 +209,43 @@ def _age_split(hist_pages: tuple, n_kv: int, residual_pages: int, pages_per_spli
 
 def plan_work(hist_pages: list[int], sizes: list[int], residual_pages: int) -> tuple[list[int], list[int]]:
     """Host work list (b, page0, page1, kind) x n and per-sequence (first, count) for
-    per-sequence split sizes: each run of sequences with one size is planned by one
-    lf_plan_decode call, its sequence and item indices shifted into place."""
+    per-sequence split sizes.  The sequences go into the list (the decode kernel's dispatch
+    order) by decreasing item size -- larger items first, the smaller ones filling the last
+    round (c4: 376.6 -> 371.7 us) -- ties in batch order; each run of consecutive sequences
+    with one size is planned by one lf_plan_decode call, its sequence and item indices
+    shifted into place."""
     lib = _native.load()
     batch = len(hist_pages)
     if len(sizes) != batch:
         raise ValueError("one split size per sequence")
-    work, seq = [], []
-    b0 = 0
-    while b0 < batch:
-        b1 = b0
-        while b1 < batch and sizes[b1] == sizes[b0]:
-            b1 += 1
-        run = [int(p) for p in hist_pages[b0:b1]]
-        m = b1 - b0
-        cap = sum(-(-(p + residual_pages) // sizes[b0]) for p in run) + m
+
+    def item_pages(b):
+        w = int(hist_pages[b]) + residual_pages
+        return w / (1 if hist_pages[b] == 0 else -(-w // int(sizes[b])))
+
+    order = sorted(range(batch), key=lambda b: -item_pages(b))
+    work, seq = [], [0] * (2 * batch)
+    r0 = 0
+    while r0 < batch:
+        r1 = r0
+        while r1 < batch and sizes[order[r1]] == sizes[order[r0]]:
+            r1 += 1
+        run = order[r0:r1]
+        m = len(run)
+        size = int(sizes[run[0]])
+        pages = [int(hist_pages[b]) for b in run]
+        cap = sum(-(-(p + residual_pages) // size) for p in pages) + m
         w = (ctypes.c_int32 * (4 * cap))()
         sq = (ctypes.c_int32 * (2 * m))()
-        n = lib.lf_plan_decode((ctypes.c_int32 * m)(*run), m, int(sizes[b0]), residual_pages, w, cap, sq)
+        n = lib.lf_plan_decode((ctypes.c_int32 * m)(*pages), m, size, residual_pages, w, cap, sq)
         if n < 0:
             _native.check(n, "lf_plan_decode")
         base = len(work) // 4
         for i in range(n):
-            work += [b0 + w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]]
-        for i in range(m):
-            seq += [base + sq[2 * i], sq[2 * i + 1]]
-        b0 = b1
+            work += [run[w[4 * i]], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]]
+        for i, b in enumerate(run):
+            seq[2 * b], seq[2 * b + 1] = base + sq[2 * i], sq[2 * i + 1]
+        r0 = r1
     return work, seq
 
 

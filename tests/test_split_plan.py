@@ -100,11 +100,22 @@ def test_edge_cases(monkeypatch):
 
 
 def test_plan_work_equals_one_planner_call_for_one_size():
-    """Per-sequence sizes that are all equal give lf_plan_decode's own work list."""
+    """Per-sequence sizes that are all equal give lf_plan_decode's own items for every
+    sequence, the sequences in decreasing item size (ties in batch order)."""
     pages = [40, 0, 7, 33, 12]
     work, seq = plan_work(pages, [5] * 5, RES)
-    assert [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)] == plan_items(pages, 5)
-    assert sum(seq[2 * b + 1] for b in range(5)) == len(work) // 4
+    items = [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)]
+    ref = plan_items(pages, 5)
+    for b in range(5):
+        mine = items[seq[2 * b]:seq[2 * b] + seq[2 * b + 1]]
+        assert mine == [it for it in ref if it[0] == b]
+    assert sum(seq[2 * b + 1] for b in range(5)) == len(items)
+    def size(b):
+        return (pages[b] + RES) / (1 if pages[b] == 0 else -(-(pages[b] + RES) // 5))
+    assert [it[0] for it in items if it[3] != 0] == sorted(range(5), key=lambda b: -size(b))
+    uniform = [64] * 4
+    w2, _ = plan_work(uniform, [9] * 4, RES)
+    assert [tuple(w2[4 * i:4 * i + 4]) for i in range(len(w2) // 4)] == plan_items(uniform, 9)
 
 
 def test_plan_work_runs_of_sizes_cover_every_page():
