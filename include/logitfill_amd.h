@@ -149,7 +149,11 @@ int32_t lf_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_l
  * ``seq_work_out`` [batch][2] = (first item, item count) of each sequence;
  * a sequence's items are consecutive.  Returns the item count n, or a
  * negative LF_E_* when ``work_cap`` is too small.  Both arrays must be copied
- * to the device before lf_decode_attention.
+ * to the device before lf_decode_attention.  Any work list of this form is
+ * valid input (sequences in any order, items of any sizes, several calls'
+ * lists concatenated with b and the first items shifted): the matrix-core
+ * kernel dispatches it in list order (workgroup item * n_kv + h), which the
+ * Python layer uses to put larger items first.
  */
 int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split, int32_t residual_pages,
                        int32_t* work_out, int32_t work_cap, int32_t* seq_work_out);
