@@ -1085,6 +1085,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                     score_tiles_fixed<2, 1, 1, 1>(kt, kv, acc0, acc1);
                 else if (z.kst0 == 4 && z.kst1 == 2 && z.kst2 == 1 && z.kst3 == 1)
                     score_tiles_fixed<2, 2, 1, 1>(kt, kv, acc0, acc1);
+                else if (z.kst0 == 4 && z.kst1 == 3 && z.kst2 == 1 && z.kst3 == 1)
+                    score_tiles_fixed<2, 3, 1, 1>(kt, kv, acc0, acc1);
+                else if (z.kst0 == 2 && z.kst1 == 3 && z.kst2 == 1 && z.kst3 == 1)
+                    score_tiles_fixed<1, 3, 1, 1>(kt, kv, acc0, acc1);
                 else
                     score_tiles(kt, z, kv, acc0, acc1);
             }
