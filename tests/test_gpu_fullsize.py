@@ -56,8 +56,10 @@ def _decode(d, mgr, gpu, scaling, pages_per_split=None, out_dtype=None):
 
 
 def test_headline_shape_full_size(gpu):
-    """c2: 16 sequences x (256 pages + 100 residual + the new token), the bench's plan (items of
-    about 33 pages, the residual in each sequence's first item); sequences 0 and 9 checked."""
+    """c2: 16 sequences x (256 pages + 100 residual + the new token), the bench's plan (the
+    dispatch-order split: sequences 0-7 in 7 items of about 37 pages, 8-15 in 9 of about 29,
+    the residual in each sequence's first item); sequence 0 of the first group and 9 of the
+    second checked."""
     B, n_q, n_kv = 16, 28, 4
     d, mgr = _build(gpu, B, n_q, n_kv, [256] * B, [100] * B, 2.5, seed=11)
     scaling = 128 ** -0.5
