@@ -1,13 +1,14 @@
-"""The split merge of the packed decode (the reduce kernel over the splits' softmax partials)
-against the oracle (reference src/logitfill/packed/reference.py:30-56 over [history ; tail ;
-new]): forced split sizes that give every sequence 1 .. 12 items, and layers decoded back to
-back on one stream whose partials reuse the same workspace addresses."""
+"""The split-K plan and merge of the packed decode (the reduce kernel over the splits' softmax
+partials) against the oracle (reference src/logitfill/packed/reference.py:30-56 over
+[history ; tail ; new]): forced split sizes that give every sequence 1 .. 12 items, ragged
+item counts, the dispatch-order split (two item sizes), and layers decoded back to back on one
+stream whose partials reuse the same workspace addresses."""
 import pytest
 import torch
 
 from logitfill_amd import _native, synth
 from logitfill_amd.packed import PackedKVManager
-from logitfill_amd.packed.reference import decode_into
+from logitfill_amd.packed.reference import decode_into, residual_pages
 from oracle import attention as oatt
 from tests.helpers import assert_decode_close, f32
 
@@ -97,3 +98,20 @@ def test_back_to_back_layers_share_the_workspace(gpu):
     for l, d in enumerate(ds):
         print(f"merge: layer {l}", flush=True)
         _check_against_oracle(mgr.layers[l], d, outs[l], [0, B - 1], d.levels, n_q, n_kv, tail)
+
+
+@pytest.mark.parametrize("B,n_q,n_kv,pages,tail", [(8, 12, 2, 200, 50), (4, 28, 4, 256, 20)])
+def test_dispatch_order_split_matches_the_oracle(gpu, B, n_q, n_kv, pages, tail):
+    """Batches of equal sequences whose plan fills one round take the dispatch-order split
+    (the first sequences in fewer, larger items): the plan holds two item sizes, the larger
+    first, and sequences of both groups match the oracle."""
+    d, mgr, st = _layer(gpu, B, n_q, n_kv, pages, tail, seed=74 + B)
+    out = torch.empty(B, n_q, D, dtype=torch.float32, device=gpu)
+    decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=_native.KERNEL_MFMA)
+    torch.cuda.synchronize()
+    sizes = st.decode_plan.pages_per_split
+    assert isinstance(sizes, tuple) and len(set(sizes)) == 2 and sizes[0] > sizes[-1]
+    seq = st.decode_plan.seq_work.cpu().tolist()
+    res = residual_pages([tail])
+    assert [seq[2 * b + 1] for b in range(B)] == [-(-(pages + res) // z) for z in sizes]
+    _check_against_oracle(st, d, out, [0, B - 1], d.levels, n_q, n_kv, tail)
