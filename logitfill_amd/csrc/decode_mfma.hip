@@ -892,7 +892,37 @@ __device__ __forceinline__ void residual_mfma(const DecodeParams& p, int b, int 
     __syncthreads();
 }
 
+
+// Bring the kernel's argument block (``Bytes`` bytes) into the scalar data cache with one round
+// of loads, issued from one asm statement so that no compiler wait splits it.  The compiler
+// reads argument fields lazily, a small load and a wait at a time where register pressure makes
+// it re-read them; with the block already cached each of those waits is a cache hit instead of
+// a memory round trip.  The loaded values are discarded (s40..s55 are clobbered); the asm
+// declares no memory clobber, so loads of read-only data may still be scalar loads.
+#define LF_ARG_LINE(off) "s_load_dwordx16 s[40:55], %0, " #off "\n\t"
+#define LF_ARG_LINES8 LF_ARG_LINE(0) LF_ARG_LINE(64) LF_ARG_LINE(128) LF_ARG_LINE(192) LF_ARG_LINE(256) \
+    LF_ARG_LINE(320) LF_ARG_LINE(384) LF_ARG_LINE(448)
+#define LF_ARG_CLOBBERS "s40", "s41", "s42", "s43", "s44", "s45", "s46", "s47", "s48", "s49", "s50", "s51", \
+    "s52", "s53", "s54", "s55"
+template <int Bytes>
+__device__ __forceinline__ void prefetch_args() {
+    constexpr int lines = (Bytes + 63) / 64;
+    static_assert(lines >= 9 && lines <= 11, "prefetch_args: add the line count of this argument block");
+    const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+    if constexpr (lines == 9)
+        asm volatile(LF_ARG_LINES8 LF_ARG_LINE(512) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
+    else if constexpr (lines == 10)
+        asm volatile(LF_ARG_LINES8 LF_ARG_LINE(512) LF_ARG_LINE(576) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
+    else
+        asm volatile(LF_ARG_LINES8 LF_ARG_LINE(512) LF_ARG_LINE(576) LF_ARG_LINE(640) "s_waitcnt lgkmcnt(0)" ::"s"(kp)
+                     : LF_ARG_CLOBBERS);
+}
+#undef LF_ARG_CLOBBERS
+#undef LF_ARG_LINES8
+#undef LF_ARG_LINE
+
 __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
+    prefetch_args<sizeof(MfmaParams)>();
     const DecodeParams& p = mp.p;
     const MfmaLayout& y = mp.y;
     const UnpackBits kv = vgpr_bits(mp.k);
@@ -913,6 +943,24 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const int pbeg = A.work[4 * item + 1];
     const int pend = A.work[4 * item + 2];
     const int kind = A.work[4 * item + 3];
+    // Tier-table entries of this thread's Key-slot block (used by items with pages, below): they
+    // depend only on the kv head, so their loads go out while the work record is in flight.  Thread tid owns block gb = tid / 4 (K-step gb / 4); tier_index entries
+    // are read whatever the tier count, which decides afterwards which are real slots.
+    const int gb = tid >> 2, n0 = 2 * (tid & 3);
+    const int i = gb >> 2;
+    const bool own = i < y.kst[0] + y.kst[1] + y.kst[2] + y.kst[3];
+    const int tier = i >= y.kfirst[3] ? 3 : i >= y.kfirst[2] ? 2 : i >= y.kfirst[1] ? 1 : 0;
+    const int lb = gb - 4 * sel4(y.kfirst, tier);
+    const bool live = own && block_live(L, tier, lb);  // live: the tier has width > 0
+    const int width = sel4(L.k_width, tier);
+    int count = 0;
+    int craw[8];
+    if (live) {
+        const int32_t* tix = sel4(L.tier_index, tier) + h * width;
+        count = sel4(L.tier_count, tier)[h];
+#pragma unroll
+        for (int pos = 0; pos < 8; ++pos) craw[pos] = tix[min(block_slot(tier, lb, pos), width - 1)];
+    }
 
     extern __shared__ __align__(16) unsigned char smem[];
     float* qperm = reinterpret_cast<float*>(smem + y.off_qperm);
@@ -938,59 +986,43 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     if (kind != 1) {
         // ---- pages (kind 0, 2) ----
         const LoopY z = loop_y(y);
-        DmaSrc ds;
-        dma_setup(ds, L, y, b, h, pbeg, wave, lane);
         unsigned char* raw0 = smem + y.off_raw;
         unsigned char* ck = smem + y.off_ck;
         const uint32_t raw_lds = lds_addr(smem) + y.off_raw;  // LDS address of page slot 0
         // slot dwords of pair q / 2 live in the slot-dword area of page slot (q / 2) % 2
         const int ks_off = z.rawa_bytes + z.rawb_ks;
-        dma_page(ds, raw_lds, raw_lds + ((pbeg >> 1) & 1) * z.slot_bytes + ks_off, true, z, wave);
 
         // ---- q permuted into slot order ----
         // K-step i of the layout holds blocks 4i .. 4i+3.  Thread tid owns block gb = tid / 4
-        // (K-step gb / 4) for heads 2 (tid % 4) and 2 (tid % 4) + 1, all 8 slot positions: the
-        // slots' channels come from the tier table in global memory and q of the workgroup's
-        // heads arrives whole, both in one round of loads while the first page's DMA is in
-        // flight (nothing here waits for the DMA explicitly; the page loop's first barrier does):
-        // q goes to qlin [8][128] (the first 4 KB of the prepared buffer), and after a barrier
-        // each thread reads its slots' channels there.  Integer tiers go to qperm (0 for padding
-        // slots and heads >= g); the fp16 tier's Qs (plain q, hi / lo) goes into the prepared
-        // buffer past qlin, which no page rewrites; Qs rows of heads >= g start at 0.
-        // (Issuing the DMA from two waves and the set-up from the other two, so that the set-up's
-        // load waits do not cover the DMA, measured slower: c2 92.5 against 90.3 us.)
+        // (K-step gb / 4) for heads 2 (tid % 4) and 2 (tid % 4) + 1, all 8 slot positions: its
+        // slots' channels were loaded with the work record (above); q of the workgroup's heads
+        // goes whole into qlin [8][128] (the first 4 KB of the prepared buffer), its loads issued
+        // right behind the first page's DMA so both land in one round.  After a barrier each
+        // thread reads its slots' channels there.
+        // Integer tiers go to qperm (0 for padding slots and heads >= g); the fp16 tier's Qs
+        // (plain q, hi / lo) goes into the prepared buffer past qlin, which no page rewrites; Qs
+        // rows of heads >= g start at 0.  Nothing here waits for the DMA; the page loop's first
+        // barrier does.
+        DmaSrc ds;
+        dma_setup(ds, L, y, b, h, pbeg, wave, lane);
+        dma_page(ds, raw_lds, raw_lds + ((pbeg >> 1) & 1) * z.slot_bytes + ks_off, true, z, wave);
+        // q [8][128] of heads h g .. h g + 7: thread tid takes channels 4 (tid % 32) + 0..3 of
+        // head tid / 32 (0 for heads >= g)
+        const int qn = tid >> 5, qc0 = 4 * (tid & 31);
+        float4 q4 = {0.f, 0.f, 0.f, 0.f};
+        if (qn < g) {
+            const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * g + qn) * kD + qc0;
+            q4.x = load_as_f32(A.query, qrow + 0, A.q_dtype) * p.qscale;
+            q4.y = load_as_f32(A.query, qrow + 1, A.q_dtype) * p.qscale;
+            q4.z = load_as_f32(A.query, qrow + 2, A.q_dtype) * p.qscale;
+            q4.w = load_as_f32(A.query, qrow + 3, A.q_dtype) * p.qscale;
+        }
+
         {
-            const int ks = z.kst0 + z.kst1 + z.kst2 + z.kst3;
-            const int gb = tid >> 2, n0 = 2 * (tid & 3);
-            const int i = gb >> 2;
-            const bool own = i < ks;
-            const int tier = i >= z.kf3 ? 3 : i >= z.kf2 ? 2 : i >= z.kf1 ? 1 : 0;
-            const int lb = gb - 4 * sel4(y.kfirst, tier);
-            const bool live = own && block_live(L, tier, lb);
-            const int width = sel4(L.k_width, tier);
-            const int32_t* tix = sel4(L.tier_index, tier);
-            const int count = live ? sel4(L.tier_count, tier)[h] : 0;
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(ck) + qn * kD + qc0) = q4;
             int chan[8];
 #pragma unroll
-            for (int pos = 0; pos < 8; ++pos) {
-                const int j = block_slot(tier, lb, pos);
-                chan[pos] = live && j < count ? tix[h * width + j] : -1;
-            }
-            {
-                // q [8][128] of heads h g .. h g + 7: thread tid takes channels 4 (tid % 32) + 0..3
-                // of head tid / 32 (0 for heads >= g)
-                float* qlin = reinterpret_cast<float*>(ck);
-                const int n = tid >> 5, c0 = 4 * (tid & 31);
-                const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * g + n) * kD + c0;
-                float4 q4 = {0.f, 0.f, 0.f, 0.f};
-                if (n < g) {
-                    q4.x = load_as_f32(A.query, qrow + 0, A.q_dtype) * p.qscale;
-                    q4.y = load_as_f32(A.query, qrow + 1, A.q_dtype) * p.qscale;
-                    q4.z = load_as_f32(A.query, qrow + 2, A.q_dtype) * p.qscale;
-                    q4.w = load_as_f32(A.query, qrow + 3, A.q_dtype) * p.qscale;
-                }
-                *reinterpret_cast<float4*>(qlin + n * kD + c0) = q4;
-            }
+            for (int pos = 0; pos < 8; ++pos) chan[pos] = live && block_slot(tier, lb, pos) < count ? craw[pos] : -1;
             __syncthreads();  // qlin complete
             const float* qlin = reinterpret_cast<const float*>(ck);
             float qv[2][8];
