@@ -53,6 +53,36 @@ __device__ __forceinline__ void load8_as_f32(const void* base, int64_t idx, int 
     }
 }
 
+// Bring the kernel's argument block (its first Bytes / 64 whole 64-byte lines: reads stay inside the
+// explicit arguments) into the scalar data cache with one round of loads, issued from one asm
+// statement so that no compiler wait splits it.  The compiler reads argument fields lazily, a small
+// load and a wait at a time where register pressure makes it re-read them; with the block already
+// cached each of those waits is a cache hit instead of a memory round trip.  The loaded values are
+// discarded (s40..s55 are clobbered); the asm declares no memory clobber, so loads of read-only
+// data may still be scalar loads.
+#define LF_ARG_LINE(off) "s_load_dwordx16 s[40:55], %0, " #off "\n\t"
+#define LF_ARG_LINES6 LF_ARG_LINE(0) LF_ARG_LINE(64) LF_ARG_LINE(128) LF_ARG_LINE(192) LF_ARG_LINE(256) LF_ARG_LINE(320)
+#define LF_ARG_CLOBBERS "s40", "s41", "s42", "s43", "s44", "s45", "s46", "s47", "s48", "s49", "s50", "s51", \
+    "s52", "s53", "s54", "s55"
+template <int Bytes>
+__device__ __forceinline__ void prefetch_args() {
+    constexpr int lines = Bytes / 64;
+    static_assert(lines >= 6 && lines <= 9, "prefetch_args: add the line count of this argument block");
+    const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+    if constexpr (lines == 6)
+        asm volatile(LF_ARG_LINES6 "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
+    else if constexpr (lines == 7)
+        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
+    else if constexpr (lines == 8)
+        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
+    else
+        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) LF_ARG_LINE(512) "s_waitcnt lgkmcnt(0)" ::"s"(kp)
+                     : LF_ARG_CLOBBERS);
+}
+#undef LF_ARG_CLOBBERS
+#undef LF_ARG_LINES6
+#undef LF_ARG_LINE
+
 // Merge the partials of every sequence into ``out`` (enqueued after a decode kernel).
 int launch_decode_reduce(const DecodeParams& p, hipStream_t stream);
 

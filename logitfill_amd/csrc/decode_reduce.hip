@@ -16,6 +16,7 @@ constexpr int kFastItems = 32;    // up to this many items: one round of loads p
                                   // (at most the 64 lanes of a wave)
 
 __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
+    prefetch_args<sizeof(DecodeParams)>();
     __shared__ float w[kReduceLds];
     __shared__ float red[8];
     const int D = p.L.head_dim;
