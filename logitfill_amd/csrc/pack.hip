@@ -595,11 +595,19 @@ __device__ __forceinline__ void tier_words(const uint8_t* codes, int seg, int kw
 //               the staged page; phases 2, 3: the channel's scale and its 32 codes into byte
 //               rows over the page; phase 4: the tiers' words (tier_words)
 template <bool IsHalf, int Ld>
-__device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const void* k_src, const void* v_src,
+__device__ __forceinline__ void pack_fast_page(const lf_packed_layer& Lsrc, const void* k_src, const void* v_src,
                                                int64_t sb, int64_t sh, int64_t st, int b, int64_t tok0, int page,
                                                bool value) {
     const int h = blockIdx.y;
     const int tid = threadIdx.x;
+    // The layer descriptor and this head's tier counts, read before any store: the multi-layer
+    // kernel's descriptor lives in device memory, which the page's stores might alias as far as
+    // the compiler knows, so a field read after a store would be a vector load of its own round
+    // trip (and the tier tables' pointers per lane a second one).
+    const lf_packed_layer L = Lsrc;
+    int tcnt[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) tcnt[t] = value || L.k_width[t] == 0 ? 0 : L.tier_count[t][h];
     const int64_t dst_tok0 = static_cast<int64_t>(page) * kFastP;
     constexpr int D = 128;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -648,10 +656,10 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
         // Constant indices into the layer descriptor only (a lane-dependent one would copy it to
         // scratch memory).
         int my_idx = 0, my_cnt = 0;
-        if (tid < koff1) { my_idx = L.tier_index[0][h * w0 + tid]; my_cnt = L.tier_count[0][h]; }
-        else if (tid < koff2) { my_idx = L.tier_index[1][h * w1 + tid - koff1]; my_cnt = L.tier_count[1][h]; }
-        else if (tid < nslots) { my_idx = L.tier_index[2][h * w2 + tid - koff2]; my_cnt = L.tier_count[2][h]; }
-        else if (tid < wall) { my_idx = L.tier_index[3][h * w16 + tid - nslots]; my_cnt = L.tier_count[3][h]; }
+        if (tid < koff1) { my_idx = L.tier_index[0][h * w0 + tid]; my_cnt = tcnt[0]; }
+        else if (tid < koff2) { my_idx = L.tier_index[1][h * w1 + tid - koff1]; my_cnt = tcnt[1]; }
+        else if (tid < nslots) { my_idx = L.tier_index[2][h * w2 + tid - koff2]; my_cnt = tcnt[2]; }
+        else if (tid < wall) { my_idx = L.tier_index[3][h * w16 + tid - nslots]; my_cnt = tcnt[3]; }
         // channel map: every channel sits in exactly one tier (rank < count), so every entry is
         // written once; padding slots (rank >= count): scale 1.0, min 0.0, code 0 (layout.py:84-85)
         if (tid < wall) {
@@ -686,7 +694,7 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     // fp16 tier (layout.py:101-111; exact for fp16 input, RNE for bf16) straight from the staged
     // page, element i = (token i / w16, slot i % w16) in memory order; padding slots are 0
     if (w16 > 0) {
-        const int cnt = L.tier_count[3][h];
+        const int cnt = tcnt[3];
         const float rk = 1.0f / static_cast<float>(w16);
         uint16_t* out = L.k_value16 + tok_row(L, b, h, dst_tok0) * w16;
         for (int i = tid; i < kFastP * w16; i += kFastThreads) {
@@ -731,9 +739,9 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& L, const v
     // ---- phase 4: the integer tiers' words ----
     const int64_t row0 = tok_row(L, b, h, dst_tok0);
     const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
-    tier_words<2, Ld>(codes, 0, kw0, w0 ? L.tier_count[0][h] : 0, L.k_code[0] + row0 * kw0, tid);
-    tier_words<4, Ld>(codes, cs.seg[1], kw1, w1 ? L.tier_count[1][h] : 0, L.k_code[1] + row0 * kw1, tid);
-    tier_words<8, Ld>(codes, cs.seg[2], kw2, w2 ? L.tier_count[2][h] : 0, L.k_code[2] + row0 * kw2, tid);
+    tier_words<2, Ld>(codes, 0, kw0, tcnt[0], L.k_code[0] + row0 * kw0, tid);
+    tier_words<4, Ld>(codes, cs.seg[1], kw1, tcnt[1], L.k_code[1] + row0 * kw1, tid);
+    tier_words<8, Ld>(codes, cs.seg[2], kw2, tcnt[2], L.k_code[2] + row0 * kw2, tid);
 }
 
 template <bool IsHalf, int Ld>
