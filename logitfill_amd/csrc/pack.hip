@@ -436,20 +436,25 @@ __device__ __host__ inline CodeSegs code_segs(const lf_packed_layer& L) {
     return s;
 }
 
-// Four byte codes (0..3) of a dword -> 8 bits, code k at bits 2k (bytes 1 and 3 fold onto 0 and 2).
-__device__ __forceinline__ uint32_t fold2(uint32_t d) { return d | (d >> 6); }
+// The word helpers take code bytes in slot order whose bytes below the tier's count are codes
+// (0..qmax) and whose later bytes may be stale page bytes: a stale byte only reaches bits of its
+// own and later slots, which tier_words masks, so no byte needs masking before packing.
 
-// 16 int2 codes (one per byte) -> LSB-first word.
+// 16 int2 codes (one per byte) -> LSB-first word: v_dot4_u32_u8 with weights 1, 4, 16, 64 puts
+// a dword's four codes into its low byte (a code byte below 4 carries nothing into the next
+// field; products of stale bytes only reach higher bits), and two byte permutes gather the four
+// low bytes.
 __device__ __forceinline__ uint32_t word_int2(uint4 b) {
-    const uint32_t t0 = fold2(b.x), t1 = fold2(b.y), t2 = fold2(b.z), t3 = fold2(b.w);
-    // nibble bytes (t.byte0, t.byte2) of t0, t1 / t2, t3, then nibble pairs folded into bytes
-    const uint32_t p01 = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
-    const uint32_t p23 = __builtin_amdgcn_perm(t3, t2, 0x06040200u);
-    const uint32_t q01 = p01 | (p01 >> 4), q23 = p23 | (p23 >> 4);
-    return __builtin_amdgcn_perm(q23, q01, 0x06040200u);
+    constexpr uint32_t kW = 0x40100401u;
+    const uint32_t t0 = __builtin_amdgcn_udot4(b.x, kW, 0u, false), t1 = __builtin_amdgcn_udot4(b.y, kW, 0u, false);
+    const uint32_t t2 = __builtin_amdgcn_udot4(b.z, kW, 0u, false), t3 = __builtin_amdgcn_udot4(b.w, kW, 0u, false);
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, 0x0c0c0400u);  // t0.byte0, t1.byte0, 0, 0
+    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, 0x04000c0cu);  // 0, 0, t2.byte0, t3.byte0
+    return lo | hi;
 }
 
-// 8 int4 codes (one per byte) -> LSB-first word.
+// 8 int4 codes (one per byte) -> LSB-first word: x | x >> 4 puts codes 2k, 2k + 1 into byte 2k
+// (a code byte below 16 carries nothing into the next field), one permute gathers bytes 0 and 2.
 __device__ __forceinline__ uint32_t word_int4(uint2 b) {
     const uint32_t t0 = b.x | (b.x >> 4), t1 = b.y | (b.y >> 4);
     return __builtin_amdgcn_perm(t1, t0, 0x06040200u);
@@ -552,15 +557,17 @@ __device__ __host__ inline FastLds fast_lds(int ld, int w16) {
 // ...; word r kw + w of the page block is then tid, + T kw, ..., so consecutive threads store
 // consecutive dwords and every store instruction covers whole lines.  Each word comes from
 // 16 / 8 / 4 code bytes of its token's row; slots at or beyond the tier's count for this head
-// are masked to 0 (layout.py:84-85).  tid / kw = (int)((tid + 0.5) * (1 / kw)) in fp32 is exact
-// for tid < 512, kw <= 512 (checked exhaustively).
+// are masked to 0 (layout.py:84-85).  tid / kw = (int)((tid + 0.5) * rcp(kw)): the hardware
+// reciprocal's relative error (1 ulp) and the product's rounding leave the value within
+// 512 / kw * 2^-21 of (tid + 0.5) / kw, which lies at least 1 / (2 kw) from an integer, so the
+// truncation is exact for tid < 512.
 template <int Bits, int Ld>
 __device__ __forceinline__ void tier_words(const uint8_t* codes, int seg, int kw, int cnt, int32_t* out, int tid) {
     if (kw == 0) return;
     constexpr int kPer = 32 / Bits;
     const int T = kFastThreads / kw;
     if (tid >= T * kw) return;
-    const int r0 = static_cast<int>((static_cast<float>(tid) + 0.5f) * (1.0f / static_cast<float>(kw)));
+    const int r0 = static_cast<int>((static_cast<float>(tid) + 0.5f) * __builtin_amdgcn_rcpf(static_cast<float>(kw)));
     const int w = tid - r0 * kw;
     const int nv = min(max(cnt - kPer * w, 0), kPer);
     const uint32_t keep = nv >= kPer ? 0xffffffffu : (1u << (Bits * nv)) - 1u;
@@ -569,13 +576,9 @@ __device__ __forceinline__ void tier_words(const uint8_t* codes, int seg, int kw
     for (int r = r0; r < kFastP; r += T) {
         uint32_t word;
         if constexpr (Bits == 2) {
-            uint4 cb = *reinterpret_cast<const uint4*>(src);
-            cb.x &= 0x03030303u; cb.y &= 0x03030303u; cb.z &= 0x03030303u; cb.w &= 0x03030303u;
-            word = word_int2(cb);
+            word = word_int2(*reinterpret_cast<const uint4*>(src));
         } else if constexpr (Bits == 4) {
-            uint2 cb = *reinterpret_cast<const uint2*>(src);
-            cb.x &= 0x0f0f0f0fu; cb.y &= 0x0f0f0f0fu;
-            word = word_int4(cb);
+            word = word_int4(*reinterpret_cast<const uint2*>(src));
         } else {
             word = *reinterpret_cast<const uint32_t*>(src);
         }
@@ -695,7 +698,9 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& Lsrc, cons
     // page, element i = (token i / w16, slot i % w16) in memory order; padding slots are 0
     if (w16 > 0) {
         const int cnt = tcnt[3];
-        const float rk = 1.0f / static_cast<float>(w16);
+        // i / w16 as in tier_words: within 2^14 / w16 * 2^-21 of (i + 0.5) / w16, at least
+        // 1 / (2 w16) from an integer, for i < 128 w16
+        const float rk = __builtin_amdgcn_rcpf(static_cast<float>(w16));
         uint16_t* out = L.k_value16 + tok_row(L, b, h, dst_tok0) * w16;
         for (int i = tid; i < kFastP * w16; i += kFastThreads) {
             const int tau = static_cast<int>((static_cast<float>(i) + 0.5f) * rk), j = i - tau * w16;

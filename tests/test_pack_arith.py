@@ -25,3 +25,29 @@ def test_markstein_and_magic_codes_match_ieee(tmp_path):
     assert "differences 0" in out.stdout
     counts = out.stdout.split("magic ")[1]
     assert int(counts.split(",")[0]) > 0 and int(counts.split("clamped ")[1].split(")")[0]) > 0
+
+
+def test_reciprocal_row_division_is_exact():
+    """The compress kernel's Key-word and fp16-tier loops take row = i / k as
+    trunc((i + 0.5) * rcp(k)) with the hardware reciprocal (1 ulp): for every k and i they use
+    (k <= 512, i < 512; k <= 128, i < 128 k) any float within 2 ulps of 1 / k gives the exact
+    quotient.  Brute force over every case."""
+    import numpy as np
+
+    def near(r):
+        out = [r]
+        lo = hi = r
+        for _ in range(2):
+            lo = np.nextafter(lo, np.float32(0))
+            hi = np.nextafter(hi, np.float32(2))
+            out += [lo, hi]
+        return out
+
+    for kmax, n_of in ((512, lambda k: 512), (128, lambda k: 128 * k)):
+        for k in range(1, kmax + 1):
+            n = n_of(k)
+            t = np.arange(n, dtype=np.float32) + np.float32(0.5)
+            want = np.arange(n) // k
+            for r in near(np.float32(1.0) / np.float32(k)):
+                got = (t * np.float32(r)).astype(np.float32).astype(np.int64)
+                assert np.array_equal(got, want), (k, float(r))
