@@ -304,11 +304,11 @@ int pack_code_row(const lf_packed_layer& L);
 // ---------------------------------------------------------------------------------------
 // Fast path for the common shape: page = Key group = Value group = head_dim = 128, int2
 // Values, 2-byte inputs with 16-byte aligned rows.  Two workgroups of 512 threads per page and
-// kv head (blockIdx.z 0: Value page, 1: Key page -- every Value page is dispatched before the
-// Key pages: mixing the memory-bound Value pages with the VALU-bound Key pages measured slower,
-// in alternate single blocks and in runs of 8, and Key pages first left a longer tail, 1 %
-// slower), about 40 KB of LDS, so four share a CU (56 KB and two for the
-// widest tier mixes).  Per element the division uses a correctly rounded reciprocal of the group
+// kv head (blockIdx.z 0: Key page, 1: Value page -- every Key page is dispatched before the
+// Value pages, ≈1 % faster than the reverse order at the current kernel; mixing the VALU-bound
+// Key pages with the memory-bound Value pages measured slower, in alternate single blocks and in
+// runs of 8), about 40 KB of LDS, of which the kernel's SGPR count lets three share a CU (56 KB
+// and two for the widest tier mixes).  Per element the division uses a correctly rounded reciprocal of the group
 // scale and one Markstein correction (div_rn); groups whose scale is not clamped above take the
 // clamp-free magic_code.  The phases are listed at pack_fast_page.  Each integer tier has a
 // 16-byte aligned segment of a token's code row (in slot order), so a word's 16 / 8 / 4 code
@@ -753,7 +753,7 @@ template <bool IsHalf, int Ld>
 __global__ __launch_bounds__(kFastThreads) void pack_fast_kernel(PackJobArgs a) {
     const int job = blockIdx.x;
     pack_fast_page<IsHalf, Ld>(a.L, a.k_src, a.v_src, a.sb, a.sh, a.st, a.jobs[3 * job + 0], a.jobs[3 * job + 1],
-                           a.jobs[3 * job + 2], blockIdx.z == 0);
+                           a.jobs[3 * job + 2], blockIdx.z == 1);
 }
 
 // Several layers' pages in one launch: job = (layer, b, src_token0, dst_page); the layer's
@@ -771,7 +771,7 @@ __global__ __launch_bounds__(kFastThreads) void pack_fast_multi_kernel(PackMulti
     const lf_packed_layer& L = m.layers[layer];
     const lf_pack_source& S = m.srcs[layer];
     pack_fast_page<IsHalf, Ld>(L, S.k, S.v, S.stride_b, S.stride_h, S.stride_t, m.jobs[4 * job + 1], m.jobs[4 * job + 2],
-                           m.jobs[4 * job + 3], blockIdx.z == 0);
+                           m.jobs[4 * job + 3], blockIdx.z == 1);
 }
 
 // ``st``: the source's token stride in elements (the Key page is read through a buffer resource
@@ -865,7 +865,7 @@ int launch_pack_pages(const lf_packed_layer& L, const void* k_src, const void* v
         const int ld = code_ld(L);
         const size_t lds = pack_fast_lds_bytes(ld, L.k_width[3]);
         const bool half = src_dtype == LF_FP16;
-        const dim3 grid2(n_jobs, L.n_kv, 2);  // z: Value page, Key page
+        const dim3 grid2(n_jobs, L.n_kv, 2);  // z: Key page, Value page
         return ld == kCodeLdNarrow ? launch_fast_single<kCodeLdNarrow>(a, half, grid2, lds, stream)
                                    : launch_fast_single<kCodeLdWide>(a, half, grid2, lds, stream);
     }
@@ -901,7 +901,7 @@ int launch_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_l
     }
     const bool half = src_dtype == LF_FP16;
     PackMultiArgs m{layers_dev, srcs_dev, jobs};
-    const dim3 grid(n_jobs, layers_host[0].n_kv, 2);  // z: Value page, Key page
+    const dim3 grid(n_jobs, layers_host[0].n_kv, 2);  // z: Key page, Value page
     return ld == kCodeLdNarrow ? launch_fast_multi<kCodeLdNarrow>(m, half, grid, lds, stream)
                                : launch_fast_multi<kCodeLdWide>(m, half, grid, lds, stream);
 }
