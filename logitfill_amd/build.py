@@ -39,9 +39,10 @@ COMMON_FLAGS = [
 
 # Per-file additions.  decode_mfma.hip: the machine scheduler's max-ILP strategy, measured
 # 82.9-83.0 -> 80.7-81.2 us per c2 layer-step (same box; the page compress, built with it,
-# got slower, 121 -> 136 us, so it stays with the default).
+# got slower, 121 -> 136 us, so it stays with the default), and the scheduler's own register
+# pressure trackers (81.6-81.8 -> 80.6-80.8 us in a second same-box A/B).
 FILE_FLAGS = {
-    "decode_mfma.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "decode_mfma.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp", "-mllvm", "-amdgpu-use-amdgpu-trackers=1"],
 }
 
 
