@@ -41,8 +41,11 @@ COMMON_FLAGS = [
 # 82.9-83.0 -> 80.7-81.2 us per c2 layer-step (same box; the page compress, built with it,
 # got slower, 121 -> 136 us, so it stays with the default), and the scheduler's own register
 # pressure trackers (81.6-81.8 -> 80.6-80.8 us in a second same-box A/B).
+_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp", "-mllvm", "-amdgpu-use-amdgpu-trackers=1"]
+# decode_reduce.hip takes the same (c1 22.40-22.41 -> 22.31-22.33, c2 within 0.1-0.6 us lower).
 FILE_FLAGS = {
-    "decode_mfma.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp", "-mllvm", "-amdgpu-use-amdgpu-trackers=1"],
+    "decode_mfma.hip": _ILP,
+    "decode_reduce.hip": _ILP,
 }
 
 
