@@ -43,9 +43,12 @@ COMMON_FLAGS = [
 # pressure trackers (81.6-81.8 -> 80.6-80.8 us in a second same-box A/B).
 _ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp", "-mllvm", "-amdgpu-use-amdgpu-trackers=1"]
 # decode_reduce.hip takes the same (c1 22.40-22.41 -> 22.31-22.33, c2 within 0.1-0.6 us lower).
+# pack.hip: the trackers alone (c3 at targets 3.0 / 4.0 127.3-128.1 -> 126.4-126.9 and
+# 129.0-129.6 -> 128.1-128.4 us, 2.5 unchanged; with max-ILP it was slower, see above).
 FILE_FLAGS = {
     "decode_mfma.hip": _ILP,
     "decode_reduce.hip": _ILP,
+    "pack.hip": ["-mllvm", "-amdgpu-use-amdgpu-trackers=1"],
 }
 
 
