@@ -168,7 +168,9 @@ typedef struct lf_decode_args {
     const int32_t* tail_len;                  /* device int32 [batch], each in
                                                  0 .. min(tail_cap, page_size - 1): a full
                                                  residual page must be packed (flushed)
-                                                 first; larger values are clamped          */
+                                                 first; both kernels clamp larger values
+                                                 to that bound (a tail_len of page_size
+                                                 leaves the page's last row out)           */
     void* out; int32_t out_dtype;             /* [batch][n_q][head_dim]                 */
     int32_t n_q;
     float scaling;                            /* softmax scale (reference: attn.scaling) */
@@ -284,7 +286,9 @@ int32_t lf_append_token(void* tail_k, void* tail_v, int32_t tail_dtype, int32_t 
  * lf_unpack_ints -- layout.py:38-46: the first ``count`` slots of each row of ``words``
  * int32 [rows][n_words] as codes int32 [rows][count]; count <= n_words * (32 / bits).
  *
- * bits must divide 32 for pack / unpack (1, 2, 4, 8, 16).
+ * 1 <= bits <= 32 for pack / unpack, as the reference's per = 32 // bits: a width that does
+ * not divide 32 leaves the top 32 % bits bits of each word zero (3 bits: ten slots a word), a
+ * width above 16 takes one slot a word (bits 32: the words themselves).
  */
 int32_t lf_asymmetric_codes(const void* x, int32_t dtype, int64_t n_groups, int32_t group, int32_t bits,
                             int32_t* codes, float* scale, float* lo, void* stream);

@@ -278,7 +278,7 @@ int32_t lf_asymmetric_codes(const void* x, int32_t dtype, int64_t n_groups, int3
 }
 
 int32_t lf_pack_ints(const int32_t* codes, int64_t rows, int32_t n, int32_t bits, int32_t* words, void* stream) {
-    if (rows < 0 || n < 0 || bits <= 0 || 32 % bits != 0) return LF_E_SHAPE;
+    if (rows < 0 || n < 0 || bits <= 0 || bits > 32) return LF_E_SHAPE;
     if (rows == 0 || n == 0) return LF_OK;
     if (!codes || !words) return LF_E_NULL;
     const int per = 32 / bits;
@@ -288,7 +288,7 @@ int32_t lf_pack_ints(const int32_t* codes, int64_t rows, int32_t n, int32_t bits
 
 int32_t lf_unpack_ints(const int32_t* words, int64_t rows, int32_t n_words, int32_t count, int32_t bits,
                        int32_t* codes, void* stream) {
-    if (rows < 0 || n_words < 0 || count < 0 || bits <= 0 || 32 % bits != 0) return LF_E_SHAPE;
+    if (rows < 0 || n_words < 0 || count < 0 || bits <= 0 || bits > 32) return LF_E_SHAPE;
     if (static_cast<int64_t>(count) > static_cast<int64_t>(n_words) * (32 / bits)) return LF_E_SHAPE;
     if (rows == 0 || count == 0) return LF_OK;
     if (!words || !codes) return LF_E_NULL;

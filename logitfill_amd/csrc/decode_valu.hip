@@ -217,8 +217,9 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
         // Residual (kind 1, 2): the BF16 tail page then the new token(s) (reference.py:35-44).
         // With q_len new tokens, row i (token i % q_len) sees new tokens 0 .. i % q_len
         // (reference.py:18-27,48: the causal mask is right-aligned).  tail_len is clamped to
-        // the residual buffer.
-        const int tl = min(max(A.tail_len[b], 0), A.tail_cap);
+        // min(tail_cap, page_size - 1), as in the matrix-core kernel: a full residual page is
+        // packed before decode reads it, and a tail_len of page_size leaves the last row out.
+        const int tl = min(max(A.tail_len[b], 0), min(A.tail_cap, L.page_size - 1));
         const int q_len = p.q_len;
         const int n_new = A.k_new != nullptr ? q_len : 0;
         const int n_res = tl + n_new;

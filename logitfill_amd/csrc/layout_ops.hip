@@ -70,7 +70,8 @@ __global__ __launch_bounds__(256) void unpack_ints_kernel(const int32_t* words, 
     const int j = static_cast<int>(e - r * count);
     const int per = 32 / bits;
     const uint32_t word = static_cast<uint32_t>(words[r * n_words + j / per]);
-    codes[e] = static_cast<int32_t>((word >> ((j % per) * bits)) & ((1u << bits) - 1u));
+    const uint32_t mask = bits >= 32 ? 0xffffffffu : (1u << bits) - 1u;  // 1u << 32 is undefined
+    codes[e] = static_cast<int32_t>((word >> ((j % per) * bits)) & mask);
 }
 
 int grid_for(int64_t n, int per_block) {

@@ -91,15 +91,18 @@ class PackedDecoder:
 
     ``hf_cache=True`` passes a ``LogitFillCache`` as ``past_key_values`` (the reference adapter's
     ``make_cache``, ``deepseek_qwen.py:141-146``), so the model derives positions and mask sizes
-    from the packed length; otherwise the decoder passes the positions itself.  With
-    ``defer_flush`` (default) the manager leaves every layer's completed page for one
-    ``flush_pending`` launch after each forward pass instead of one launch per layer."""
+    from the packed length; otherwise the decoder passes the positions itself.
+
+    ``defer_flush``: None (default) keeps the manager's own setting; True or False sets it on
+    the manager.  A deferring manager leaves every layer's completed page for one
+    ``flush_pending`` launch after each forward pass (``step`` calls it) instead of one launch
+    per layer; results are the same either way."""
 
     def __init__(self, model, manager, attention_fn=packed_attention, *, hf_cache: bool = False,
-                 defer_flush: bool = True):
+                 defer_flush: bool | None = None):
         self.model, self.manager = model, manager
-        if defer_flush and hasattr(manager, "defer_flush"):
-            manager.defer_flush = True
+        if defer_flush is not None and hasattr(manager, "defer_flush"):
+            manager.defer_flush = bool(defer_flush)
         attach_packed(model, manager, attention_fn)
         self.cache = None
         if hf_cache:

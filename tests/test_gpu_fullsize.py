@@ -99,3 +99,35 @@ def test_config4_longest_contexts(gpu):
     for b in (int(order[-1]), int(order[-2]), int(order[0])):
         print(f"c4 shape: sequence {b}, {pages[b]} pages + {resid[b]}", flush=True)
         assert_decode_close(out[b], _oracle(d, mgr, b, n_q, n_kv, scaling))
+
+
+def test_config4_full_batch_bench_plan(gpu):
+    """c4 at its own workload: 32 sequences with the bench's seeded ragged contexts U[4K, 64K]
+    (``synth.ragged_lengths(32, seed=4)``, residuals 1-127), 40 q / 8 kv heads, target 2.5,
+    decoded with the automatic split the bench times (the planner's size, sequences dispatched
+    by decreasing item size).  Checked against the oracle: the first and the last sequence in
+    that dispatch order, the longest, the shortest and a middle one."""
+    from logitfill_amd.packed.reference import plan_work, residual_pages
+
+    B, n_q, n_kv = 32, 40, 8
+    pages, resid = synth.ragged_lengths(B, seed=4)
+    d, mgr = _build(gpu, B, n_q, n_kv, pages, resid, 2.5, seed=14)
+    scaling = 128 ** -0.5
+    q = d.query
+    out = torch.empty(q.shape, dtype=q.dtype, device=gpu)
+    decode_into(mgr, 0, q, d.key_new, d.value_new, scaling, out)   # the bench's call: auto kernel and split
+    torch.cuda.synchronize()
+    plan = mgr.layers[0].decode_plan
+    work = plan.work.cpu().numpy().reshape(-1, 4)
+    assert plan.n_work == work.shape[0] and plan.n_work > B        # split-K over ragged page counts
+    size = plan.pages_per_split
+    sizes = [size] * B if isinstance(size, int) else list(size)
+    want, _ = plan_work(pages, sizes, residual_pages(resid))
+    assert np.array_equal(work.reshape(-1), np.asarray(want))      # the plan the bench dispatches
+    dispatch = list(dict.fromkeys(int(b) for b in work[:, 0]))     # sequences in dispatch order
+    order = np.argsort(pages, kind="stable")
+    picks = dict.fromkeys([dispatch[0], dispatch[-1], int(order[-1]), int(order[0]), int(order[B // 2])])
+    for b in picks:
+        print(f"c4 batch 32: sequence {b}, {pages[b]} pages + {resid[b]}, "
+              f"{int((work[:, 0] == b).sum())} items", flush=True)
+        assert_decode_close(out[b], _oracle(d, mgr, b, n_q, n_kv, scaling))

@@ -45,11 +45,14 @@ def test_asymmetric_codes_bit_exact(gpu, dtype, group, bits):
     assert np.array_equal(low.cpu().numpy().view(np.uint32), want_l.view(np.uint32))
 
 
-@pytest.mark.parametrize("bits", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 8, 10, 16, 20, 32])
 @pytest.mark.parametrize("n", [1, 5, 16, 17, 40, 128])
 def test_pack_and_unpack_ints_bit_exact(gpu, bits, n):
+    """Every width of the reference's pack_ints (layout.py:21-46): per = 32 // bits slots a word,
+    so widths that do not divide 32 leave the top bits of each word zero (3 bits: ten slots,
+    bits 30-31 unused) and widths above 16 take one slot a word (bits 32: the words themselves)."""
     rng = np.random.default_rng(bits * 1000 + n)
-    codes = rng.integers(0, 1 << bits, size=(3, 5, n), dtype=np.int64).astype(np.int32)
+    codes = rng.integers(0, min(1 << bits, 1 << 31), size=(3, 5, n), dtype=np.int64).astype(np.int32)
     words = dl.pack_ints(torch.from_numpy(codes).to(gpu), bits)
     want = ol.pack_ints(codes, bits)
     assert tuple(words.shape) == want.shape

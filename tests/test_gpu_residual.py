@@ -69,3 +69,27 @@ def test_residual_paths_match_oracle(gpu, tail_dtype, new_dtype, pages, tail):
         ref = oatt.reference_attention(store, f32(d.query[b])[:, None, :], k_new, v_new, scaling, N_Q, N_KV)[:, 0, :]
         print(f"residual: tail {tail_dtype} x {tail}, new {new_dtype}, pages {pages}, sequence {b}", flush=True)
         assert_decode_close(out[b], ref, out_dtype="fp32")
+
+
+@pytest.mark.parametrize("kernel", [_native.KERNEL_MFMA, _native.KERNEL_VALU])
+def test_full_tail_length_is_clamped_alike(gpu, kernel):
+    """A raw caller that leaves tail_len at page_size (a full residual page not yet packed) gets
+    the same result from both kernels: each clamps tail_len to min(tail_cap, page_size - 1), as
+    the header documents, so the page's last row is left out -- the result equals a decode with
+    tail_len 127, bit for bit, whatever that row holds."""
+    d = synth.make_layer(B, N_Q, N_KV, D, 2 * 128 + 128, 2.5, seed=391, device=gpu)
+    mgr = PackedKVManager([d.levels], N_Q, N_KV, D, 128, 128, 128, 2, gpu, batch_size=B, capacity_tokens=256)
+    st = mgr.layers[0]
+    st.fill_pages(d.key, d.value, [2] * B)
+    st.set_tail(d.key[:, :, 256:383], d.value[:, :, 256:383], [127] * B)
+    scaling = D ** -0.5
+    want = torch.empty(B, N_Q, D, dtype=torch.float32, device=gpu)
+    decode_into(mgr, 0, d.query, d.key_new, d.value_new, scaling, want, kernel=kernel)
+    tk, tv = st.tail_buffers()
+    tk[:, :, 127].copy_(d.key[:, :, 383] * 50)      # a row that would move the result
+    tv[:, :, 127].copy_(d.value[:, :, 383] * 50)
+    st.tail_len_device().fill_(128)                 # what a raw ABI caller might pass
+    got = torch.empty_like(want)
+    decode_into(mgr, 0, d.query, d.key_new, d.value_new, scaling, got, kernel=kernel)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

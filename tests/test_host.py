@@ -168,7 +168,11 @@ def test_argument_validation_rejects_before_launch():
 def test_layout_helper_validation_rejects_before_launch():
     """The device layout helpers check sizes on the host; nothing is launched here."""
     lib = _native.load()
-    assert lib.lf_pack_ints(None, 1, 4, 3, None, None) == -2          # 3 does not divide 32
+    assert lib.lf_pack_ints(None, 1, 4, 33, None, None) == -2         # wider than a word
+    assert lib.lf_pack_ints(None, 1, 4, 0, None, None) == -2
+    assert lib.lf_pack_ints(None, 1, 4, 3, None, None) == -1          # 3 bits: ten slots a word
+    assert lib.lf_unpack_ints(None, 1, 1, 11, 3, None, None) == -2    # 11 slots > 1 word x 10
+    assert lib.lf_unpack_ints(None, 1, 1, 2, 32, None, None) == -2    # bits 32: one slot a word
     assert lib.lf_pack_ints(None, 0, 4, 2, None, None) == 0           # empty: nothing to do
     assert lib.lf_pack_ints(None, 1, 4, 2, None, None) == -1
     assert lib.lf_unpack_ints(None, 1, 1, 17, 2, None, None) == -2    # 17 slots > 1 word x 16

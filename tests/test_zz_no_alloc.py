@@ -61,8 +61,9 @@ def test_noalloc_refuses_partials_beyond_the_array(gpu):
     n_work = limit // lib.lf_decode_workspace_bytes(28, 128, 1) + 1       # one item past the limit
     plan = DecodePlan([4], 4, 1, gpu, residual_pages([2]))
     a = _native.DecodeArgs()
-    a.query, a.q_dtype = d.query.data_ptr(), _native.LF_BF16
-    a.out, a.out_dtype = d.query.data_ptr(), _native.LF_BF16
+    # query and out stay NULL: were the size check to regress, the call would fall through to
+    # the argument checks and return LF_E_NULL without launching anything
+    a.q_dtype, a.out_dtype = _native.LF_BF16, _native.LF_BF16
     a.tail_len = layer.tail_len_device().data_ptr()
     a.n_q, a.scaling, a.q_len = 28, 1.0, 1
     a.work, a.seq_work, a.n_work = plan.work.data_ptr(), plan.seq_work.data_ptr(), n_work
