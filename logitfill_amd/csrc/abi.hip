@@ -93,18 +93,17 @@ int32_t decode_checked(const lf_packed_layer* layer, const lf_decode_args* args,
     // q_len new tokens: the kernels serve n_q * q_len query rows (row = head * q_len + token)
     const int64_t rows = static_cast<int64_t>(A.n_q) * q_len;
     if (rows > (1 << 20)) return LF_E_SHAPE;
+    // rows per kv head: any number (the kernels tile them across workgroups)
     const int g = static_cast<int>(rows / layer->n_kv);
-    if (g > 16) return LF_E_UNSUPPORTED;
     if (layer->bit_v != 2) return LF_E_UNSUPPORTED;  // as reference.py:62
     const int D = layer->head_dim;
-    if (D < 8 || D > 512 || (D & (D - 1)) != 0) return LF_E_UNSUPPORTED;
+    if (D < 8 || D > 1024 || (D & (D - 1)) != 0) return LF_E_UNSUPPORTED;  // as kernel.cu:224-230
     if (layer->v_groups > 64) return LF_E_UNSUPPORTED;
     if (A.tail_cap < 0 || A.tail_cap > layer->page_size) return LF_E_SHAPE;
     if (A.tail_cap > 0 && (!A.tail_k || !A.tail_v)) return LF_E_NULL;
     if (A.n_work <= 0 || static_cast<int64_t>(A.n_work) * layer->n_kv > 0x7fffffff) return LF_E_SHAPE;
     if (workspace_bytes < lf_decode_workspace_bytes(static_cast<int32_t>(rows), D, A.n_work)) return LF_E_WORKSPACE;
     if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
-    if (q_len > 1 && A.kernel == 2) return LF_E_UNSUPPORTED;  // the MFMA kernel takes one token
 
     DecodeParams p;
     p.L = *layer;
@@ -118,7 +117,7 @@ int32_t decode_checked(const lf_packed_layer* layer, const lf_decode_args* args,
     p.part = static_cast<float*>(workspace);
     p.dense_splits = 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (A.kernel != 1 && q_len == 1) {
+    if (A.kernel != 1) {
         bool handled = false;
         const int r = launch_decode_mfma(p, s, &handled);
         if (handled || A.kernel == 2) return handled ? r : LF_E_UNSUPPORTED;
@@ -162,7 +161,7 @@ int32_t lf_pack_pages(const lf_packed_layer* layer, const void* k_src, const voi
     if (n_jobs < 0 || n_jobs > kMaxPackJobs) return LF_E_SHAPE;
     if (n_jobs == 0) return LF_OK;
     if (!k_src || !v_src || !jobs) return LF_E_NULL;
-    if (layer->page_size > 1024 || layer->head_dim > 512) return LF_E_SHAPE;
+    if (layer->page_size > 1024 || layer->head_dim > 1024) return LF_E_SHAPE;
     return lf::launch_pack_pages(*layer, k_src, v_src, src_dtype, src_stride_b, src_stride_h, src_stride_t,
                                  jobs, n_jobs, static_cast<hipStream_t>(stream));
 }

@@ -4,9 +4,10 @@
 // softmax attention over [history ; tail ; new]); replaces the CUDA kernel
 // src/logitfill/packed/kernel.cu:112-190.  Shapes served: head_dim 128,
 // page = Key group = 128 tokens, one Value group per token (v_group 128), int2
-// Values, 1 <= g = n_q/n_kv <= 8.  Anything else runs the VALU kernel.
+// Values, any number of query rows per kv head ((n_q / n_kv) * q_len, row = head * q_len +
+// token, served 8 rows per workgroup).  Anything else runs the VALU kernel.
 //
-// Work: one workgroup of 4 waves per (split item, kv head); wave w computes
+// Work: one workgroup of 4 waves per (split item, kv head, tile of 8 query rows); wave w computes
 // tokens 32w..32w+31 (two 16-token tiles) of every page of the item.  Pages arrive by LDS-DMA
 // (global_load_lds) into a ring of two page slots, one page ahead of the page being computed.
 // Per page: a barrier (the page landed, the previous page is computed), the page's
@@ -166,6 +167,7 @@ struct MfmaParams {
     MfmaLayout y;
     UnpackBits k;
     int res_mfma;  // residual pass: 0 VALU, 1 bf16 matrix cores, 2 fp16 matrix cores (residual_mfma)
+    int n_rt;      // row tiles per kv head: ceil(p.g / 8)
 };
 
 // Tier-local rank of position ``pos`` (0..7) of local block ``lb``.  Register r of a
@@ -586,14 +588,15 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
     if (lane < 8) reinterpret_cast<float*>(ck + kCkBias)[4 * lane + wave] = bsum;
 }
 
-// q of the workgroup's heads, scaled into the log2 domain, into qlin [8][128] (0 for heads >= g).
-__device__ __forceinline__ void load_q(const DecodeParams& p, int b, int h, float* qlin, int tid) {
+// q of the workgroup's rows row0 .. row0 + g - 1, scaled into the log2 domain, into qlin [8][128]
+// (0 for rows >= g).
+__device__ __forceinline__ void load_q(const DecodeParams& p, int b, int h, int row0, int g, float* qlin, int tid) {
     const lf_decode_args& A = p.A;
     for (int e = tid; e < 8 * kD; e += kThreads) {
         const int n = e / kD, c = e % kD;
-        qlin[e] = n < p.g ? load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * p.g + n) * kD + c, A.q_dtype) *
-                                p.qscale
-                          : 0.f;
+        qlin[e] = n < g ? load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * p.g + row0 + n) * kD + c,
+                                      A.q_dtype) * p.qscale
+                        : 0.f;
     }
 }
 
@@ -723,33 +726,45 @@ __device__ __forceinline__ void score_tiles_fixed(const KTiles& t, const UnpackB
 }
 
 // Residual pass on the matrix cores, for 2-byte tail and new-token rows of one dtype (Bf: bf16,
-// else fp16) with 16-byte aligned rows.  The residual is one dense page: token tt < tl is tail
-// row tt, token tl the new token, tokens past them are masked (rows read for them are the new
-// row, or tail row 0 when there is none, so every value read is a stored one).  Wave w takes
-// tokens 32w..32w+31 as two 16-row tiles:
+// else fp16) with 16-byte aligned rows.  The residual is the tl tail rows followed by the new
+// tokens (q_len of them, or none), taken as dense chunks of 128 tokens: token tt < tl is tail row
+// tt, token tl + j new token j, tokens past them are masked (rows read for them are stored rows:
+// new token 0, or tail row 0 when there is none, so every value read is a stored one).  New token
+// j is masked for query rows whose token index (row % q_len) is below j -- the right-aligned
+// causal mask of reference.py:18-27,48 (with one new token nothing is masked but the chunk's
+// end).  Wave w takes tokens c0 + 32w .. + 31 of each chunk as two 16-row tiles:
 //   scores  S^T = K . Qb^T: the A operand (lane: token row n16, channels 32 kb + 8 s .. + 7 of
 //           K-step s) straight from global memory; Qb = the LDS query (q * scaling * log2 e)
 //           split hi (columns 0..7) / lo (columns 8..15), recombined by one DPP add;
 //   values  O = P . V with P = 2^(s - m) split hi (rows 0..7) / lo (rows 8..15): the score
 //           accumulator layout is the A-operand layout; the wave's 32 V rows arrive by LDS-DMA
 //           into its own 8 KB of ``vst`` and each lane gathers its 8 tokens of one channel.
-// One pass per wave (its max is final); the wave's (m, l, o) go to partial slot ``rw`` with a
-// zero midpoint term.  ``vst`` may overlap partial slots other than 0..3: the stores wait for
-// every wave's last V read.
+// A chunk after the first (only when tl + q_len > 128) rescales the wave's running (m, l, O) by
+// 2^(m_old - m_new).  The wave's (m, l, o) go to partial slot ``rw`` with a zero midpoint term.
+// ``vst`` may overlap partial slots other than 0..3: the stores wait for every wave's last V read.
 template <bool Bf>
-__device__ __forceinline__ void residual_mfma(const DecodeParams& p, int b, int h, int rw, int tl, float* qlin,
-                                              float* red, float* wstat, unsigned char* vst, int tid) {
+__device__ __forceinline__ void residual_mfma(const DecodeParams& p, int b, int h, int row0, int g, int rw, int tl,
+                                              float* qlin, float* red, float* wstat, float* alpha_lds,
+                                              unsigned char* vst, int tid) {
     using T8 = typename std::conditional<Bf, bf16x8, half8>::type;
     const lf_decode_args& A = p.A;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n16 = lane & 15, kb = lane >> 4;
     const bool has_new = A.k_new != nullptr;
-    const int n_res = tl + (has_new ? 1 : 0);
+    const int q_len = p.q_len;
+    const int n_res = tl + (has_new ? q_len : 0);
     const int64_t bh = static_cast<int64_t>(b) * p.L.n_kv + h;
     const uint16_t* tk = static_cast<const uint16_t*>(A.tail_k) + bh * A.tail_cap * kD;
     const uint16_t* tv = static_cast<const uint16_t*>(A.tail_v) + bh * A.tail_cap * kD;
-    const uint16_t* fk = has_new ? static_cast<const uint16_t*>(A.k_new) + bh * kD : tk;
-    const uint16_t* fv = has_new ? static_cast<const uint16_t*>(A.v_new) + bh * kD : tv;
+    // new token 0 of this (b, h): k_new / v_new are [batch][n_kv][q_len][128]
+    const uint16_t* fk = has_new ? static_cast<const uint16_t*>(A.k_new) + bh * q_len * kD : tk;
+    const uint16_t* fv = has_new ? static_cast<const uint16_t*>(A.v_new) + bh * q_len * kD : tv;
+    // the row of residual token tt (a stored row for masked tokens)
+    auto row_of = [&](const uint16_t* tail, const uint16_t* fresh, int tt) -> const uint16_t* {
+        return tt < tl ? tail + static_cast<int64_t>(tt) * kD : tt < n_res ? fresh + static_cast<int64_t>(tt - tl) * kD : fresh;
+    };
+    // token index of the query row in score column n16 (lanes n16 < 8 hold the hi + lo sums)
+    const int tq = (row0 + (n16 & 7)) % q_len;
     float O[8][4];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
@@ -757,121 +772,144 @@ __device__ __forceinline__ void residual_mfma(const DecodeParams& p, int b, int 
         for (int r = 0; r < 4; ++r) O[nt][r] = 0.f;
     float mx = -__builtin_inff(), lsum = 0.f;
     if (n_res > 0) {  // uniform over the workgroup
-        // V rows by LDS-DMA: instruction i moves rows 32 w + 4 i .. + 3 (16 lanes per row)
-        const uint32_t vbase = lds_addr(vst) + 8192 * wave;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int tt = 32 * wave + 4 * i + (lane >> 4);
-            const uint16_t* row = tt < tl ? tv + static_cast<int64_t>(tt) * kD : fv;
-            dma16(reinterpret_cast<const unsigned char*>(row + 8 * (lane & 15)), vbase + 1024 * i);
-        }
-        uint4 ka[2][4];
-#pragma unroll
-        for (int tile = 0; tile < 2; ++tile) {
-            const int tt = 32 * wave + 16 * tile + n16;
-            const uint4* row = reinterpret_cast<const uint4*>((tt < tl ? tk + static_cast<int64_t>(tt) * kD : fk) + 32 * kb);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) ka[tile][s] = row[s];
-        }
-        load_q(p, b, h, qlin, tid);  // its wait also covers the K and V loads: one round trip
-        __syncthreads();             // q in LDS
         T8 bq[4];
-        {
-            const float4* q4 = reinterpret_cast<const float4*>(qlin + (n16 & 7) * kD + 32 * kb);
-            const bool lo = n16 >= 8;
+        for (int c0 = 0; c0 < n_res; c0 += kPage) {  // uniform over the workgroup
+            // V rows by LDS-DMA: instruction i moves rows 32 w + 4 i .. + 3 (16 lanes per row)
+            const uint32_t vbase = lds_addr(vst) + 8192 * wave;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const float4 a = q4[2 * s], c = q4[2 * s + 1];
-                const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            for (int i = 0; i < 8; ++i) {
+                const int tt = c0 + 32 * wave + 4 * i + (lane >> 4);
+                dma16(reinterpret_cast<const unsigned char*>(row_of(tv, fv, tt) + 8 * (lane & 15)), vbase + 1024 * i);
+            }
+            uint4 ka[2][4];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    if constexpr (Bf) {
-                        const __bf16 hi = static_cast<__bf16>(x[j]);
-                        bq[s][j] = lo ? static_cast<__bf16>(x[j] - static_cast<float>(hi)) : hi;
-                    } else {
-                        const _Float16 hi = static_cast<_Float16>(x[j]);
-                        bq[s][j] = lo ? static_cast<_Float16>(x[j] - static_cast<float>(hi)) : hi;
+            for (int tile = 0; tile < 2; ++tile) {
+                const int tt = c0 + 32 * wave + 16 * tile + n16;
+                const uint4* row = reinterpret_cast<const uint4*>(row_of(tk, fk, tt) + 32 * kb);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) ka[tile][s] = row[s];
+            }
+            if (c0 == 0) {
+                load_q(p, b, h, row0, g, qlin, tid);  // its wait also covers the K and V loads: one round trip
+                __syncthreads();                      // q in LDS
+                const float4* q4 = reinterpret_cast<const float4*>(qlin + (n16 & 7) * kD + 32 * kb);
+                const bool lo = n16 >= 8;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const float4 a = q4[2 * s], c = q4[2 * s + 1];
+                    const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        if constexpr (Bf) {
+                            const __bf16 hi = static_cast<__bf16>(x[j]);
+                            bq[s][j] = lo ? static_cast<__bf16>(x[j] - static_cast<float>(hi)) : hi;
+                        } else {
+                            const _Float16 hi = static_cast<_Float16>(x[j]);
+                            bq[s][j] = lo ? static_cast<_Float16>(x[j] - static_cast<float>(hi)) : hi;
+                        }
                     }
                 }
-            }
-        }
-        float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            if constexpr (Bf) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[0][s]), bq[s], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[1][s]), bq[s], acc1, 0, 0, 0);
             } else {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[0][s]), bq[s], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[1][s]), bq[s], acc1, 0, 0, 0);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this chunk's V rows have landed
+            }
+            float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if constexpr (Bf) {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[0][s]), bq[s], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[1][s]), bq[s], acc1, 0, 0, 0);
+                } else {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[0][s]), bq[s], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[1][s]), bq[s], acc1, 0, 0, 0);
+                }
+            }
+            // hi + lo columns (lanes n16 < 8: row n16, tokens 4 kb + r of each tile); masked -inf
+            const int tb = c0 + 32 * wave + 4 * kb;
+            const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
+            float sv[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const int xi = __builtin_bit_cast(int, accs[r]);
+                const float sum = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
+                const int tt = tb + (r & 3) + 16 * (r >> 2);
+                sv[r] = tt < n_res && tt - tl <= tq ? sum : -__builtin_inff();
+            }
+            float cm = sv[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) cm = fmaxf(cm, sv[i]);
+            cm = rows_max(cm);
+            const float m_new = fmaxf(mx, cm);
+            const float moff = m_new == -__builtin_inff() ? 0.f : m_new;
+            if (c0 > 0) {
+                // rescale the running sums: O row 4 kb + r holds row (4 kb + r) % 8 of the tile,
+                // whose factor lane (kb 0, n16 = that row) publishes
+                const float alpha = __builtin_amdgcn_exp2f(mx - moff);
+                lsum *= alpha;
+                if (kb == 0 && n16 < 8) alpha_lds[wave * 8 + n16] = alpha;
+                __builtin_amdgcn_wave_barrier();
+                const float4 arow = *reinterpret_cast<const float4*>(alpha_lds + wave * 8 + 4 * (kb & 1));
+#pragma unroll
+                for (int nt = 0; nt < 8; ++nt) {
+                    O[nt][0] *= arow.x;
+                    O[nt][1] *= arow.y;
+                    O[nt][2] *= arow.z;
+                    O[nt][3] *= arow.w;
+                }
+            }
+            mx = m_new;
+            float pp[8], psum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                pp[i] = __builtin_amdgcn_exp2f(sv[i] - moff);
+                psum += pp[i];
+            }
+            lsum += rows_sum(psum);
+            // A operand: k = 8 kb + j <-> token 4 kb + j (tile 0, j < 4) / 16 + 4 kb + j - 4 (tile 1);
+            // hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8
+            uint32_t ahi[4], alo[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float x0 = pp[2 * j], x1 = pp[2 * j + 1];
+                uint16_t hb[2], lb[2];
+                if constexpr (Bf) {
+                    const __bf16 h0 = static_cast<__bf16>(x0), h1 = static_cast<__bf16>(x1);
+                    const __bf16 l0 = static_cast<__bf16>(x0 - static_cast<float>(h0)), l1 = static_cast<__bf16>(x1 - static_cast<float>(h1));
+                    hb[0] = __builtin_bit_cast(uint16_t, h0); hb[1] = __builtin_bit_cast(uint16_t, h1);
+                    lb[0] = __builtin_bit_cast(uint16_t, l0); lb[1] = __builtin_bit_cast(uint16_t, l1);
+                } else {
+                    const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
+                    const _Float16 l0 = static_cast<_Float16>(x0 - static_cast<float>(h0)), l1 = static_cast<_Float16>(x1 - static_cast<float>(h1));
+                    hb[0] = __builtin_bit_cast(uint16_t, h0); hb[1] = __builtin_bit_cast(uint16_t, h1);
+                    lb[0] = __builtin_bit_cast(uint16_t, l0); lb[1] = __builtin_bit_cast(uint16_t, l1);
+                }
+                ahi[j] = hb[0] | (static_cast<uint32_t>(hb[1]) << 16);
+                alo[j] = lb[0] | (static_cast<uint32_t>(lb[1]) << 16);
+            }
+            uint4 au;
+            au.x = __builtin_amdgcn_update_dpp(ahi[0], alo[0], 0x118, 0xf, 0xc, false);
+            au.y = __builtin_amdgcn_update_dpp(ahi[1], alo[1], 0x118, 0xf, 0xc, false);
+            au.z = __builtin_amdgcn_update_dpp(ahi[2], alo[2], 0x118, 0xf, 0xc, false);
+            au.w = __builtin_amdgcn_update_dpp(ahi[3], alo[3], 0x118, 0xf, 0xc, false);
+            // this wave's V rows have landed (the first chunk's barrier waited for all of its vector
+            // memory, later chunks wait above)
+            const uint16_t* vs = reinterpret_cast<const uint16_t*>(vst + 8192 * wave);
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) {
+                const int c = 16 * nt + n16;
+                uint16_t e[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) e[j] = vs[(4 * kb + (j & 3) + 16 * (j >> 2)) * kD + c];
+                const uint4 bu = {e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16),
+                                  e[4] | (static_cast<uint32_t>(e[5]) << 16), e[6] | (static_cast<uint32_t>(e[7]) << 16)};
+                float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
+                if constexpr (Bf)
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, au), __builtin_bit_cast(bf16x8, bu), o4, 0, 0, 0);
+                else
+                    o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, au), __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
+                O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
             }
         }
-        // hi + lo columns (lanes n16 < 8: head n16, tokens 4 kb + r of each tile); masked -inf
-        const int tb = 32 * wave + 4 * kb;
-        const float accs[8] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1], acc1[2], acc1[3]};
-        float sv[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int xi = __builtin_bit_cast(int, accs[r]);
-            const float sum = accs[r] + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x108, 0xf, 0xf, true));
-            sv[r] = tb + (r & 3) + 16 * (r >> 2) < n_res ? sum : -__builtin_inff();
-        }
-        mx = sv[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-        mx = rows_max(mx);
-        const float moff = mx == -__builtin_inff() ? 0.f : mx;
-        float pp[8], psum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            pp[i] = __builtin_amdgcn_exp2f(sv[i] - moff);
-            psum += pp[i];
-        }
-        lsum = rows_sum(psum);
-        // A operand: k = 8 kb + j <-> token 4 kb + j (tile 0, j < 4) / 16 + 4 kb + j - 4 (tile 1);
-        // hi in lanes n16 < 8, lo (moved 8 lanes up) in lanes n16 >= 8
-        uint32_t ahi[4], alo[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float x0 = pp[2 * j], x1 = pp[2 * j + 1];
-            uint16_t hb[2], lb[2];
-            if constexpr (Bf) {
-                const __bf16 h0 = static_cast<__bf16>(x0), h1 = static_cast<__bf16>(x1);
-                const __bf16 l0 = static_cast<__bf16>(x0 - static_cast<float>(h0)), l1 = static_cast<__bf16>(x1 - static_cast<float>(h1));
-                hb[0] = __builtin_bit_cast(uint16_t, h0); hb[1] = __builtin_bit_cast(uint16_t, h1);
-                lb[0] = __builtin_bit_cast(uint16_t, l0); lb[1] = __builtin_bit_cast(uint16_t, l1);
-            } else {
-                const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
-                const _Float16 l0 = static_cast<_Float16>(x0 - static_cast<float>(h0)), l1 = static_cast<_Float16>(x1 - static_cast<float>(h1));
-                hb[0] = __builtin_bit_cast(uint16_t, h0); hb[1] = __builtin_bit_cast(uint16_t, h1);
-                lb[0] = __builtin_bit_cast(uint16_t, l0); lb[1] = __builtin_bit_cast(uint16_t, l1);
-            }
-            ahi[j] = hb[0] | (static_cast<uint32_t>(hb[1]) << 16);
-            alo[j] = lb[0] | (static_cast<uint32_t>(lb[1]) << 16);
-        }
-        uint4 au;
-        au.x = __builtin_amdgcn_update_dpp(ahi[0], alo[0], 0x118, 0xf, 0xc, false);
-        au.y = __builtin_amdgcn_update_dpp(ahi[1], alo[1], 0x118, 0xf, 0xc, false);
-        au.z = __builtin_amdgcn_update_dpp(ahi[2], alo[2], 0x118, 0xf, 0xc, false);
-        au.w = __builtin_amdgcn_update_dpp(ahi[3], alo[3], 0x118, 0xf, 0xc, false);
-        // this wave's V rows have landed (the barrier above waited for all of its vector memory)
-        const uint16_t* vs = reinterpret_cast<const uint16_t*>(vst + 8192 * wave);
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-            const int c = 16 * nt + n16;
-            uint16_t e[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) e[j] = vs[(4 * kb + (j & 3) + 16 * (j >> 2)) * kD + c];
-            const uint4 bu = {e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16),
-                              e[4] | (static_cast<uint32_t>(e[5]) << 16), e[6] | (static_cast<uint32_t>(e[7]) << 16)};
-            float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
-            if constexpr (Bf)
-                o4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, au), __builtin_bit_cast(bf16x8, bu), o4, 0, 0, 0);
-            else
-                o4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, au), __builtin_bit_cast(half8, bu), o4, 0, 0, 0);
-            O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];
-        }
-        // rows r (hi) + r + 8 (lo): lanes kb < 2 hold heads 4 kb + r
+        // rows r (hi) + r + 8 (lo): lanes kb < 2 hold rows 4 kb + r
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
@@ -901,16 +939,34 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const lf_packed_layer& L = p.L;
     const lf_decode_args& A = p.A;
     // Item-major: workgroup id = item * n_kv + h, so the work list's order is the dispatch
-    // order (the host's split plan relies on it).
+    // order (the host's split plan relies on it).  With more than 8 query rows per kv head the
+    // rows come in tiles of 8, one workgroup each: the n_rt tiles of (item, h) pair u take ids
+    // ((u / 8) * n_rt + rt) * 8 + u % 8.  Workgroup ids go round-robin over the 8 XCDs, so a
+    // pair's tiles run on one XCD, close together in time, and its later tiles read the pages
+    // from that XCD's L2; ids past the last pair (the grid is padded to whole groups of 8 pairs)
+    // return at once.
     const int n_kv = L.n_kv;
-    const int item = blockIdx.x / n_kv;
-    const int h = blockIdx.x - item * n_kv;
+    const int n_rt = mp.n_rt;
+    int item, h, rt = 0;
+    if (n_rt == 1) {
+        item = blockIdx.x / n_kv;
+        h = blockIdx.x - item * n_kv;
+    } else {
+        const int x8 = static_cast<int>(blockIdx.x >> 3);
+        const int grp = x8 / n_rt;
+        rt = x8 - grp * n_rt;
+        const int u = 8 * grp + static_cast<int>(blockIdx.x & 7);
+        if (u >= A.n_work * n_kv) return;
+        item = u / n_kv;
+        h = u - item * n_kv;
+    }
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n16 = lane & 15;  // MFMA column / row index
     const int kb = lane >> 4;   // lane group
-    const int g = p.g;
+    const int row0 = 8 * rt;              // this tile's rows row0 .. row0 + g - 1 of the kv head's p.g
+    const int g = min(8, p.g - row0);
     const int b = A.work[4 * item + 0];
     const int pbeg = A.work[4 * item + 1];
     const int pend = A.work[4 * item + 2];
@@ -983,7 +1039,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         const int qn = tid >> 5, qc0 = 4 * (tid & 31);
         float4 q4 = {0.f, 0.f, 0.f, 0.f};
         if (qn < g) {
-            const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * g + qn) * kD + qc0;
+            const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * p.g + row0 + qn) * kD + qc0;
             q4.x = load_as_f32(A.query, qrow + 0, A.q_dtype) * p.qscale;
             q4.y = load_as_f32(A.query, qrow + 1, A.q_dtype) * p.qscale;
             q4.z = load_as_f32(A.query, qrow + 2, A.q_dtype) * p.qscale;
@@ -1257,10 +1313,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         const int cap = min(A.tail_cap, kPage);
         const int tl = min(max(A.tail_len[b], 0), min(cap, kPage - 1));
         unsigned char* vst = reinterpret_cast<unsigned char*>(red + kWaves * 8 * kD);
-        if (mp.res_mfma == 1) residual_mfma<true>(p, b, h, rw, tl, qlin, red, wstat, vst, tid);
-        else residual_mfma<false>(p, b, h, rw, tl, qlin, red, wstat, vst, tid);
+        if (mp.res_mfma == 1) residual_mfma<true>(p, b, h, row0, g, rw, tl, qlin, red, wstat, alpha_lds, vst, tid);
+        else residual_mfma<false>(p, b, h, row0, g, rw, tl, qlin, red, wstat, alpha_lds, vst, tid);
     } else if (kind != 0) {
         // ---- residual (kind 1, 2): the tail page and the new token (at most page_size tokens) ----
+        // One new token (q_len 1; the host sends other calls with a residual to the VALU kernel).
         // VALU: wave w scores tokens 32w..32w+31 (lane % 32 = token, lane / 32 = channel half;
         // q read as float4 from LDS), then accumulates them into channels 2*lane, 2*lane+1.
         // One pass, so each wave's max is final.  For 2-byte residual and new-token rows every
@@ -1274,7 +1331,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         const int ch0 = 64 * (lane >> 5);
         const bool has_new = A.k_new != nullptr;
         const bool two_byte = A.tail_dtype != LF_FP32 && (!has_new || A.new_dtype != LF_FP32);
-        load_q(p, b, h, qlin, tid);
+        load_q(p, b, h, row0, g, qlin, tid);
         const int tl = min(max(A.tail_len[b], 0), min(cap, kPage - 1));
         float kv[64];
         float v0[32], v1[32];
@@ -1427,7 +1484,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 l += sc * wstat[(w * 3 + 1) * 8 + i];
             }
         }
-        float* rec = part_rec(p, item, h, i);
+        float* rec = part_rec(p, item, h, row0 + i);
         rec[c] = o;
         if (c == 0) {
             rec[kD] = M;
@@ -1444,7 +1501,7 @@ bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>
 bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     if (L.head_dim != kD || L.page_size != kPage || L.k_group != kPage || L.bit_v != 2 || L.v_group != kD)
         return false;
-    if (g < 1 || g > 8) return false;
+    if (g < 1) return false;
     if (L.cap_kgroups % 2 != 0) return false;  // Key scale/min are fetched as page pairs
     if (L.k_width[0] + L.k_width[1] + L.k_width[2] == 0) return false;
     for (int t = 0; t < 3; ++t)
@@ -1524,14 +1581,20 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
     const bool rows16 = (!has_tail || (aligned(p.A.tail_k, 16) && aligned(p.A.tail_v, 16))) &&
                         (!has_new || (aligned(p.A.k_new, 16) && aligned(p.A.v_new, 16)));
     mp.res_mfma = (has_tail || has_new) && one_dtype && rows16 && res_dt != LF_FP32 ? (res_dt == LF_BF16 ? 1 : 2) : 0;
-    if (!rows_aligned || !plan_layout(p.L, p.g, mp.y)) {
+    // Several new tokens need the matrix-core residual pass (the VALU pass takes one).
+    const bool res_ok = p.q_len == 1 || mp.res_mfma != 0 || (!has_tail && !has_new);
+    if (!rows_aligned || !res_ok || !plan_layout(p.L, p.g, mp.y)) {
         *handled = false;
         return LF_OK;
     }
+    mp.n_rt = (p.g + 7) / 8;
+    const int64_t pairs = static_cast<int64_t>(p.A.n_work) * p.L.n_kv;
+    const int64_t blocks = mp.n_rt == 1 ? pairs : (pairs + 7) / 8 * 8 * mp.n_rt;
+    if (blocks > 0x7fffffff) return LF_E_SHAPE;
     *handled = true;
     const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&decode_mfma_kernel), mp.y.lds_bytes);
     if (rc != LF_OK) return rc;
-    hipLaunchKernelGGL(decode_mfma_kernel, dim3(p.A.n_work * p.L.n_kv), dim3(kThreads), mp.y.lds_bytes, stream, mp);
+    hipLaunchKernelGGL(decode_mfma_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), mp.y.lds_bytes, stream, mp);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);
     return launch_decode_reduce(p, stream);

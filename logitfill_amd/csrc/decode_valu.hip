@@ -11,35 +11,39 @@
 // channels for the value accumulation.  The Key scale is folded into the
 // query once per Key group:
 //     score_i = sum_c q_ic (code_c s_c + m_c) = sum_slot (q s)_slot code_slot + sum_c q_ic m_c
-// This kernel is the general path (any g <= 16, head_dim a power of two in 8..512, up to 64
-// Value groups, Value rows of ceil(D / 16) words); the MFMA kernel covers the fast shapes.
+// This kernel is the general path (any number of query rows per kv head, head_dim a power of two
+// in 8..1024, up to 64 Value groups, Value rows of ceil(D / 16) words); the MFMA kernel covers
+// the fast shapes.  Query rows are served in tiles of G rows (16, or 8 at head_dim 1024 to keep
+// the LDS within 160 KB): workgroup (item, kv head, tile) holds rows G * tile .. + G - 1 of its kv
+// head, so any GQA group (MQA included) and any number of new tokens stays on the kernel.
 #include "decode_common.hpp"
 
 namespace lf {
 namespace {
 
-constexpr int kMaxG = 16;
+// Query rows per workgroup (the row tile) at head_dim D.
+__host__ __device__ constexpr int valu_tile_rows(int D) { return D > 512 ? 8 : 16; }
 
 // Dynamic LDS of one workgroup (floats unless noted), in this order:
-//   qT    [D][kMaxG]        q * scaling * log2(e), channel-major
-//   p     [64][kMaxG]       probabilities of the current chunk
+//   qT    [D][G]            q * scaling * log2(e), channel-major
+//   p     [64][G]           probabilities of the current chunk
 //   vsc   [64][v_groups]    Value scale per token and channel group
 //   vmn   [64][v_groups]    Value min
 //   vcode [64][v_words]     Value code words of the chunk (uint32)
-//   qp    [n_slots][kMaxG]  q * Key scale per tier slot of the current Key group
+//   qp    [n_slots][G]      q * Key scale per tier slot of the current Key group
 struct ValuLds {
     int qT, p, vsc, vmn, vcode, qp, total;
 };
 
-__host__ __device__ inline ValuLds valu_lds(int D, int v_groups, int v_words, int n_slots) {
+__host__ __device__ inline ValuLds valu_lds(int D, int G, int v_groups, int v_words, int n_slots) {
     ValuLds o;
     int off = 0;
-    o.qT = off;    off += D * kMaxG * 4;
-    o.p = off;     off += 64 * kMaxG * 4;
+    o.qT = off;    off += D * G * 4;
+    o.p = off;     off += 64 * G * 4;
     o.vsc = off;   off += 64 * v_groups * 4;
     o.vmn = off;   off += 64 * v_groups * 4;
     o.vcode = off; off += 64 * v_words * 4;
-    o.qp = off;    off += n_slots * kMaxG * 4;
+    o.qp = off;    off += n_slots * G * 4;
     o.total = off;
     return o;
 }
@@ -50,12 +54,15 @@ __device__ __forceinline__ int slot_tier(const int* off, int slot) {
 
 template <int D>
 __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
+    constexpr int kMaxG = valu_tile_rows(D);
     const lf_packed_layer& L = p.L;
     const lf_decode_args& A = p.A;
     const int item = blockIdx.x;
     const int h = blockIdx.y;
     const int lane = threadIdx.x;
-    const int g = p.g;
+    // rows row0 .. row0 + g - 1 of this kv head's p.g query rows (row = head * q_len + token)
+    const int row0 = kMaxG * static_cast<int>(blockIdx.z);
+    const int g = min(kMaxG, p.g - row0);
     const int* w4 = A.work + 4 * item;
     const int b = w4[0];
     const int pbeg = w4[1], pend = w4[2], kind = w4[3];
@@ -68,7 +75,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
     const int n_slots = off[3] + L.k_width[3];
     const int vgs = L.v_groups;
     const int vws = L.v_words;
-    const ValuLds lay = valu_lds(D, vgs, vws, n_slots);
+    const ValuLds lay = valu_lds(D, kMaxG, vgs, vws, n_slots);
     extern __shared__ __align__(16) unsigned char smem[];
     float* qT = reinterpret_cast<float*>(smem + lay.qT);        // [D][kMaxG]
     float* pb = reinterpret_cast<float*>(smem + lay.p);         // [64][kMaxG]
@@ -81,7 +88,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
     for (int idx = lane; idx < kMaxG * D; idx += 64) {
         const int i = idx / D, c = idx % D;
         float v = 0.f;
-        if (i < g) v = load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * g + i) * D + c, A.q_dtype);
+        if (i < g) v = load_as_f32(A.query, (static_cast<int64_t>(b) * A.n_q + h * p.g + row0 + i) * D + c, A.q_dtype);
         qT[c * kMaxG + i] = v * p.qscale;
     }
     __syncthreads();
@@ -252,7 +259,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
                 if (tt_lane >= tl && q_len > 1) {
 #pragma unroll
                     for (int i = 0; i < kMaxG; ++i)
-                        if (tt_lane - tl > i % q_len) score[i] = -__builtin_inff();
+                        if (tt_lane - tl > (row0 + i) % q_len) score[i] = -__builtin_inff();
                 }
             }
             float alpha[kMaxG];
@@ -284,7 +291,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
 
     // Partials: o per lane-channel, m uniform, l reduced across the wave.
     for (int i = 0; i < g; ++i) {
-        float* r = part_rec(p, item, h, i);
+        float* r = part_rec(p, item, h, row0 + i);
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc)
             if (lane + 64 * cc < D) r[lane + 64 * cc] = o[cc][i];
@@ -301,7 +308,8 @@ int launch_valu_d(const DecodeParams& p, size_t lds, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&decode_valu_kernel<D>);
     const int rc = allow_dynamic_lds(fn, lds);
     if (rc != LF_OK) return rc;
-    hipLaunchKernelGGL(decode_valu_kernel<D>, dim3(p.A.n_work, p.L.n_kv), dim3(64), lds, stream, p);
+    const int tiles = (p.g + valu_tile_rows(D) - 1) / valu_tile_rows(D);
+    hipLaunchKernelGGL(decode_valu_kernel<D>, dim3(p.A.n_work, p.L.n_kv, tiles), dim3(64), lds, stream, p);
     return LF_OK;
 }
 
@@ -310,8 +318,9 @@ int launch_valu_d(const DecodeParams& p, size_t lds, hipStream_t stream) {
 int launch_decode_valu(const DecodeParams& p, hipStream_t stream) {
     const int D = p.L.head_dim;
     const int n_slots = p.L.k_width[0] + p.L.k_width[1] + p.L.k_width[2] + p.L.k_width[3];
-    const size_t lds = static_cast<size_t>(valu_lds(D, p.L.v_groups, p.L.v_words, n_slots).total);
+    const size_t lds = static_cast<size_t>(valu_lds(D, valu_tile_rows(D), p.L.v_groups, p.L.v_words, n_slots).total);
     if (lds > 160 * 1024) return LF_E_UNSUPPORTED;
+    if ((p.g + valu_tile_rows(D) - 1) / valu_tile_rows(D) > 65535) return LF_E_SHAPE;  // grid z
     int rc;
     switch (D) {
         case 8: rc = launch_valu_d<8>(p, lds, stream); break;
@@ -321,6 +330,7 @@ int launch_decode_valu(const DecodeParams& p, hipStream_t stream) {
         case 128: rc = launch_valu_d<128>(p, lds, stream); break;
         case 256: rc = launch_valu_d<256>(p, lds, stream); break;
         case 512: rc = launch_valu_d<512>(p, lds, stream); break;
+        case 1024: rc = launch_valu_d<1024>(p, lds, stream); break;
         default: return LF_E_UNSUPPORTED;
     }
     if (rc != LF_OK) return rc;

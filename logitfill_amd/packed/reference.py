@@ -4,13 +4,15 @@ Drop-in for the reference's ``logitfill.packed.reference``
 (``src/logitfill/packed/reference.py``):
 
 * ``packed_attention(manager, layer_idx, query, key_new, value_new, scaling)``
-  -- one query token per sequence goes to the HIP split-K decode kernel over
-  the packed pages, the residual page and the new token
+  -- the new query token(s) of each sequence go to the HIP split-K decode
+  kernel over the packed pages, the residual page and the new tokens
   (``lf_decode_attention``); this replaces ``_kernel_attention`` and the CUDA
-  kernel it launches (``reference.py:59-109``).
-* Calls the reference sends to its dense path -- several query tokens
-  (``reference.py:62``), ``bit_v != 2`` -- run ``reference_attention`` on the
-  device: HIP dequantisation of the history, then float32 softmax attention
+  kernel it launches (``reference.py:59-109``).  Several query tokens (chunked
+  scoring, speculative decoding), which the reference sends to its dense path
+  (``reference.py:62``), stay on the kernel with the right-aligned causal mask
+  (``reference.py:18-27,48``).
+* Shapes no kernel serves -- ``bit_v != 2`` -- run ``reference_attention`` on
+  the device: HIP dequantisation of the history, then float32 softmax attention
   with the right-aligned causal mask (``reference.py:18-56``).
 
 Nothing here runs on the CPU: a missing extension or a CPU tensor raises.
@@ -305,15 +307,19 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     kernel = kernel_choice() if kernel is None else kernel
     P = layer.page_size
     hist_pages = tuple(h // P for h in layer.hist_lens)
-    res_pages = residual_pages(layer.tail_lens)
+    # q_len new tokens lengthen the residual (a chunk of 128 tokens more past a full page)
+    res_pages = residual_pages(layer.tail_lens) + (max(layer.tail_lens, default=0) + q_len - 1) // P * (
+        RESIDUAL_FIXED_PAGES + RESIDUAL_TAIL_PAGES)
+    # workgroups per (item, kv head): one per tile of query rows
+    tiles = -(-(manager.n_q // manager.n_kv * q_len) // MFMA_TILE_ROWS)
     if pages_per_split is None:
         # the split depends on the history, the residual cost, the environment's override and
         # whether the matrix-core kernel's dispatch order applies: chosen again when one changes
-        age = kernel != _native.KERNEL_VALU and q_len == 1
-        choice_key = (hist_pages, res_pages, os.environ.get("LOGITFILL_AMD_PAGES_PER_SPLIT"), age)
+        age = kernel != _native.KERNEL_VALU and tiles == 1
+        choice_key = (hist_pages, res_pages, os.environ.get("LOGITFILL_AMD_PAGES_PER_SPLIT"), age, tiles)
         cached = layer.__dict__.get("_lf_split_choice")
         if cached is None or cached[0] != choice_key:
-            size = choose_pages_per_split(list(hist_pages), layer.n_kv, res_pages, layer.device)
+            size = choose_pages_per_split(list(hist_pages), layer.n_kv * tiles, res_pages, layer.device)
             if age and choice_key[2] is None:
                 sizes = age_split(list(hist_pages), layer.n_kv, res_pages, size, _cu_count(layer.device))
                 size = size if sizes is None else tuple(sizes)
@@ -394,8 +400,14 @@ def _kernel_attention(manager, layer_idx: int, query: torch.Tensor, key_new: tor
     return out.view(B, n_q, q_len, D)
 
 
-# Query rows per kv head the decode kernels serve ((n_q / n_kv) * q_len).
-MAX_ROWS_PER_KV_HEAD = 16
+# Query rows per workgroup of the matrix-core decode kernel: rows beyond it ((n_q / n_kv) * q_len
+# per kv head) run as further row tiles, each a workgroup of its own over the same pages.
+MFMA_TILE_ROWS = 8
+
+
+def valu_tile_rows(head_dim: int) -> int:
+    """Query rows per workgroup of the general decode kernel (8 at head_dim 1024, else 16)."""
+    return 8 if head_dim > 512 else 16
 
 # Calls that took the dense dequantise-then-attend path because the decode kernels do not
 # serve their shape, by reason (read by tests and benchmarks; see ``packed_attention``).
@@ -406,21 +418,20 @@ _WARNED: set = set()
 def kernel_unsupported_reason(manager, q_len: int = 1) -> str | None:
     """Why ``lf_decode_attention`` would not serve this manager's shape, or None when it does
     (the checks of the C entry point: int2 Values as the reference kernel requires,
-    ``reference.py:62``; head_dim a power of two in 8..512; at most 16 query rows per kv head;
-    at most 64 Value groups; the general kernel's LDS within 160 KB)."""
+    ``reference.py:62``; head_dim a power of two in 8..1024, as the reference kernel takes,
+    ``kernel.cu:224-230``; at most 64 Value groups; the general kernel's LDS within 160 KB).
+    Any number of query rows per kv head is served: the kernels tile them across workgroups."""
     D = int(manager.head_dim)
     if manager.bit_v != 2:
         return f"bit_v={manager.bit_v} (the decode kernels take int2 Values)"
-    if D < 8 or D > 512 or D & (D - 1):
-        return f"head_dim={D} (the decode kernels take powers of two in 8..512)"
-    rows = manager.n_q // manager.n_kv * int(q_len)
-    if rows > MAX_ROWS_PER_KV_HEAD:
-        return f"{rows} query rows per kv head (at most {MAX_ROWS_PER_KV_HEAD})"
+    if D < 8 or D > 1024 or D & (D - 1):
+        return f"head_dim={D} (the decode kernels take powers of two in 8..1024)"
     vg = D // int(manager.v_group_size)
     if vg > 64:
         return f"{vg} Value groups per token (at most 64)"
     slots = max(sum(layer.widths) for layer in manager.layers) if manager.layers else D
-    lds = 4 * (16 * D + 16 * 64 + 2 * 64 * vg + 64 * -(-D // 16) + 16 * slots)
+    G = valu_tile_rows(D)
+    lds = 4 * (G * D + G * 64 + 2 * 64 * vg + 64 * -(-D // 16) + G * slots)
     if lds > 160 * 1024:
         return f"{lds} bytes of LDS for the general kernel (at most 160 KB)"
     return None

@@ -136,15 +136,15 @@ def test_decode_general_shapes_against_oracle(gpu, D, n_q, n_kv, page, vg):
 
 
 def test_unsupported_shapes_take_the_counted_dense_path(gpu):
-    """bit_v 4 and 24 query rows per kv head are outside the decode kernels (the reference
-    kernel also takes int2 Values only, reference.py:62): packed_attention runs the dense
-    dequantise-then-attend path on the device, counts the call, and matches the oracle; with
-    LOGITFILL_AMD_STRICT=1 it raises instead."""
+    """Values at 4 and 8 bits are outside the decode kernels (the reference kernel also takes
+    int2 Values only, reference.py:62): packed_attention runs the dense dequantise-then-attend
+    path on the device, counts the call, and matches the oracle; with LOGITFILL_AMD_STRICT=1 it
+    raises instead.  (Any GQA group stays on the kernels: tests/test_gpu_rows.py.)"""
     import os
 
     dref.DENSE_FALLBACKS.clear()
     D, n_kv = 64, 1
-    for n_q, bit_v in ((2, 4), (24, 2)):
+    for n_q, bit_v in ((2, 4), (24, 8)):
         levels = np.zeros((n_kv, D), dtype=np.int64)
         T = 2 * 64 + 5
         g = torch.Generator().manual_seed(n_q)
