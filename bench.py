@@ -41,7 +41,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-dense", action="store_true", help="skip the BF16 dense comparator")
     p.add_argument("--no-compress", action="store_true", help="skip the page-compress (config 3) timing")
-    p.add_argument("--cpu-seqs", type=int, default=1, help="sequences timed by the CPU baseline")
+    p.add_argument("--cpu-seqs", type=int, default=16,
+                   help="sequences timed by the CPU baseline (default: the whole c2 batch, about 20 s of CPU work)")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the other decode configs (c2 at target 3.0, c1, c4) reported beside the headline")
     p.add_argument("--no-step", action="store_true", help="skip the full decode-step timing (attention + commit)")
@@ -102,7 +103,10 @@ def algorithmic_bytes(widths, words, n_kv, n_q, D, H, R1, k_group=128, v_group=1
     return total, n_kv * H * payload_tok
 
 
-def build_state(cfg, layers, dev, capacity_pages=None):
+def build_state(cfg, layers, dev, capacity_pages=None, q_len=1):
+    """Manager with ``layers`` seeded layers of config ``cfg`` and each layer's decode inputs:
+    (query, key_new, value_new) of one new token ``[B, n_q, D]`` / ``[B, n_kv, D]``, or with
+    ``q_len`` > 1 new tokens ``[B, n_q, q_len, D]`` / ``[B, n_kv, q_len, D]``."""
     import torch
 
     from logitfill_amd import synth
@@ -125,7 +129,14 @@ def build_state(cfg, layers, dev, capacity_pages=None):
             rv = torch.stack([d.value[b, :, pages[b] * 128:pages[b] * 128 + 127] for b in range(B)])
             st.set_tail(rk, rv, resid)
             del rk, rv
-        inputs.append((d.query.contiguous(), d.key_new.contiguous(), d.value_new.contiguous()))
+        if q_len == 1:
+            inputs.append((d.query.contiguous(), d.key_new.contiguous(), d.value_new.contiguous()))
+        else:
+            g = torch.Generator(device=dev).manual_seed(9000 + layer)
+            q = (torch.randn(B, n_q, q_len, D, generator=g, device=dev) * D ** -0.5).to(torch.bfloat16)
+            kn = torch.randn(B, n_kv, q_len, D, generator=g, device=dev).to(torch.bfloat16)
+            vn = torch.randn(B, n_kv, q_len, D, generator=g, device=dev).to(torch.bfloat16)
+            inputs.append((q, kn, vn))
         del d
         torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -180,19 +191,20 @@ def time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split):
     return ms / steps, wall / steps * 1e3
 
 
-def decode_point(cfg, layers, steps, warmup, kernel, pages_per_split, dev):
-    """Build ``layers`` layers of a config, time the decode; returns (us per layer-step, bytes per
-    layer-step, payload bytes per layer-step, wall ms per step) and frees the state."""
+def decode_point(cfg, layers, steps, warmup, kernel, pages_per_split, dev, q_len=1):
+    """Build ``layers`` layers of a config, time the decode (``q_len`` new tokens per sequence);
+    returns (us per layer-step, bytes per layer-step, payload bytes per layer-step, wall ms per
+    step) and frees the state."""
     import torch
 
-    mgr, inputs = build_state(cfg, layers, dev)
+    mgr, inputs = build_state(cfg, layers, dev, q_len=q_len)
     ms_step, wall_ms = time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split)
     n_q, n_kv, D = cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
     pages, resid, _ = seq_lengths(cfg)
     tot, pay = 0, 0
     for st in mgr.layers:
         for p, r in zip(pages, resid):
-            t, pl = algorithmic_bytes(st.widths, st.words, n_kv, n_q, D, p * 128, r + 1)
+            t, pl = algorithmic_bytes(st.widths, st.words, n_kv, n_q * q_len, D, p * 128, r + q_len)
             tot += t
             pay += pl
     del mgr, inputs
@@ -604,16 +616,19 @@ def main():
         legs["compress"] = round(time.perf_counter() - t0, 2)
     if not args.no_extra and args.config == "c2" and args.layers is None:
         extra = {}
-        for name, n_layers in (("c2_k4", None), ("c1", None), ("c4", 8)):
-            c = dict(synth.CONFIGS[name])
+        for name, n_layers, q_len in (("c2_k4", None, 1), ("c1", None, 1), ("c4", 8, 1), ("c2_q4", None, 4)):
+            c = dict(synth.CONFIGS[name.replace("_q4", "")])
             nl = n_layers or c["layers"]
             print(f"[bench] {name} ({nl} layers) ...", file=sys.stderr, flush=True)
             t0 = time.perf_counter()
-            us_x, bytes_x, pay_x, _ = decode_point(c, nl, 10, 2, kernel, None, dev)
+            us_x, bytes_x, pay_x, _ = decode_point(c, nl, 10, 2, kernel, None, dev, q_len=q_len)
             legs[name] = round(time.perf_counter() - t0, 2)
+            tokens = (f", {q_len} new query tokens per sequence (speculative decoding: the right-aligned causal "
+                      f"mask on the new tokens, {c['n_q'] // c['n_kv'] * q_len} query rows per kv head)"
+                      if q_len > 1 else "")
             extra[name] = {"workload": f"{c['layers']}-layer model shape timed on {nl} distinct layers, batch "
                                        f"{c['batch']}, {c['n_q']}q/{c['n_kv']}kv heads, {context_text(c)}, "
-                                       f"target_bit {c['target_bit']}",
+                                       f"target_bit {c['target_bit']}{tokens}",
                            "us_per_layer_step": round(us_x, 2), "bytes_per_layer_step": int(bytes_x),
                            "hbm_gbs": round(bytes_x / us_x / 1e3, 1),
                            "hbm_frac": round(bytes_x / us_x / 1e3 / HBM_PEAK_GBS, 4),
@@ -641,7 +656,7 @@ def main():
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         t0 = time.perf_counter()
-        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seqs)
+        result["cpu_baseline"] = cpu_baseline(cfg, max(1, min(args.cpu_seqs, cfg["batch"])))
         legs["cpu_baseline"] = round(time.perf_counter() - t0, 2)
         if not args.no_compress:
             t0 = time.perf_counter()
