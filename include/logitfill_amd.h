@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 6
+#define LF_ABI_VERSION 7
 
 /* Element types of query / residual / output tensors. */
 enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
@@ -66,6 +66,20 @@ enum lf_status {
  * (src/logitfill/packed/layout.py:49-68) is passed as ``tier_index[t]``
  * int32 [n_kv][k_width[t]] (ascending channel ids, zero padded) and
  * ``tier_count[t]`` int32 [n_kv].  Pointers of empty tiers may be NULL.
+ *
+ * Beside the reference arrays, a layer whose Key group is the page (k_group == page_size)
+ * may carry a page-major copy of the integer tiers' Key scales and mins, the form the
+ * matrix-core decode kernel reads (one contiguous block per page instead of one fp16 pair
+ * per slot and page, each in a cache line of its own):
+ *
+ *   k_sm_page   fp16  [batch][n_kv][cap_kgroups][16 * nb]
+ *
+ * nb = 4 * (2 * ceil(k_words[0] / 4) + ceil(k_words[1] / 4) + ceil(ceil(k_words[2] / 2) / 4))
+ * blocks of 8 slots, tier by tier; block i holds 8 scales then 8 mins.  The slot order inside a
+ * tier's blocks is the decode kernel's code-unpack order (logitfill_amd/csrc/lf_common.hpp,
+ * sm_slot / sm_place); positions that are no channel of the head hold scale 1.0 and min 0.0.
+ * Every packer writes it when the pointer is not NULL (the values are bit-identical to the
+ * reference arrays'); decode takes the matrix-core kernel only when it is present.
  */
 typedef struct lf_packed_layer {
     int32_t*  k_code[3];
@@ -84,6 +98,7 @@ typedef struct lf_packed_layer {
     int32_t k_width[4];
     int32_t k_words[3];
     int32_t v_words, v_groups;
+    uint16_t* k_sm_page;              /* page-major Key scale/min copy, or NULL (see above) */
 } lf_packed_layer;
 
 /* ABI version (LF_ABI_VERSION) and a static build string. */

@@ -57,6 +57,7 @@ class PackedLayer(ctypes.Structure):
         ("k_words", c_int32 * 3),
         ("v_words", c_int32),
         ("v_groups", c_int32),
+        ("k_sm_page", c_void_p),
     ]
 
 
@@ -114,7 +115,7 @@ _SIGNATURES = {
     "lf_noalloc_scratch_bytes": (c_int64, []),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 _LIB = None
 
 

@@ -9,7 +9,9 @@
 //
 // Work: one workgroup of 4 waves per (split item, kv head, tile of 8 query rows); wave w computes
 // tokens 32w..32w+31 (two 16-token tiles) of every page of the item.  Pages arrive by LDS-DMA
-// (global_load_lds) into a ring of two page slots, one page ahead of the page being computed.
+// (global_load_lds, 16-byte chunks: the Key codes, the Value scales / mins / codes, the fp16-tier
+// rows and the page's block of the page-major Key scale/min copy k_sm_page) into a ring of two
+// page slots, one page ahead of the page being computed.
 // Per page: a barrier (the page landed, the previous page is computed), the page's
 // "preparation" (the per-page operands below) into the one prepared buffer by all waves, a
 // second barrier, then the compute.  Partials (m, l, o) of each item go to the workspace;
@@ -54,7 +56,6 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kD = 128;
 constexpr int kPage = 128;
 constexpr int kMaxDma = 8;    // 16-byte DMA instructions per wave per page (<= 2048 chunks)
-constexpr int kMaxKsDma = 4;  // 4-byte Key scale/min DMA instructions per wave per page
 constexpr int kMaxKSteps = 16; // K-steps of a page: at most 4 per tier (128 channels)
 constexpr float kLazyRescale = 8.f;  // log2-domain headroom before the running max moves
 constexpr int kRawbVs = 0;    // rest buffer: Value scale [128] fp16
@@ -73,16 +74,15 @@ struct MfmaLayout {
     int kst[4];          // K-steps per tier (int2: even; K-step s takes half s&1 of 4 words)
     int kfirst[4];       // first K-step of each tier
     int nb;              // padded blocks (4 per K-step)
-    int nb_int;          // padded blocks of the integer tiers
+    int nb_int;          // padded blocks of the integer tiers (the page-major scale/min block's)
     int w16p;            // fp16-tier row stride in the prepared buffer (multiple of 8)
     int seg_end[3];      // cumulative 16-byte chunks of the Key-code rows K0, K1, K2 (region A)
     int n_chunks;        // region A + region B chunks
     int ja, jb;          // 64-chunk DMA blocks of the Key codes (chunks [0, seg_end[2])) and of the rest
-    int n_kslots;        // 2 * nb_int * 8: Key scale slots, then Key min slots
     int rawa_bytes;      // Key-code buffer: K0, K1, K2 rows of the page, padded to whole DMA blocks
-    int rawb_ks;         // rest buffer (v scale at 0, v min at 256, [128][8] u32 Value codes at 512,
-                         // fp16-tier rows at 4608, padded to whole DMA blocks):
-                         // [n_kslots] u32 Key scale / min page pairs
+    int rawb_sm;         // rest buffer (v scale at 0, v min at 256, [128][8] u32 Value codes at 512,
+                         // fp16-tier rows at 4608, padded to whole DMA blocks): the page's
+                         // k_sm_page block [nb_int][8 scales, 8 mins] fp16 at this offset
     int rawb_bytes;
     int ck_v16;          // prepared: [128][w16p] fp16 Key fp16 tier, zero padded (after Qs), one spare dword
     int ck_bytes;
@@ -124,19 +124,16 @@ __device__ __forceinline__ T sel3(const T (&a)[3], int t) {
     return t == 0 ? a[0] : t == 1 ? a[1] : a[2];
 }
 
-// LDS-DMA: each lane's 16 (4) bytes at ``g`` land at lds + 16 (4) * lane.  Issued through
-// asm so the compiler does not order every later LDS read behind it (it cannot tell the
-// buffers apart and would wait for all DMA in flight); the waits are explicit instead.  The
-// compiler writes M0 just before the asm; an LDS-DMA instruction needs one wait state after
-// an SALU write of M0, hence the s_nop.
+// LDS-DMA: each lane's 16 bytes at ``g`` land at lds + 16 * lane.  Issued through asm so the
+// compiler does not order every later LDS read behind it (it cannot tell the buffers apart and
+// would wait for all DMA in flight); the waits are explicit instead.  The compiler writes M0 just
+// before the asm; an LDS-DMA instruction needs one wait state after an SALU write of M0, hence
+// the s_nop.
 __device__ __forceinline__ uint32_t lds_addr(unsigned char* p) {
     return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)p)));
 }
 __device__ __forceinline__ void dma16(const unsigned char* g, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
-}
-__device__ __forceinline__ void dma4(const unsigned char* g, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
 
 // Bit patterns of the exponent-field code unpack, held in VGPRs: with register operands the
@@ -233,50 +230,47 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a0, uint32_t a1, uint32
 // spills and reloads the tuple whole inside the page loop.
 struct LoopY {
     int kst0, kst1, kst2, kst3, kf1, kf2, kf3, nb, nb_int, w16p;
-    int seg0, seg1, ja, rawa_bytes, rawb_ks, slot_bytes, ck_v16, n_kslots;
+    int seg0, seg1, ja, rawa_bytes, rawb_sm, slot_bytes, ck_v16;
 };
 
 __device__ __forceinline__ LoopY loop_y(const MfmaLayout& y) {
     LoopY z{y.kst[0], y.kst[1], y.kst[2], y.kst[3], y.kfirst[1], y.kfirst[2], y.kfirst[3], y.nb, y.nb_int, y.w16p,
-            y.seg_end[0], y.seg_end[1], y.ja, y.rawa_bytes, y.rawb_ks, y.slot_bytes, y.ck_v16, y.n_kslots};
+            y.seg_end[0], y.seg_end[1], y.ja, y.rawa_bytes, y.rawb_sm, y.slot_bytes, y.ck_v16};
     asm volatile("" : "+s"(z.kst0), "+s"(z.kst1), "+s"(z.kst2), "+s"(z.kst3), "+s"(z.kf1), "+s"(z.kf2), "+s"(z.kf3),
                       "+s"(z.nb), "+s"(z.nb_int), "+s"(z.w16p));
-    asm volatile("" : "+s"(z.seg0), "+s"(z.seg1), "+s"(z.ja), "+s"(z.rawa_bytes), "+s"(z.rawb_ks),
-                      "+s"(z.slot_bytes), "+s"(z.ck_v16), "+s"(z.n_kslots));
+    asm volatile("" : "+s"(z.seg0), "+s"(z.seg1), "+s"(z.ja), "+s"(z.rawa_bytes), "+s"(z.rawb_sm),
+                      "+s"(z.slot_bytes), "+s"(z.ck_v16));
     return z;
 }
 
-// Operands of one Qs block: q of (block, head) and the block's Key scale / min pair words.
+// Operands of one Qs block: q of (block, head) and the block's 8 Key scales and 8 Key mins
+// (fp16, from the page's k_sm_page block).
 struct QsRegs {
     float4 q0, q1;
-    uint4 s0, s1, m0, m1;
+    uint4 s, m;
 };
 
-__device__ __forceinline__ void qs_fetch(const float* qrow, const uint32_t* ksc, const uint32_t* kmn, QsRegs& r) {
+__device__ __forceinline__ void qs_fetch(const float* qrow, const unsigned char* smb, QsRegs& r) {
     r.q0 = *reinterpret_cast<const float4*>(qrow);
     r.q1 = *reinterpret_cast<const float4*>(qrow + 4);
-    r.s0 = *reinterpret_cast<const uint4*>(ksc);
-    r.s1 = *reinterpret_cast<const uint4*>(ksc + 4);
-    r.m0 = *reinterpret_cast<const uint4*>(kmn);
-    r.m1 = *reinterpret_cast<const uint4*>(kmn + 4);
+    r.s = *reinterpret_cast<const uint4*>(smb);
+    r.m = *reinterpret_cast<const uint4*>(smb + 16);
 }
 
 // Qs of an integer-tier block for one head -- hi into ``qs_hi``, lo (the fp16 residual) into
-// ``qs_lo`` -- and the block's share of the bias sum_slot q * (min - beta * scale); page Odd
-// takes the high halves of the pair words.  Padding slots have q == 0; their scale/min words
-// hold a real slot's (finite) values.  Written so the compiler uses mixed-precision FMAs on
-// the fp16 halves directly.
-template <bool Odd>
+// ``qs_lo`` -- and the block's share of the bias sum_slot q * (min - beta * scale).  Padding
+// slots have q == 0 and scale 1.0, min 0.0.  Written so the compiler uses mixed-precision FMAs
+// on the fp16 halves directly.
 __device__ __forceinline__ float qs_math(const QsRegs& r, half8* qs_hi, half8* qs_lo, float beta_lo, float beta_hi) {
     const float qv[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    const uint32_t sw[8] = {r.s0.x, r.s0.y, r.s0.z, r.s0.w, r.s1.x, r.s1.y, r.s1.z, r.s1.w};
-    const uint32_t mw[8] = {r.m0.x, r.m0.y, r.m0.z, r.m0.w, r.m1.x, r.m1.y, r.m1.z, r.m1.w};
+    const uint32_t sw[4] = {r.s.x, r.s.y, r.s.z, r.s.w};
+    const uint32_t mw[4] = {r.m.x, r.m.y, r.m.z, r.m.w};
     half8 hi, lo;
     float bsum = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const _Float16 sc = __builtin_bit_cast(half2v, sw[k])[Odd ? 1 : 0];
-        const _Float16 mn = __builtin_bit_cast(half2v, mw[k])[Odd ? 1 : 0];
+        const _Float16 sc = __builtin_bit_cast(half2v, sw[k >> 1])[k & 1];
+        const _Float16 mn = __builtin_bit_cast(half2v, mw[k >> 1])[k & 1];
         const _Float16 hk = static_cast<_Float16>(fmaf(qv[k], static_cast<float>(sc), 0.f));
         hi[k] = hk;
         lo[k] = static_cast<_Float16>(fmaf(qv[k], static_cast<float>(sc), -static_cast<float>(hk)));
@@ -321,20 +315,15 @@ __device__ __forceinline__ float rows_max(float x) {
 }
 
 // Per-lane DMA state.  A page is fetched as 16-byte chunks in two regions -- region A: the
-// Key-code rows K0, K1, K2; region B: Value scale, Value min, Value codes, fp16-tier rows --
-// plus one dword per Key scale/min slot (the fp16 pair of pages (p & ~1, p | 1)).  Block j
-// (64 chunks) of region A lands in the Key-code buffer at 1024 j, block j of region B in the
-// rest buffer at 1024 j; slot dwords follow region B at rawb_ks.  Wave w issues blocks
-// w, w + 4, ...  Every lane of an issued instruction loads: lanes past a region's last chunk
-// re-read that chunk into the block padding of their buffer, lanes past the last slot re-read
-// a real slot into the slot area's padding.
+// Key-code rows K0, K1, K2; region B: Value scale, Value min, Value codes, fp16-tier rows and the
+// page's k_sm_page block.  Block j (64 chunks) of region A lands in the Key-code buffer at 1024 j,
+// block j of region B in the rest buffer at 1024 j.  Wave w issues blocks w, w + 4, ...  Every
+// lane of an issued instruction loads: lanes past a region's last chunk re-read that chunk into
+// the block padding of their buffer.
 struct DmaSrc {
     const unsigned char* chunk[kMaxDma];
     uint32_t chunk_stride[kMaxDma];  // bytes per page of the chunk's segment
-    const unsigned char* ks[kMaxKsDma];
     int n_chunk;                // 16-byte DMA instructions this wave issues per page
-    int n_ks;                   // 4-byte slot DMA instructions this wave issues per page
-    int per_page;               // DMA instructions this wave issues per page
 };
 
 __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout& y, int b, int h, int pbeg,
@@ -342,6 +331,7 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
     const int64_t row0 = tok_row(L, b, h, static_cast<int64_t>(pbeg) * kPage);
     const int na = y.seg_end[2];             // region A chunks
     const int nb_chunks = y.n_chunks - na;   // region B chunks
+    const int c_f16 = 288, c_sm = 288 + kPage * L.k_width[3] * 2 / 16;  // region B segment starts
     s.n_chunk = 0;
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
@@ -362,7 +352,7 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
                 stride = kPage * L.k_words[2] * 4;
             }
         } else if (j < y.ja + y.jb) {
-            // region B: v scale (16 chunks), v min (16), v codes (256), fp16-tier rows
+            // region B: v scale (16 chunks), v min (16), v codes (256), fp16-tier rows, the k_sm_page block
             const int c = min(64 * (j - y.ja) + lane, nb_chunks - 1);
             if (c < 16) {
                 src = reinterpret_cast<const unsigned char*>(L.v_scale + row0) + 16 * c;
@@ -370,76 +360,37 @@ __device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout&
             } else if (c < 32) {
                 src = reinterpret_cast<const unsigned char*>(L.v_min + row0) + 16 * (c - 16);
                 stride = kPage * 2;
-            } else if (c < 32 + 256) {
+            } else if (c < c_f16) {
                 src = reinterpret_cast<const unsigned char*>(L.v_code + row0 * 8) + 16 * (c - 32);
                 stride = kPage * 32;
-            } else {
-                src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]) + 16 * (c - 288);
+            } else if (c < c_sm) {
+                src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]) + 16 * (c - c_f16);
                 stride = kPage * L.k_width[3] * 2;
+            } else {
+                src = reinterpret_cast<const unsigned char*>(L.k_sm_page + sm_page_idx(L, b, h, pbeg)) + 16 * (c - c_sm);
+                stride = 32 * y.nb_int;
             }
         }
         s.chunk[i] = src;
         s.chunk_stride[i] = stride;
     }
-    // Key scale/min slots.  Padding slots, and lanes past the last slot, read slot 0 of the
-    // first integer tier (the padding slots' q is zero).
-    s.n_ks = 0;
-    const int t0 = L.k_width[0] ? 0 : L.k_width[1] ? 1 : 2;
-    const unsigned char* dummy = reinterpret_cast<const unsigned char*>(
-        sel3(L.k_scale, t0) + kgrp_idx(L, b, h, sel4(L.k_width, t0), 0, pbeg & ~1));
-#pragma unroll
-    for (int i = 0; i < kMaxKsDma; ++i) {
-        const int e0 = (kWaves * i + wave) * 64;
-        if (e0 < y.n_kslots) s.n_ks = i + 1;
-        const int e = e0 + lane;
-        const unsigned char* src = dummy;
-        if (e < y.n_kslots) {
-            const bool is_min = e >= y.n_kslots / 2;
-            const int slot = is_min ? e - y.n_kslots / 2 : e;
-            const int gb = slot >> 3, pos = slot & 7;
-            const int tier = gb >= 4 * y.kfirst[2] ? 2 : gb >= 4 * y.kfirst[1] ? 1 : 0;
-            const int lb = gb - 4 * sel4(y.kfirst, tier);
-            if (block_live(L, tier, lb)) {
-                const int j = block_slot(tier, lb, pos);
-                const int width = sel4(L.k_width, tier);
-                if (j < width) {
-                    const uint16_t* base = is_min ? sel3(L.k_min, tier) : sel3(L.k_scale, tier);
-                    src = reinterpret_cast<const unsigned char*>(base + kgrp_idx(L, b, h, width, j, pbeg & ~1));
-                }
-            }
-        }
-        s.ks[i] = src;
-    }
-    s.per_page = s.n_chunk + s.n_ks;
 }
 
 // Issue the DMA of page ``page`` into the page slot at LDS address ``slot`` (32-bit): block j
 // of region A lands at 1024 j, block j of region B at rawa_bytes + 1024 j = 1024 (ja + j), so
-// this wave's i-th 16-byte instruction (block wave + 4 i overall) lands at 1024 (wave + 4 i).
-// The Key scale/min slot dwords hold a page pair (p & ~1, p | 1): they are fetched once per
-// pair (``ks``: the item's first page and every even page) into the slot-dword area at LDS
-// address ``ks_dst``, which the pages of the pair share.  The sources advance one page (the
-// slot sources one pair per fetch).
-__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t slot, uint32_t ks_dst, bool ks, const LoopY& z, int wave) {
-    // The counts pass through an empty asm so the compiler keeps one compare per instruction
+// this wave's i-th instruction (block wave + 4 i overall) lands at 1024 (wave + 4 i).  The
+// sources advance one page.
+__device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t slot, int wave) {
+    // The count passes through an empty asm so the compiler keeps one compare per instruction
     // instead of hoisting per-instruction conditions out of the page loop.
-    int n_chunk = __builtin_amdgcn_readfirstlane(s.n_chunk), n_ks = __builtin_amdgcn_readfirstlane(s.n_ks);
-    asm volatile("" : "+s"(n_chunk), "+s"(n_ks));
+    int n_chunk = __builtin_amdgcn_readfirstlane(s.n_chunk);
+    asm volatile("" : "+s"(n_chunk));
     const uint32_t d16 = slot + 1024 * wave;
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
         if (i < n_chunk) {
             dma16(s.chunk[i], d16 + 4096 * i);
             s.chunk[i] += s.chunk_stride[i];
-        }
-    }
-    if (!ks) return;
-    const uint32_t d4 = ks_dst + 256 * wave;
-#pragma unroll
-    for (int i = 0; i < kMaxKsDma; ++i) {
-        if (i < n_ks) {
-            dma4(s.ks[i], d4 + kWaves * 256 * i);
-            s.ks[i] += 4;
         }
     }
 }
@@ -487,8 +438,8 @@ __device__ __forceinline__ F16Map f16_map(const LoopY& z, int w16, int tid) {
 __device__ __forceinline__ float beta_lo_of(int tier) { return tier == 0 ? 16.f : tier == 1 ? 256.f : 1024.f; }
 __device__ __forceinline__ float beta_hi_of(int tier) { return tier == 0 ? 4.f : tier == 1 ? 16.f : 1024.f; }
 
-__device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, const unsigned char* raw, const unsigned char* ksb,
-                                          const float* qperm, int g, int tid, int wave, PrepRegs& r) {
+__device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, const unsigned char* raw,
+                                          const float* qperm, int tid, int wave, PrepRegs& r) {
     // read k of thread (tg, w) takes token 4 tg + (k + tg) % 4: the 32 lanes of a half wave then
     // hit 32 different banks
     const int tg = tid >> 3, w = tid & 7;
@@ -509,24 +460,21 @@ __device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, cons
     }
     const int lane = tid & 63, n = lane & 7, j = lane >> 3;
     const int nbw = (z.nb_int + 3) >> 2, gb = min(wave * nbw + j, z.nb_int - 1);
-    const uint32_t* ksc = reinterpret_cast<const uint32_t*>(ksb);
-    qs_fetch(qperm + (gb * 8 + n) * 8, ksc + gb * 8, ksc + z.n_kslots / 2 + gb * 8, r.qs);
+    qs_fetch(qperm + (gb * 8 + n) * 8, raw + z.rawb_sm + 32 * gb, r.qs);
 }
 
 // Integer-tier Qs and bias of head n for block gb from fetched operands.
-__device__ __forceinline__ float qs_block(const LoopY& z, const QsRegs& r, half8* qs, int page, int gb, int n) {
+__device__ __forceinline__ float qs_block(const LoopY& z, const QsRegs& r, half8* qs, int gb, int n) {
     const int tier = gb >= 4 * z.kf2 ? 2 : gb >= 4 * z.kf1 ? 1 : 0;
     half8* hi = qs + gb * 16 + n;
     half8* lo = qs + gb * 16 + 8 + n;
-    return (page & 1) ? qs_math<true>(r, hi, lo, beta_lo_of(tier), beta_hi_of(tier))
-                      : qs_math<false>(r, hi, lo, beta_lo_of(tier), beta_hi_of(tier));
+    return qs_math(r, hi, lo, beta_lo_of(tier), beta_hi_of(tier));
 }
 
-// Finish page ``page``: fetched registers ``r`` (and, for what they do not hold, rest buffer
-// ``raw`` and slot dwords ``ksb``) into prepared buffer ``ck`` (all threads).
+// Finish the page: fetched registers ``r`` (and, for what they do not hold, the page's rest
+// buffer ``raw``) into prepared buffer ``ck`` (all threads).
 __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, const PrepRegs& r, const unsigned char* raw,
-                                           const unsigned char* ksb, unsigned char* ck, const float* qperm, int page,
-                                           int g, int w16, int tid, int wave) {
+                                           unsigned char* ck, const float* qperm, int g, int w16, int tid, int wave) {
     const int lane = tid & 63;
     {
         // Value codes: dwords (group tg, word w, tokens 0..3) -> byte columns.  The reads came
@@ -569,16 +517,15 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
     const int nbw = (z.nb_int + 3) >> 2;
     half8* qs = reinterpret_cast<half8*>(ck + kCkQs);
     const int gb_own = wave * nbw + j;
-    float bsum = qs_block(z, r.qs, qs, page, min(gb_own, z.nb_int - 1), n);
+    float bsum = qs_block(z, r.qs, qs, min(gb_own, z.nb_int - 1), n);
     if (!(n < g && j < nbw && gb_own < z.nb_int)) bsum = 0.f;
     if (nbw > 8) {
-        const uint32_t* ksc = reinterpret_cast<const uint32_t*>(ksb);
         for (int jj = j + 8; jj < nbw; jj += 8) {
             const int gb2 = wave * nbw + jj;
             if (n < g && gb2 < z.nb_int) {
                 QsRegs q2;
-                qs_fetch(qperm + (gb2 * 8 + n) * 8, ksc + gb2 * 8, ksc + z.n_kslots / 2 + gb2 * 8, q2);
-                bsum += qs_block(z, q2, qs, page, gb2, n);
+                qs_fetch(qperm + (gb2 * 8 + n) * 8, raw + z.rawb_sm + 32 * gb2, q2);
+                bsum += qs_block(z, q2, qs, gb2, n);
             }
         }
     }
@@ -1017,8 +964,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         unsigned char* raw0 = smem + y.off_raw;
         unsigned char* ck = smem + y.off_ck;
         const uint32_t raw_lds = lds_addr(smem) + y.off_raw;  // LDS address of page slot 0
-        // slot dwords of pair q / 2 live in the slot-dword area of page slot (q / 2) % 2
-        const int ks_off = z.rawa_bytes + z.rawb_ks;
 
         // ---- q permuted into slot order ----
         // K-step i of the layout holds blocks 4i .. 4i+3.  Thread tid owns block gb = tid / 4
@@ -1033,7 +978,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         // barrier does.
         DmaSrc ds;
         dma_setup(ds, L, y, b, h, pbeg, wave, lane);
-        dma_page(ds, raw_lds, raw_lds + ((pbeg >> 1) & 1) * z.slot_bytes + ks_off, true, z, wave);
+        dma_page(ds, raw_lds, wave);
         // q [8][128] of heads h g .. h g + 7: thread tid takes channels 4 (tid % 32) + 0..3 of
         // head tid / 32 (0 for heads >= g)
         const int qn = tid >> 5, qc0 = 4 * (tid & 31);
@@ -1104,15 +1049,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             // The preparation reads go out first; page + 1's DMA is issued while they are in
             // flight (a DMA instruction can wait for the address unit, shared by the CU's waves).
             const unsigned char* raw = raw0 + (rel & 1) * z.slot_bytes;
-            const unsigned char* ksb = raw0 + ((page >> 1) & 1) * z.slot_bytes + ks_off;
             PrepRegs pr;
-            prep_load(z, fm, raw + z.rawa_bytes, ksb, qperm, g, tid, wave, pr);
-            if (page + 1 < pend) {
-                const int q = page + 1;
-                dma_page(ds, raw_lds + ((rel + 1) & 1) * z.slot_bytes, raw_lds + ((q >> 1) & 1) * z.slot_bytes + ks_off,
-                         (q & 1) == 0, z, wave);
-            }
-            prep_store(z, fm, pr, raw + z.rawa_bytes, ksb, ck, qperm, page, g, w16, tid, wave);
+            prep_load(z, fm, raw + z.rawa_bytes, qperm, tid, wave, pr);
+            if (page + 1 < pend) dma_page(ds, raw_lds + ((rel + 1) & 1) * z.slot_bytes, wave);
+            prep_store(z, fm, pr, raw + z.rawa_bytes, ck, qperm, g, w16, tid, wave);
             lds_barrier();  // page prepared
             __builtin_amdgcn_s_setprio(0);
             // ---- compute page ``page`` from the prepared buffer and its Key codes ----
@@ -1502,11 +1442,11 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
     if (L.head_dim != kD || L.page_size != kPage || L.k_group != kPage || L.bit_v != 2 || L.v_group != kD)
         return false;
     if (g < 1) return false;
-    if (L.cap_kgroups % 2 != 0) return false;  // Key scale/min are fetched as page pairs
     if (L.k_width[0] + L.k_width[1] + L.k_width[2] == 0) return false;
+    // the Key scales and mins come from the page-major copy, 16-byte chunks of it
+    if (L.k_sm_page == nullptr || !aligned(L.k_sm_page, 16)) return false;
     for (int t = 0; t < 3; ++t)
-        if (L.k_width[t] && (!aligned(L.k_code[t], 16) || !aligned(L.k_scale[t], 4) || !aligned(L.k_min[t], 4)))
-            return false;
+        if (L.k_width[t] && !aligned(L.k_code[t], 16)) return false;
     if (L.k_width[3] && !aligned(L.k_value16, 16)) return false;
     if (!aligned(L.v_code, 4) || !aligned(L.v_scale, 16) || !aligned(L.v_min, 16)) return false;
     y.kst[0] = 2 * ((L.k_words[0] + 3) / 4);
@@ -1527,19 +1467,19 @@ bool plan_layout(const lf_packed_layer& L, int g, MfmaLayout& y) {
         seg += kPage * L.k_words[t] * 4 / 16;
         y.seg_end[t] = seg;
     }
-    // region B (DMA order): v scale, v min, v codes (256 chunks), fp16-tier rows
-    y.n_chunks = y.seg_end[2] + 16 + 16 + 256 + kPage * L.k_width[3] * 2 / 16;
+    // region B (DMA order): v scale, v min, v codes (256 chunks), fp16-tier rows, the page's
+    // k_sm_page block (nb_int x 32 bytes; sm_page in lf_common.hpp gives the same block count)
+    if (sm_page(L.k_words).nb != y.nb_int) return false;
+    y.n_chunks = y.seg_end[2] + 16 + 16 + 256 + kPage * L.k_width[3] * 2 / 16 + 2 * y.nb_int;
     y.ja = (y.seg_end[2] + 63) / 64;
     y.jb = (y.n_chunks - y.seg_end[2] + 63) / 64;
     if (y.ja + y.jb > kMaxDma * kWaves) return false;
-    y.n_kslots = 2 * y.nb_int * 8;
-    if (y.n_kslots > kMaxKsDma * kWaves * 64) return false;
     // Key-code buffer: the K0, K1, K2 rows; rest buffer: v scale, v min, Value codes, fp16 tier,
-    // then the Key scale/min slots.  Every lane of a DMA instruction writes, so both regions are
-    // padded to whole 64-chunk blocks (1024 bytes) and the slot area to whole 64-slot blocks.
+    // the scale/min block.  Every lane of a DMA instruction writes, so both regions are padded to
+    // whole 64-chunk blocks (1024 bytes).
     y.rawa_bytes = 1024 * y.ja;
-    y.rawb_ks = 1024 * y.jb;
-    y.rawb_bytes = y.rawb_ks + ((y.n_kslots + 63) / 64) * 256;
+    y.rawb_sm = kRawbF16 + kPage * L.k_width[3] * 2;
+    y.rawb_bytes = 1024 * y.jb;
     // prepared buffer: fixed-offset parts, Qs [nb][16][8] fp16 at kCkQs, fp16-tier rows after it
     y.ck_v16 = kCkQs + y.nb * 16 * 16;
     y.ck_bytes = round_up(y.ck_v16 + kPage * y.w16p * 2 + 4, 16);  // + the spare dword of the repack

@@ -171,8 +171,16 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
             }
             if (half == 0) {
                 const int64_t o = kgrp_idx(L, b, h, L.k_width[t], j, grp0 + g);
-                L.k_scale[t][o] = f32_to_f16(s);
-                L.k_min[t][o] = f32_to_f16(lo);
+                const uint16_t hs = f32_to_f16(s), hl = f32_to_f16(lo);
+                L.k_scale[t][o] = hs;
+                L.k_min[t][o] = hl;
+                if (L.k_sm_page != nullptr && ngroups == 1) {  // the page-major copy (one Key group a page)
+                    int lb, bp;
+                    sm_place(t, j, lb, bp);
+                    uint16_t* blk = L.k_sm_page + sm_page_idx(L, b, h, page) + 16 * (sm_page(L.k_words).blk0[t] + lb);
+                    blk[bp] = hs;
+                    blk[8 + bp] = hl;
+                }
             }
         }
     }
@@ -186,6 +194,20 @@ __global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackJobArgs a)
             const int64_t o = kgrp_idx(L, b, h, w, j, grp0 + g);
             L.k_scale[t][o] = 0x3C00u;
             L.k_min[t][o] = 0;
+        }
+    }
+    // The page-major copy's positions of no channel of this head: scale 1.0, min 0.0.
+    if (L.k_sm_page != nullptr && ngroups == 1) {
+        const SmPage sp = sm_page(L.k_words);
+        for (int p = threadIdx.x; p < 8 * sp.nb; p += kPackThreads) {
+            const int gb = p >> 3, pos = p & 7;
+            const int t = gb >= sp.blk0[2] ? 2 : gb >= sp.blk0[1] ? 1 : 0;
+            const int cnt = L.k_width[t] ? L.tier_count[t][h] : 0;
+            if (sm_slot(t, gb - sp.blk0[t], pos) >= cnt) {
+                uint16_t* blk = L.k_sm_page + sm_page_idx(L, b, h, page) + 16 * gb;
+                blk[pos] = 0x3C00u;
+                blk[8 + pos] = 0;
+            }
         }
     }
     __syncthreads();
@@ -538,17 +560,21 @@ __device__ __host__ inline int code_ld(const lf_packed_layer& L) {
 
 // LDS layout of the Key workgroup: the code rows (the staged page, 128 rows of 256 bytes,
 // lies in their first 32 KB until phase 1 has read it), partial min/max, the channel map, the
-// fp16 tier's channels.
+// fp16 tier's channels, the page's block of the page-major Key scale/min copy (gathered here and
+// stored as whole 16-byte chunks: at most 48 blocks of 32 bytes).
 struct FastLds {
-    int pmm, cpos, tidx, total;
+    int pmm, cpos, tidx, sm, total;
 };
+
+constexpr int kSmBlockMax = 48;  // 8-slot blocks of three integer tiers of at most 4 K-steps each
 
 __device__ __host__ inline FastLds fast_lds(int ld, int w16) {
     FastLds f;
     f.pmm = kFastP * ld;                                 // after [128][ld] code bytes (ld % 16 == 0)
     f.cpos = f.pmm + 4 * 128 * 8;                        // [4][128] float2 -> [128] int16
     f.tidx = f.cpos + 128 * 2;                           // [w16] int16
-    f.total = f.tidx + ((w16 * 2 + 15) & ~15) + 16;
+    f.sm = f.tidx + ((w16 * 2 + 15) & ~15);              // [48][16] fp16 (16-byte aligned)
+    f.total = f.sm + kSmBlockMax * 32 + 16;
     return f;
 }
 
@@ -611,6 +637,13 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& Lsrc, cons
     int tcnt[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) tcnt[t] = value || L.k_width[t] == 0 ? 0 : L.tier_count[t][h];
+    // the page's block of the page-major scale/min copy (none: 0 blocks) and the tiers' first
+    // blocks, in scalar registers before any store
+    const bool has_sm = !value && L.k_sm_page != nullptr;
+    const SmPage sp = sm_page(L.k_words);
+    int sm_nb = has_sm ? sp.nb : 0, sm_b1 = sp.blk0[1], sm_b2 = sp.blk0[2];
+    uint16_t* smg = has_sm ? L.k_sm_page + sm_page_idx(L, b, h, page) : nullptr;
+    asm volatile("" : "+s"(sm_nb), "+s"(sm_b1), "+s"(sm_b2), "+s"(smg));
     const int64_t dst_tok0 = static_cast<int64_t>(page) * kFastP;
     constexpr int D = 128;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -629,6 +662,7 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& Lsrc, cons
     int16_t* cpos = reinterpret_cast<int16_t*>(smem + fl.cpos);            // [128] code byte of a channel,
                                                                             // -1 - rank for the fp16 tier
     int16_t* tidx = reinterpret_cast<int16_t*>(smem + fl.tidx);            // [w16] channel of an fp16 slot
+    uint16_t* smblk = reinterpret_cast<uint16_t*>(smem + fl.sm);           // the page's k_sm_page block
     const CodeSegs cs = code_segs(L);  // cs.seg[3] <= Ld (the launcher's choice of Ld)
 
     const int w0 = L.k_width[0], w1 = L.k_width[1], w2 = L.k_width[2], w16 = L.k_width[3];
@@ -680,6 +714,18 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& Lsrc, cons
                 km[o] = 0;
             }
         }
+        // page-major copy (k_sm_page), gathered in LDS: positions of no channel of this head --
+        // ranks at or past the tier's count, padding ranks of a block -- hold scale 1.0, min 0.0;
+        // the channels' own positions are written with their scales in phase 2
+        if (tid < 8 * sm_nb) {
+            const int gb = tid >> 3, pos = tid & 7;
+            const int t = gb >= sm_b2 ? 2 : gb >= sm_b1 ? 1 : 0;
+            const int j = sm_slot(t, gb - (t == 2 ? sm_b2 : t == 1 ? sm_b1 : 0), pos);
+            if (j >= tcnt[t]) {
+                smblk[16 * gb + pos] = 0x3C00u;
+                smblk[16 * gb + 8 + pos] = 0;
+            }
+        }
         __syncthreads();
     }
 
@@ -727,8 +773,16 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& Lsrc, cons
             const int64_t o = kgrp_idx(L, b, h, width, j, page);
             uint16_t* ks = t == 2 ? L.k_scale[2] : t == 1 ? L.k_scale[1] : L.k_scale[0];
             uint16_t* km = t == 2 ? L.k_min[2] : t == 1 ? L.k_min[1] : L.k_min[0];
-            ks[o] = f32_to_f16(sc);
-            km[o] = f32_to_f16(lo);
+            const uint16_t hs = f32_to_f16(sc), hl = f32_to_f16(lo);
+            ks[o] = hs;
+            km[o] = hl;
+            if (sm_nb != 0) {
+                int lb, bp;
+                sm_place(t, j, lb, bp);
+                uint16_t* blk = smblk + 16 * ((t == 2 ? sm_b2 : t == 1 ? sm_b1 : 0) + lb);
+                blk[bp] = hs;
+                blk[8 + bp] = hl;
+            }
         }
         uint8_t* crow = codes + (32 * ck) * Ld + pos;
         if (raw <= 1e5f) {
@@ -741,7 +795,8 @@ __device__ __forceinline__ void pack_fast_page(const lf_packed_layer& Lsrc, cons
     }
     __syncthreads();
 
-    // ---- phase 4: the integer tiers' words ----
+    // ---- phase 4: the integer tiers' words; the page-major scale/min block leaves as 16-byte chunks ----
+    if (tid < 2 * sm_nb) reinterpret_cast<uint4*>(smg)[tid] = reinterpret_cast<const uint4*>(smblk)[tid];
     const int64_t row0 = tok_row(L, b, h, dst_tok0);
     const int kw0 = L.k_words[0], kw1 = L.k_words[1], kw2 = L.k_words[2];
     tier_words<2, Ld>(codes, 0, kw0, tcnt[0], L.k_code[0] + row0 * kw0, tid);

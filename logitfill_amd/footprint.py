@@ -11,11 +11,16 @@ The stored layout pads differently: every head's tier row is as wide as the wide
 slots keep a scale and a min too.  ``stored_footprint`` counts those bytes -- the ones a
 decode step actually reads (it agrees with ``bench.algorithmic_bytes``) -- and
 ``stored_bytes`` sums the tensors of a live cache layer; the analytical figure understates
-both whenever heads differ in their tier counts.
+both whenever heads differ in their tier counts.  Beside the reference layout a layer stores a
+page-major copy of the Key scales and mins (``page_copy_bytes``, the form the matrix-core decode
+kernel reads in place of the reference's scale/min arrays: per page and kv head, 8-slot blocks
+of the integer tiers, 32 bytes each).
 """
 from __future__ import annotations
 
 import numpy as np
+
+from logitfill_amd.packed.layout import sm_page_elems
 
 LEVEL_BITS = np.array([2, 4, 8, 16], dtype=np.int64)
 
@@ -87,14 +92,18 @@ def stored_footprint(levels, seq_len: int, *, page_size: int = 128, k_group_size
     hist = int(seq_len) // page_size * page_size
     residual = int(seq_len) - hist
     groups = hist // k_group_size
-    k_payload = k_meta = tables = 0
+    k_payload = k_meta = tables = page_copy = 0
     for layer in range(L):
         counts = [(values[layer] == code).sum(axis=-1) for code in range(4)]
         widths = [int(c.max()) if c.size else 0 for c in counts]
+        words = []
         for t, bits in enumerate((2, 4, 8)):
             per = 32 // bits
-            k_payload += hist * H * 4 * (-(-widths[t] // per))
+            words.append(-(-widths[t] // per))
+            k_payload += hist * H * 4 * words[t]
             k_meta += H * widths[t] * groups * 2 * 2
+        if k_group_size == page_size and sum(words):
+            page_copy += (hist // page_size) * H * 2 * sm_page_elems(words)
         k_payload += hist * H * widths[3] * 2
         # index [H, width] + count [H] + local [H, D] (int32) per tier, and the [H, D] tier map
         tables += sum(4 * (H * w + H + H * D) for w in widths) + 4 * H * D
@@ -106,7 +115,8 @@ def stored_footprint(levels, seq_len: int, *, page_size: int = 128, k_group_size
         v_meta = hist * L * H * (D // v_group_size) * 2 * 2
     parts = {"k_payload_bytes": float(k_payload), "v_payload_bytes": float(v_payload),
              "metadata_bytes": float(k_meta + v_meta + tables),
-             "residual_bytes": float(residual * channels * 2 * dtype_bytes)}
+             "residual_bytes": float(residual * channels * 2 * dtype_bytes),
+             "page_copy_bytes": float(page_copy)}
     out = _summary(seq_len, hist, residual, values, bit_v, parts, float(seq_len * channels * 2))
     out["scale_min_bytes"] = float(k_meta + v_meta)
     out["table_bytes"] = float(tables)
@@ -118,7 +128,8 @@ def stored_bytes(layer, b: int = 0) -> dict:
     its tensors: the packed history rows ``[0, hist_len)`` (``history_views``) and the
     residual tail (the per-layer tier tables are not per sequence and are left out)."""
     hist, tail = int(layer.hist_lens[b]), int(layer.tail_lens[b])
-    out = {"k_payload_bytes": 0, "v_payload_bytes": 0, "scale_min_bytes": 0, "residual_bytes": 0}
+    out = {"k_payload_bytes": 0, "v_payload_bytes": 0, "scale_min_bytes": 0, "residual_bytes": 0,
+           "page_copy_bytes": 0}
     hist_k, hist_v = layer.history_views(b)
     if hist_k is not None:
         for t in range(3):
@@ -130,10 +141,14 @@ def stored_bytes(layer, b: int = 0) -> dict:
         else:
             out["v_payload_bytes"] += hist_v["code"].numel() * hist_v["code"].element_size()
             out["scale_min_bytes"] += sum(hist_v[k].numel() * hist_v[k].element_size() for k in ("scale", "min"))
+        copy = layer.page_scale_copy(b)
+        if copy is not None:
+            out["page_copy_bytes"] = copy.numel() * copy.element_size()
     tk, tv = layer.tail_buffers()
     if tail and tk is not None:
         out["residual_bytes"] = tail * layer.n_kv * layer.head_dim * (tk.element_size() + tv.element_size())
     out["history_tokens"] = hist
     out["residual_tokens"] = tail
-    out["total_bytes"] = sum(out[k] for k in ("k_payload_bytes", "v_payload_bytes", "scale_min_bytes", "residual_bytes"))
+    out["total_bytes"] = sum(out[k] for k in ("k_payload_bytes", "v_payload_bytes", "scale_min_bytes", "residual_bytes",
+                                              "page_copy_bytes"))
     return out

@@ -29,6 +29,7 @@ from logitfill_amd.packed.layout import (
     _ptr,
     device_tables,
     make_layer_struct,
+    sm_page_elems,
     tier_tables,
     tier_widths,
     value_words,
@@ -135,6 +136,15 @@ class _LayerStore:
             hist_v = {"code": s["v_code"][b, :, :H], "scale": s["v_scale"][b, :, :H], "min": s["v_min"][b, :, :H]}
         return hist_k, hist_v
 
+    def page_scale_copy(self, b: int = 0):
+        """Sequence ``b``'s pages of the page-major Key scale/min copy (``[n_kv, pages,
+        16 * blocks]`` fp16, the matrix-core decode kernel's form of the Key scales and mins), or
+        None when the layer keeps none or holds no page."""
+        self.flush()
+        if self._s is None or "k_sm_page" not in self._s or self.hist_lens[b] == 0:
+            return None
+        return self._s["k_sm_page"][b, :, : self.hist_lens[b] // self.page_size]
+
     def export_reference(self, b: int = 0):
         """Contiguous copies of ``history_views(b)``: the exact tensors the reference would hold."""
         hk, hv = self.history_views(b)
@@ -154,16 +164,17 @@ class _LayerStore:
         old, old_cap = self._s, self._cap
         B, H, D, dev = self.batch, self.n_kv, self.head_dim, self.device
         W, WD = self.widths, self.words
-        # Key-group capacity rounded up to even: the decode kernel fetches the fp16 scale/min of
-        # two consecutive pages as one aligned 4-byte word.
         groups = cap // self.k_group_size
-        groups += groups & 1
         s = {
             "k_code": [torch.zeros(B, H, cap, WD[t], dtype=torch.int32, device=dev) for t in range(3)],
             "k_scale": [torch.ones(B, H, W[t], groups, dtype=torch.float16, device=dev) for t in range(3)],
             "k_min": [torch.zeros(B, H, W[t], groups, dtype=torch.float16, device=dev) for t in range(3)],
             "k_value16": torch.zeros(B, H, cap, W[3], dtype=torch.float16, device=dev),
         }
+        if self.k_group_size == P and sum(WD):
+            # page-major copy of the Key scales / mins for the matrix-core decode kernel (the
+            # packers write it beside the reference arrays; lf_common.hpp: sm_page)
+            s["k_sm_page"] = torch.zeros(B, H, groups, sm_page_elems(WD), dtype=torch.float16, device=dev)
         if self.bit_v >= 16:
             s["v_value16"] = torch.zeros(B, H, cap, D, dtype=torch.float16, device=dev)
         else:
@@ -180,6 +191,8 @@ class _LayerStore:
             for name in ("k_value16", "v_value16", "v_code", "v_scale", "v_min"):
                 if name in s:
                     s[name][:, :, :old_cap].copy_(old[name])
+            if "k_sm_page" in s:
+                s["k_sm_page"][:, :, :og].copy_(old["k_sm_page"])
         self._s, self._cap = s, cap
         self._struct = None
 
@@ -199,7 +212,7 @@ class _LayerStore:
                 k_group=self.k_group_size, v_group=self.v_group_size, bit_v=self.bit_v,
                 k_code=s["k_code"], k_scale=s["k_scale"], k_min=s["k_min"], k_value16=s["k_value16"],
                 v_code=s.get("v_code"), v_scale=s.get("v_scale"), v_min=s.get("v_min"),
-                v_value16=s.get("v_value16"))
+                v_value16=s.get("v_value16"), k_sm_page=s.get("k_sm_page"))
         return self._struct
 
     def tail_buffers(self):

@@ -147,10 +147,19 @@ def _ptr(t) -> int:
     return 0 if t is None or t.numel() == 0 else int(t.data_ptr())
 
 
+def sm_page_elems(words) -> int:
+    """fp16 elements of one page's block of the page-major Key scale/min copy (``k_sm_page``):
+    8-slot blocks of the integer tiers in the decode kernel's K-step order -- int2 2 * ceil(w / 4)
+    steps, int4 ceil(w / 4), int8 ceil(ceil(w / 2) / 4), 4 blocks a step -- each 8 scales then 8
+    mins (``lf_common.hpp``: sm_page)."""
+    steps = 2 * -(-int(words[0]) // 4) + -(-int(words[1]) // 4) + -(-(-(-int(words[2]) // 2)) // 4)
+    return 16 * 4 * steps
+
+
 def make_layer_struct(table: dict, table_dev: dict, *, batch: int, n_kv: int, head_dim: int,
                       cap_tokens: int, cap_kgroups: int, page_size: int, k_group: int, v_group: int,
                       bit_v: int, k_code, k_scale, k_min, k_value16, v_code=None, v_scale=None,
-                      v_min=None, v_value16=None) -> _native.PackedLayer:
+                      v_min=None, v_value16=None, k_sm_page=None) -> _native.PackedLayer:
     """Fill an ``lf_packed_layer`` from device tensors (kept alive by the caller)."""
     widths, words = tier_widths(table)
     s = _native.PackedLayer()
@@ -163,6 +172,7 @@ def make_layer_struct(table: dict, table_dev: dict, *, batch: int, n_kv: int, he
     s.v_scale = _ptr(v_scale)
     s.v_min = _ptr(v_min)
     s.v_value16 = _ptr(v_value16)
+    s.k_sm_page = _ptr(k_sm_page)
     for t in range(4):
         s.tier_index[t] = _ptr(table_dev[t]["index"])
         s.tier_count[t] = _ptr(table_dev[t]["count"])

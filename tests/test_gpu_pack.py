@@ -197,3 +197,63 @@ def test_cpu_tensors_raise(gpu):
         pl.quantize_key_page(d.key[0], t2, 128)
     with pytest.raises(RuntimeError, match="ROCm"):
         PackedKVManager([d.levels], 4, 4, 128, 128, 128, 128, 2, "cpu")
+
+
+def _sm_blocks(words):
+    """First block of each integer tier and the block count of a page's k_sm_page block."""
+    steps = [2 * -(-words[0] // 4), -(-words[1] // 4), -(-(-(-words[2] // 2)) // 4)]
+    return [0, 4 * steps[0], 4 * (steps[0] + steps[1])], 4 * sum(steps)
+
+
+def _check_page_copy(layer, b):
+    """Every page's k_sm_page block holds, per integer tier, exactly the reference arrays' fp16
+    (scale, min) pairs of the head's real channels and (1.0, 0.0) at every other position of the
+    tier's blocks (the positions themselves are what the decode parity tests pin: the matrix-core
+    kernel reads the Key scales only from this copy)."""
+    hk, _ = layer.export_reference(b)
+    copy = layer.page_scale_copy(b).cpu().numpy().view(np.uint16)      # [n_kv, pages, 16 * nb]
+    blk0, nb = _sm_blocks(layer.words)
+    ends = blk0[1:] + [nb]
+    counts = [layer.table[t]["count"].cpu().numpy() for t in range(3)]
+    for h in range(layer.n_kv):
+        for p in range(copy.shape[1]):
+            blocks = copy[h, p].reshape(nb, 2, 8)                         # [block][scale, min][8]
+            for t in range(3):
+                seg = blocks[blk0[t]:ends[t]]
+                got = sorted(zip(seg[:, 0].reshape(-1).tolist(), seg[:, 1].reshape(-1).tolist()))
+                cnt = int(counts[t][h])
+                sc = hk[t]["scale"][h, :cnt, p].cpu().numpy().view(np.uint16).tolist()
+                mn = hk[t]["min"][h, :cnt, p].cpu().numpy().view(np.uint16).tolist()
+                want = sorted(list(zip(sc, mn)) + [(0x3C00, 0)] * (seg.shape[0] * 8 - cnt))
+                assert got == want, (h, p, t)
+
+
+@pytest.mark.parametrize("path", ["fast", "generic", "deferred"])
+def test_page_major_scale_copy_matches_reference_arrays(gpu, path):
+    """The page-major Key scale/min copy written by the fast packer (bf16 pages), the generic
+    packer (float32 pages) and the one-launch deferred flush (lf_pack_pages_multi) against the
+    reference-layout arrays of the same pages, for ragged heads (c2's tier sampler)."""
+    n_kv, D, B = 4, 128, 2
+    lv = synth.sample_tier_levels(n_kv, D, 2.5, seed=77)
+    d = synth.make_layer(B, 28, n_kv, D, 3 * 128 + 50, 2.5, seed=77)
+    d.levels = lv
+    key = d.key.float() if path == "generic" else d.key
+    value = d.value.float() if path == "generic" else d.value
+    m = PackedKVManager([lv, lv], 28, n_kv, D, 128, 128, 128, 2, gpu, batch_size=B,
+                        defer_flush=path == "deferred")
+    if path == "deferred":
+        # a decode loop: every layer commits the token, then one flush packs the step's pages of
+        # both layers in one lf_pack_pages_multi launch
+        kg, vg = key.to(gpu), value.to(gpu)
+        for t in range(3 * 128 + 50):
+            for layer in range(2):
+                m.commit(layer, kg[:, :, t:t + 1], vg[:, :, t:t + 1])
+            m.flush_pending()
+    else:
+        for layer in range(2):
+            m.commit(layer, key.to(gpu), value.to(gpu))
+    torch.cuda.synchronize()
+    for layer in range(2):
+        for b in range(B):
+            assert m.layers[layer].hist_lens[b] == 3 * 128
+            _check_page_copy(m.layers[layer], b)

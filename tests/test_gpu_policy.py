@@ -43,6 +43,6 @@ def test_stored_bytes_match_footprint(gpu, tb, tokens):
     mgr.commit(0, d.key.to(gpu), d.value.to(gpu))
     live = footprint.stored_bytes(mgr.layers[0], 0)
     want = footprint.stored_footprint(d.levels[None], tokens)
-    for key in ("k_payload_bytes", "v_payload_bytes", "scale_min_bytes", "residual_bytes"):
+    for key in ("k_payload_bytes", "v_payload_bytes", "scale_min_bytes", "residual_bytes", "page_copy_bytes"):
         assert live[key] == want[key], key
     assert live["history_tokens"] == want["history_tokens"] and live["residual_tokens"] == want["residual_tokens"]

@@ -112,6 +112,11 @@ def test_stored_footprint_known_answer():
     assert f["v_payload_bytes"] == 128 * 2 * 2 * 4
     assert f["table_bytes"] == 4 * (106 + 90 + 74 + 70) + 4 * 64
     assert f["residual_bytes"] == 10 * 64 * 4
+    # page-major Key scale/min copy: int2 2 words -> 2 K-steps, int4 2 -> 1, int8 1 -> 1: 4 steps
+    # of 4 blocks, 32 bytes a block, per page (2) and head (2)
+    assert f["page_copy_bytes"] == 2 * 2 * 4 * 4 * 32
+    assert f["total_bytes"] == sum(f[k] for k in ("k_payload_bytes", "v_payload_bytes", "metadata_bytes",
+                                                  "residual_bytes", "page_copy_bytes"))
 
 
 @pytest.mark.parametrize("tb", [2.5, 3.0])
