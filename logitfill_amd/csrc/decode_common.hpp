@@ -53,8 +53,9 @@ __device__ __forceinline__ void load8_as_f32(const void* base, int64_t idx, int 
     }
 }
 
-// Bring the kernel's argument block (its first Bytes / 64 whole 64-byte lines: reads stay inside the
-// explicit arguments) into the scalar data cache with one round of loads, issued from one asm
+// Bring the kernel's argument block (ceil(Bytes / 64) whole 64-byte lines: the last may reach into
+// the hidden arguments that follow the explicit ones in the kernarg segment) into the scalar data
+// cache with one round of loads, issued from one asm
 // statement so that no compiler wait splits it.  The compiler reads argument fields lazily, a small
 // load and a wait at a time where register pressure makes it re-read them; with the block already
 // cached each of those waits is a cache hit instead of a memory round trip.  The loaded values are
@@ -66,8 +67,8 @@ __device__ __forceinline__ void load8_as_f32(const void* base, int64_t idx, int 
     "s52", "s53", "s54", "s55"
 template <int Bytes>
 __device__ __forceinline__ void prefetch_args() {
-    constexpr int lines = Bytes / 64;
-    static_assert(lines >= 6 && lines <= 9, "prefetch_args: add the line count of this argument block");
+    constexpr int lines = (Bytes + 63) / 64;
+    static_assert(lines >= 6 && lines <= 10, "prefetch_args: add the line count of this argument block");
     const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
     if constexpr (lines == 6)
         asm volatile(LF_ARG_LINES6 "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
@@ -75,9 +76,12 @@ __device__ __forceinline__ void prefetch_args() {
         asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
     else if constexpr (lines == 8)
         asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
-    else
+    else if constexpr (lines == 9)
         asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) LF_ARG_LINE(512) "s_waitcnt lgkmcnt(0)" ::"s"(kp)
                      : LF_ARG_CLOBBERS);
+    else
+        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) LF_ARG_LINE(512) LF_ARG_LINE(576)
+                     "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
 }
 #undef LF_ARG_CLOBBERS
 #undef LF_ARG_LINES6

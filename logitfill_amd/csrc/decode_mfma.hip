@@ -86,7 +86,9 @@ struct MfmaLayout {
     int rawb_bytes;
     int ck_v16;          // prepared: [128][w16p] fp16 Key fp16 tier, zero padded (after Qs), one spare dword
     int ck_bytes;
-    int off_qperm;       // [nb][8 heads][8] fp32: q * scaling*log2e per slot (0 for padding)
+    int off_qperm;       // [nb][2][8 heads][4] fp32: q * scaling*log2e per slot (0 for padding), a block's
+                         // positions 0..3 of the 8 heads, then its positions 4..7 (a 16-byte read
+                         // per lane and half, consecutive lanes at consecutive addresses)
     int off_small;       // alpha [waves][8], wave m/l/mid [waves][3][8]
     int slot_bytes;      // one page slot: Key-code buffer, then rest buffer
     int off_ck;          // the prepared buffer
@@ -252,7 +254,7 @@ struct QsRegs {
 
 __device__ __forceinline__ void qs_fetch(const float* qrow, const unsigned char* smb, QsRegs& r) {
     r.q0 = *reinterpret_cast<const float4*>(qrow);
-    r.q1 = *reinterpret_cast<const float4*>(qrow + 4);
+    r.q1 = *reinterpret_cast<const float4*>(qrow + 32);
     r.s = *reinterpret_cast<const uint4*>(smb);
     r.m = *reinterpret_cast<const uint4*>(smb + 16);
 }
@@ -460,7 +462,7 @@ __device__ __forceinline__ void prep_load(const LoopY& z, const F16Map& fm, cons
     }
     const int lane = tid & 63, n = lane & 7, j = lane >> 3;
     const int nbw = (z.nb_int + 3) >> 2, gb = min(wave * nbw + j, z.nb_int - 1);
-    qs_fetch(qperm + (gb * 8 + n) * 8, raw + z.rawb_sm + 32 * gb, r.qs);
+    qs_fetch(qperm + gb * 64 + 4 * n, raw + z.rawb_sm + 32 * gb, r.qs);
 }
 
 // Integer-tier Qs and bias of head n for block gb from fetched operands.
@@ -524,7 +526,7 @@ __device__ __forceinline__ void prep_store(const LoopY& z, const F16Map& fm, con
             const int gb2 = wave * nbw + jj;
             if (n < g && gb2 < z.nb_int) {
                 QsRegs q2;
-                qs_fetch(qperm + (gb2 * 8 + n) * 8, raw + z.rawb_sm + 32 * gb2, q2);
+                qs_fetch(qperm + gb2 * 64 + 4 * n, raw + z.rawb_sm + 32 * gb2, q2);
                 bsum += qs_block(z, q2, qs, gb2, n);
             }
         }
@@ -1011,9 +1013,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
                 for (int r = 0; r < 2; ++r) {
                     const int n = n0 + r;
                     if (i < z.kf3) {
-                        float4* dst = reinterpret_cast<float4*>(qperm + (gb * 8 + n) * 8);
-                        dst[0] = float4{qv[r][0], qv[r][1], qv[r][2], qv[r][3]};
-                        dst[1] = float4{qv[r][4], qv[r][5], qv[r][6], qv[r][7]};
+                        float* dst = qperm + gb * 64 + 4 * n;
+                        *reinterpret_cast<float4*>(dst) = float4{qv[r][0], qv[r][1], qv[r][2], qv[r][3]};
+                        *reinterpret_cast<float4*>(dst + 32) = float4{qv[r][4], qv[r][5], qv[r][6], qv[r][7]};
                     }
                     if (i >= z.kf3 || n >= g) {
                         half8 hi, lo;
