@@ -49,8 +49,11 @@ __device__ __forceinline__ float bf16f(uint16_t x) { return __uint_as_float(stat
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void*)p)));
 }
+// The V rows stream through once: their DMA carries the non-temporal hint, as the packed kernel's
+// pages do (208.7 -> 188.4 us per c2 layer-step in a same-box A/B).  The same hint on the K loads,
+// which go straight into registers, made the kernel slower (209 -> 257 us), so they have none.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(lds) : "memory");
 }
 
 // Max of x over the four 16-lane rows (permlane swaps; see decode_mfma.hip for why both
