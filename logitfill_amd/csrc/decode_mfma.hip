@@ -331,52 +331,50 @@ struct DmaSrc {
     int n_chunk;                // 16-byte DMA instructions this wave issues per page
 };
 
-__device__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout& y, int b, int h, int pbeg,
-                          int wave, int lane) {
+// The segments of a region are consecutive in chunk order, so chunk c of a lane lies at
+// base[s] + 16 c, base[s] = the segment's first byte - 16 * (its first chunk), for the segment s
+// that c falls in: the bases and strides are scalars, and each lane picks its own with compares
+// and selects -- no divergent branches, a few dozen instructions before the first DMA.  Empty
+// segments (a tier of width 0) have equal boundaries and are never picked.
+__device__ __forceinline__ void dma_setup(DmaSrc& s, const lf_packed_layer& L, const MfmaLayout& y, int b, int h,
+                                          int pbeg, int wave, int lane) {
     const int64_t row0 = tok_row(L, b, h, static_cast<int64_t>(pbeg) * kPage);
     const int na = y.seg_end[2];             // region A chunks
     const int nb_chunks = y.n_chunks - na;   // region B chunks
+    const int e0 = y.seg_end[0], e1 = y.seg_end[1];
     const int c_f16 = 288, c_sm = 288 + kPage * L.k_width[3] * 2 / 16;  // region B segment starts
+    const auto addr = [](const void* ptr, int64_t bytes, int first_chunk) {
+        return reinterpret_cast<uint64_t>(ptr) + static_cast<uint64_t>(bytes) - 16u * static_cast<uint64_t>(first_chunk);
+    };
+    // region A: Key-code rows K0, K1, K2
+    const uint64_t ka0 = addr(L.k_code[0], row0 * L.k_words[0] * 4, 0);
+    const uint64_t ka1 = addr(L.k_code[1], row0 * L.k_words[1] * 4, e0);
+    const uint64_t ka2 = addr(L.k_code[2], row0 * L.k_words[2] * 4, e1);
+    const uint32_t ks0 = kPage * L.k_words[0] * 4, ks1 = kPage * L.k_words[1] * 4, ks2 = kPage * L.k_words[2] * 4;
+    // region B: v scale (16 chunks), v min (16), v codes (256), fp16-tier rows, the k_sm_page block
+    const uint64_t vb0 = addr(L.v_scale, row0 * 2, 0);
+    const uint64_t vb1 = addr(L.v_min, row0 * 2, 16);
+    const uint64_t vb2 = addr(L.v_code, row0 * 32, 32);
+    const uint64_t vb3 = addr(L.k_value16, row0 * L.k_width[3] * 2, c_f16);
+    const uint64_t vb4 = addr(L.k_sm_page, sm_page_idx(L, b, h, pbeg) * 2, c_sm);
+    const uint32_t vs3 = kPage * L.k_width[3] * 2, vs4 = 32 * y.nb_int;
     s.n_chunk = 0;
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
         const int j = kWaves * i + wave;
         if (j < y.ja + y.jb) s.n_chunk = i + 1;
-        const unsigned char* src = reinterpret_cast<const unsigned char*>(L.k_code[0]);
+        uint64_t src = ka0;
         uint32_t stride = 0;
         if (j < y.ja) {
             const int c = min(64 * j + lane, na - 1);
-            if (c < y.seg_end[0]) {
-                src = reinterpret_cast<const unsigned char*>(L.k_code[0] + row0 * L.k_words[0]) + 16 * c;
-                stride = kPage * L.k_words[0] * 4;
-            } else if (c < y.seg_end[1]) {
-                src = reinterpret_cast<const unsigned char*>(L.k_code[1] + row0 * L.k_words[1]) + 16 * (c - y.seg_end[0]);
-                stride = kPage * L.k_words[1] * 4;
-            } else {
-                src = reinterpret_cast<const unsigned char*>(L.k_code[2] + row0 * L.k_words[2]) + 16 * (c - y.seg_end[1]);
-                stride = kPage * L.k_words[2] * 4;
-            }
+            src = (c >= e1 ? ka2 : c >= e0 ? ka1 : ka0) + 16u * static_cast<uint32_t>(c);
+            stride = c >= e1 ? ks2 : c >= e0 ? ks1 : ks0;
         } else if (j < y.ja + y.jb) {
-            // region B: v scale (16 chunks), v min (16), v codes (256), fp16-tier rows, the k_sm_page block
             const int c = min(64 * (j - y.ja) + lane, nb_chunks - 1);
-            if (c < 16) {
-                src = reinterpret_cast<const unsigned char*>(L.v_scale + row0) + 16 * c;
-                stride = kPage * 2;
-            } else if (c < 32) {
-                src = reinterpret_cast<const unsigned char*>(L.v_min + row0) + 16 * (c - 16);
-                stride = kPage * 2;
-            } else if (c < c_f16) {
-                src = reinterpret_cast<const unsigned char*>(L.v_code + row0 * 8) + 16 * (c - 32);
-                stride = kPage * 32;
-            } else if (c < c_sm) {
-                src = reinterpret_cast<const unsigned char*>(L.k_value16 + row0 * L.k_width[3]) + 16 * (c - c_f16);
-                stride = kPage * L.k_width[3] * 2;
-            } else {
-                src = reinterpret_cast<const unsigned char*>(L.k_sm_page + sm_page_idx(L, b, h, pbeg)) + 16 * (c - c_sm);
-                stride = 32 * y.nb_int;
-            }
+            src = (c >= c_sm ? vb4 : c >= c_f16 ? vb3 : c >= 32 ? vb2 : c >= 16 ? vb1 : vb0) + 16u * static_cast<uint32_t>(c);
+            stride = c >= c_sm ? vs4 : c >= c_f16 ? vs3 : c >= 32 ? kPage * 32 : kPage * 2;
         }
-        s.chunk[i] = src;
+        s.chunk[i] = reinterpret_cast<const unsigned char*>(src);
         s.chunk_stride[i] = stride;
     }
 }
@@ -390,7 +388,9 @@ __device__ __forceinline__ void dma_page(DmaSrc& s, uint32_t slot, int wave) {
     // instead of hoisting per-instruction conditions out of the page loop.
     int n_chunk = __builtin_amdgcn_readfirstlane(s.n_chunk);
     asm volatile("" : "+s"(n_chunk));
-    const uint32_t d16 = slot + 1024 * wave;
+    // the destinations are uniform: kept in an SGPR (one scalar add per instruction into M0)
+    uint32_t d16 = __builtin_amdgcn_readfirstlane(slot + 1024 * wave);
+    asm volatile("" : "+s"(d16));
 #pragma unroll
     for (int i = 0; i < kMaxDma; ++i) {
         if (i < n_chunk) {
@@ -882,6 +882,48 @@ __device__ __forceinline__ void residual_mfma(const DecodeParams& p, int b, int 
     __syncthreads();
 }
 
+
+// Merge NP wave partials (m, l, mid of each head in wstat [NP][3][8], o in red [NP][8][128])
+// into the item's partial record of each of the g rows: thread tid takes row tid / 32, channels
+// 4 (tid % 32) .. + 3.  Every LDS read of a thread goes out in one batch (the partials of a
+// head are the same for the 32 threads of a half wave: broadcast reads), then one exp2 per
+// partial, then the stores.
+template <int NP>
+__device__ __forceinline__ void merge_partials(const DecodeParams& p, int item, int h, int row0, int g,
+                                               const float* wstat, const float* red, int tid) {
+    const int i = tid >> 5, c4 = 4 * (tid & 31);
+    if (i >= g) return;
+    float mw[NP], lw[NP], dw[NP];
+    float4 ow[NP];
+#pragma unroll
+    for (int w = 0; w < NP; ++w) {
+        mw[w] = wstat[(w * 3 + 0) * 8 + i];
+        lw[w] = wstat[(w * 3 + 1) * 8 + i];
+        dw[w] = wstat[(w * 3 + 2) * 8 + i];
+        ow[w] = *reinterpret_cast<const float4*>(red + (w * 8 + i) * kD + c4);
+    }
+    float M = mw[0];
+#pragma unroll
+    for (int w = 1; w < NP; ++w) M = fmaxf(M, mw[w]);
+    float4 o = {0.f, 0.f, 0.f, 0.f};
+    float l = 0.f;
+    if (M != -__builtin_inff()) {
+#pragma unroll
+        for (int w = 0; w < NP; ++w) {
+            const float sc = __builtin_amdgcn_exp2f(mw[w] - M);
+            o.x = fmaf(sc, ow[w].x + dw[w], o.x);
+            o.y = fmaf(sc, ow[w].y + dw[w], o.y);
+            o.z = fmaf(sc, ow[w].z + dw[w], o.z);
+            o.w = fmaf(sc, ow[w].w + dw[w], o.w);
+            l = fmaf(sc, lw[w], l);
+        }
+    }
+    // records are (D + 2) floats: 8-byte aligned, so the four channels go out as two float2
+    float* rec = part_rec(p, item, h, row0 + i);
+    *reinterpret_cast<float2*>(rec + c4) = float2{o.x, o.y};
+    *reinterpret_cast<float2*>(rec + c4 + 2) = float2{o.z, o.w};
+    if (c4 == 0) *reinterpret_cast<float2*>(rec + kD) = float2{M, l};
+}
 
 __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
     prefetch_args<sizeof(MfmaParams)>();
@@ -1415,27 +1457,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     }
 
     // ---- merge the wave partials and store this item's partial ----
-    const int n_part = kind == 2 ? 2 * kWaves : kWaves;
-    for (int e = tid; e < g * kD; e += kThreads) {
-        const int i = e / kD, c = e % kD;
-        float M = -__builtin_inff();
-        for (int w = 0; w < n_part; ++w) M = fmaxf(M, wstat[(w * 3 + 0) * 8 + i]);
-        float o = 0.f, l = 0.f;
-        if (M != -__builtin_inff()) {
-            for (int w = 0; w < n_part; ++w) {
-                const float mw = wstat[(w * 3 + 0) * 8 + i];
-                const float sc = __builtin_amdgcn_exp2f(mw - M);
-                o += sc * (red[(w * 8 + i) * kD + c] + wstat[(w * 3 + 2) * 8 + i]);
-                l += sc * wstat[(w * 3 + 1) * 8 + i];
-            }
-        }
-        float* rec = part_rec(p, item, h, row0 + i);
-        rec[c] = o;
-        if (c == 0) {
-            rec[kD] = M;
-            rec[kD + 1] = l;
-        }
-    }
+    if (kind == 2) merge_partials<2 * kWaves>(p, item, h, row0, g, wstat, red, tid);
+    else merge_partials<kWaves>(p, item, h, row0, g, wstat, red, tid);
 }
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
