@@ -430,7 +430,10 @@ __device__ __forceinline__ F16Map f16_map(const LoopY& z, int w16, int tid) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int d = tid + 256 * i;
-        const int t = hw ? d / hw : 0, c = hw ? d - t * hw : 0;
+        // d / hw through the reciprocal: (d + 0.5) / hw lies at least 0.5 / hw (>= 1/128) from an
+        // integer, far beyond the rounding of the product for d < 512
+        const int t = hw ? static_cast<int>((static_cast<float>(d) + 0.5f) * __builtin_amdgcn_rcpf(static_cast<float>(hw))) : 0;
+        const int c = hw ? d - t * hw : 0;
         const bool live = hw && t < kPage;
         const bool lo = live && 2 * c < w16, hi = live && 2 * c + 1 < w16;
         m.src[i] = lo ? kRawbF16 + 2 * (t * w16 + 2 * c) : 0;
@@ -1032,10 +1035,22 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
         float4 q4 = {0.f, 0.f, 0.f, 0.f};
         if (qn < g) {
             const int64_t qrow = (static_cast<int64_t>(b) * A.n_q + h * p.g + row0 + qn) * kD + qc0;
-            q4.x = load_as_f32(A.query, qrow + 0, A.q_dtype) * p.qscale;
-            q4.y = load_as_f32(A.query, qrow + 1, A.q_dtype) * p.qscale;
-            q4.z = load_as_f32(A.query, qrow + 2, A.q_dtype) * p.qscale;
-            q4.w = load_as_f32(A.query, qrow + 3, A.q_dtype) * p.qscale;
+            // 2-byte q (8-byte aligned): the thread's four channels in one load
+            if (A.q_dtype != LF_FP32 && (reinterpret_cast<uintptr_t>(A.query) & 7) == 0) {
+                const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(A.query) + qrow);
+                const bool bf = A.q_dtype == LF_BF16;
+                const uint16_t e[4] = {static_cast<uint16_t>(raw.x), static_cast<uint16_t>(raw.x >> 16),
+                                       static_cast<uint16_t>(raw.y), static_cast<uint16_t>(raw.y >> 16)};
+                q4.x = (bf ? bf16_to_f32(e[0]) : f16_to_f32(e[0])) * p.qscale;
+                q4.y = (bf ? bf16_to_f32(e[1]) : f16_to_f32(e[1])) * p.qscale;
+                q4.z = (bf ? bf16_to_f32(e[2]) : f16_to_f32(e[2])) * p.qscale;
+                q4.w = (bf ? bf16_to_f32(e[3]) : f16_to_f32(e[3])) * p.qscale;
+            } else {
+                q4.x = load_as_f32(A.query, qrow + 0, A.q_dtype) * p.qscale;
+                q4.y = load_as_f32(A.query, qrow + 1, A.q_dtype) * p.qscale;
+                q4.z = load_as_f32(A.query, qrow + 2, A.q_dtype) * p.qscale;
+                q4.w = load_as_f32(A.query, qrow + 3, A.q_dtype) * p.qscale;
+            }
         }
 
         {

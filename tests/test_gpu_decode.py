@@ -100,6 +100,25 @@ def test_reference_kernel_test_shape(gpu):
     assert_decode_close(fast[0, :, 0], ref[:, 0], out_dtype="fp32", max_abs=1e-5, rel_l2=1e-5)
 
 
+def test_query_not_8_byte_aligned(gpu):
+    """A bf16 query whose rows start 2 bytes past an 8-byte boundary (a view into a larger
+    buffer): the kernel's 8-byte q loads give way to element loads, same result."""
+    d = synth.make_layer(1, 8, 2, 128, 3 * 128 + 5, 2.5, seed=13)
+    mgr, lens = build(d, [3], [5], 8, 2, 128, gpu)
+    q = d.query.to(gpu)
+    buf = torch.empty(q.numel() + 1, dtype=q.dtype, device=gpu)
+    qv = buf[1:].view(q.shape)
+    qv.copy_(q)
+    assert qv.data_ptr() % 8 == 2
+    outs = []
+    for qq in (q, qv):
+        out = torch.empty(q.shape, dtype=torch.float32, device=gpu)
+        decode_into(mgr, 0, qq, d.key_new.to(gpu), d.value_new.to(gpu), 0.1, out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("q_dtype", [torch.float16, torch.float32])
 def test_query_and_output_dtypes(gpu, q_dtype):
     d = synth.make_layer(1, 8, 2, 128, 3 * 128 + 5, 2.5, seed=12)
