@@ -113,9 +113,17 @@ def residual_pages(tail_lens) -> int:
     return RESIDUAL_FIXED_PAGES + (RESIDUAL_TAIL_PAGES * t + 63) // 127
 
 
-# Fixed cost of one split-K item (query load, page-ring start-up, the partial result's store
-# and its share of the cross-split reduce), in packed pages.
-ITEM_OVERHEAD_PAGES = 3
+# Fixed cost of one split-K item, in packed pages: the workgroup's prologue (argument block, work
+# record, DMA set-up, q and tier table: the first page's barrier passes ≈8 us after the start on
+# c2 and c1, per-workgroup stamps), its epilogue (≈1.6 us) and its share of the cross-split reduce,
+# against 1.7-2.2 us per page.
+ITEM_OVERHEAD_PAGES = 5
+# A workgroup with a CU to itself (a launch of at most one workgroup per CU) runs its pages and
+# its fixed cost this much faster than two sharing a CU.  Fitted to c1 (8 x 64 pages + a
+# 37-token residual, 2 kv heads): 5-page items (224 workgroups, one per CU) 19.7-19.8 us per
+# layer-step against 20.0-20.2 for the one-round 3-page items (368), 21.0 for 4 pages (272:
+# some share) and 20.9-26 for 6-10 pages (same-process comparison).
+ALONE_FACTOR = 0.78
 
 
 @functools.lru_cache(maxsize=256)
@@ -123,11 +131,17 @@ def _pages_per_split(pages: tuple, n_kv: int, residual_pages: int, slots: int) -
     p = np.asarray(pages, dtype=np.int64)
     work = p + residual_pages
     top = max(1, -(-n_kv * int(work.sum()) // slots))
-    size = np.arange(top, 0, -1, dtype=np.int64)[:, None]             # largest first
+    # sizes above the one-round size leave slots empty: worth it only when every workgroup then
+    # has a CU to itself
+    size = np.arange(max(top, int(work.max())), 0, -1, dtype=np.int64)[:, None]   # largest first
     items = np.where(p[None, :] == 0, 1, -(-work[None, :] // size))   # lf_plan_decode's count
-    rounds = -(-(n_kv * items.sum(axis=1)) // slots)
+    wgs = n_kv * items.sum(axis=1)
+    rounds = -(-wgs // slots)
     largest = (-(-work[None, :] // items)).max(axis=1)
-    cost = rounds * (largest + ITEM_OVERHEAD_PAGES)
+    cost = (rounds * (largest + ITEM_OVERHEAD_PAGES)).astype(np.float64)
+    alone = wgs <= slots // 2
+    cost = np.where(alone, (largest + ITEM_OVERHEAD_PAGES) * ALONE_FACTOR, cost)
+    cost = np.where((size[:, 0] > top) & ~alone, np.inf, cost)
     return int(size[int(np.argmin(cost)), 0])                          # ties: fewest items
 
 
@@ -137,8 +151,9 @@ def choose_pages_per_split(hist_pages: list[int], n_kv: int, residual_pages: int
     work (its pages plus its residual) divides evenly; with ragged lengths the per-sequence
     rounding makes more items than slots, and the excess runs as a second round of full-size
     items.  The size is therefore the one, up to that one-round size, that minimises
-    rounds x (largest item + the per-item cost), with ties going to fewer items; uniform
-    batches keep the one-round size."""
+    rounds x (largest item + the per-item cost), with ties going to fewer items -- or a larger
+    size whose items leave every workgroup a CU of its own, when that costs less at
+    ``ALONE_FACTOR`` (small batches: c1 takes 5-page items instead of 3)."""
     forced = env_int("LOGITFILL_AMD_PAGES_PER_SPLIT", 0)
     if forced > 0:
         return forced

@@ -10,7 +10,8 @@ import heapq
 import pytest
 
 from logitfill_amd import _native, synth
-from logitfill_amd.packed.reference import (ITEM_OVERHEAD_PAGES, LATE_SLOWDOWN, age_split, choose_pages_per_split,
+from logitfill_amd.packed.reference import (ALONE_FACTOR, ITEM_OVERHEAD_PAGES, LATE_SLOWDOWN, age_split,
+                                            choose_pages_per_split,
                                             plan_work, residual_pages)
 
 SLOTS = 512  # 256 CUs x 2 workgroups
@@ -54,14 +55,26 @@ def test_residual_cost_grows_with_the_tail():
     assert costs == sorted(costs)
 
 
-@pytest.mark.parametrize("hist_pages,n_kv,tail,expect", [([256] * 16, 4, 100, 33), ([64] * 8, 2, 37, 3)])
-def test_uniform_batches_keep_one_round(hist_pages, n_kv, tail, expect):
-    """c2 and c1: every sequence's work divides into the one-round size; the plan fills the
-    slots exactly once."""
-    res = residual_pages([tail])
+def test_uniform_batch_keeps_one_round():
+    """c2: every sequence's work divides into the one-round size; the plan fills the slots
+    exactly once."""
+    hist_pages, n_kv, res = [256] * 16, 4, residual_pages([100])
     pps = choose_pages_per_split(hist_pages, n_kv, res)
-    assert pps == expect == one_round_size(hist_pages, n_kv, res)
+    assert pps == 33 == one_round_size(hist_pages, n_kv, res)
     assert n_kv * len(plan_items(hist_pages, pps, res)) <= SLOTS
+
+
+def test_small_batch_takes_a_cu_per_workgroup():
+    """c1 (8 x 64 pages + a 37-token residual, 2 kv heads): 5-page items, 14 per sequence, 224
+    workgroups -- each with a CU of its own -- instead of the one-round 3-page items (368,
+    sharing CUs): (5 + overhead) x ALONE_FACTOR < 3 + overhead.  4-page items (272 workgroups)
+    would share CUs again and cost more than either."""
+    hist_pages, n_kv, res = [64] * 8, 2, residual_pages([37])
+    assert one_round_size(hist_pages, n_kv, res) == 3
+    pps = choose_pages_per_split(hist_pages, n_kv, res)
+    assert pps == 5
+    assert n_kv * len(plan_items(hist_pages, pps, res)) == 224 <= SLOTS // 2
+    assert (5 + ITEM_OVERHEAD_PAGES) * ALONE_FACTOR < 3 + ITEM_OVERHEAD_PAGES < 4 + ITEM_OVERHEAD_PAGES
 
 
 def test_ragged_batch_avoids_the_second_round():
@@ -92,7 +105,8 @@ def test_chosen_size_is_best_of_the_scan_by_simulation():
 
 
 def test_edge_cases(monkeypatch):
-    assert choose_pages_per_split([0], 1, RES) == 1
+    assert choose_pages_per_split([0], 1, RES) >= 1  # a sequence without pages is one item at any size
+    assert len(plan_items([0], choose_pages_per_split([0], 1, RES))) == 1
     assert choose_pages_per_split([0, 0, 3], 2, RES) >= 1
     assert choose_pages_per_split([512], 8, RES) == one_round_size([512], 8)
     monkeypatch.setenv("LOGITFILL_AMD_PAGES_PER_SPLIT", "7")
