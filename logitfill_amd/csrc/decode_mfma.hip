@@ -172,25 +172,23 @@ struct MfmaParams {
     int n_rt;      // row tiles per kv head: ceil(p.g / 8)
 };
 
-// Tier-local rank of position ``pos`` (0..7) of local block ``lb``.  Register r of a
-// block (positions 2r, 2r+1) holds the code pair the unpack helpers below produce.
-__device__ __forceinline__ int block_slot(int tier, int lb, int pos) {
-    const int r = pos >> 1, odd = pos & 1;
-    if (tier == 0) {  // word 4*(lb/8) + lb%4, half (lb/4)%2: codes (4h + r, 4h + r + 8)
-        const int word = 4 * (lb >> 3) + (lb & 3), half = (lb >> 2) & 1;
-        return 16 * word + 4 * half + r + 8 * odd;
-    }
-    if (tier == 1) return 8 * lb + r + 4 * odd;                          // int4 word lb: codes (r, r + 4)
-    if (tier == 2) return 4 * (2 * lb + (r >> 1)) + (r & 1) + 2 * odd;  // int8 words 2lb, 2lb+1: bytes (r&1, +2)
-    return 8 * lb + pos;                                                 // fp16: natural order
+// Tier-local ranks of positions 0..7 of local block ``lb``.  Register r of a block (positions
+// 2r, 2r+1) holds the code pair the unpack helpers below produce: int2 -- word 4 (lb / 8) + lb % 4,
+// half (lb / 4) % 2: codes (4 half + r, 4 half + r + 8); int4 word lb: codes (r, r + 4); int8 words
+// 2 lb, 2 lb + 1: bytes (r & 1, + 2); fp16: natural order.  Computed for a per-lane tier without
+// branches: a base per tier plus the position's offset, packed as 4-bit fields.
+__device__ __forceinline__ void block_slots(int tier, int lb, int (&slot)[8]) {
+    const int base = tier == 0 ? 16 * (4 * (lb >> 3) + (lb & 3)) + 4 * ((lb >> 2) & 1) : 8 * lb;
+    const uint32_t offs = tier == 0 ? 0xB3A29180u : tier == 1 ? 0x73625140u : tier == 2 ? 0x75643120u : 0x76543210u;
+#pragma unroll
+    for (int pos = 0; pos < 8; ++pos) slot[pos] = base + static_cast<int>((offs >> (4 * pos)) & 15u);
 }
 
-// Is local block ``lb`` of ``tier`` backed by stored words?
+// Is local block ``lb`` of ``tier`` backed by stored words?  (Selects, no branches.)
 __device__ __forceinline__ bool block_live(const lf_packed_layer& L, int tier, int lb) {
-    if (tier == 0) return 4 * (lb >> 3) + (lb & 3) < L.k_words[0];
-    if (tier == 1) return lb < L.k_words[1];
-    if (tier == 2) return 2 * lb < L.k_words[2];
-    return 8 * lb < L.k_width[3];
+    const int v = tier == 0 ? 4 * (lb >> 3) + (lb & 3) : tier == 1 ? lb : tier == 2 ? 2 * lb : 8 * lb;
+    const int lim = tier == 0 ? L.k_words[0] : tier == 1 ? L.k_words[1] : tier == 2 ? L.k_words[2] : L.k_width[3];
+    return v < lim;
 }
 
 // int2, half H of word w: registers r = (code 4H+r, code 4H+r+8); even r: bits to mantissa
@@ -980,11 +978,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const int width = sel4(L.k_width, tier);
     int count = 0;
     int craw[8];
+    int slot[8];
+    block_slots(tier, lb, slot);
     if (live) {
         const int32_t* tix = sel4(L.tier_index, tier) + h * width;
         count = sel4(L.tier_count, tier)[h];
 #pragma unroll
-        for (int pos = 0; pos < 8; ++pos) craw[pos] = tix[min(block_slot(tier, lb, pos), width - 1)];
+        for (int pos = 0; pos < 8; ++pos) craw[pos] = tix[min(slot[pos], width - 1)];
     }
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1057,7 +1057,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             *reinterpret_cast<float4*>(reinterpret_cast<float*>(ck) + qn * kD + qc0) = q4;
             int chan[8];
 #pragma unroll
-            for (int pos = 0; pos < 8; ++pos) chan[pos] = live && block_slot(tier, lb, pos) < count ? craw[pos] : -1;
+            for (int pos = 0; pos < 8; ++pos) chan[pos] = live && slot[pos] < count ? craw[pos] : -1;
             __syncthreads();  // qlin complete
             const float* qlin = reinterpret_cast<const float*>(ck);
             float qv[2][8];
@@ -1065,7 +1065,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             for (int r = 0; r < 2; ++r) {
                 const int n = n0 + r;
 #pragma unroll
-                for (int pos = 0; pos < 8; ++pos) qv[r][pos] = chan[pos] >= 0 && n < g ? qlin[n * kD + chan[pos]] : 0.f;
+                for (int pos = 0; pos < 8; ++pos) {
+                    // read unconditionally (channel 0 for a padding slot), then select: no branch
+                    const float x = qlin[n * kD + max(chan[pos], 0)];
+                    qv[r][pos] = chan[pos] >= 0 && n < g ? x : 0.f;
+                }
             }
             if (own) {
                 _Float16* qs16 = reinterpret_cast<_Float16*>(ck + kCkQs);
