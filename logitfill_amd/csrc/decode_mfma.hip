@@ -944,8 +944,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const int n_rt = mp.n_rt;
     int item, h, rt = 0;
     if (n_rt == 1) {
-        item = blockIdx.x / n_kv;
-        h = blockIdx.x - item * n_kv;
+        // grid (n_kv, items): the linear id item * n_kv + h without a division (a plan of more
+        // than 65535 items comes as a 1-D grid of item * n_kv + h)
+        if (gridDim.x == static_cast<unsigned>(n_kv)) {
+            item = blockIdx.y;
+            h = blockIdx.x;
+        } else {
+            item = blockIdx.x / n_kv;
+            h = blockIdx.x - item * n_kv;
+        }
     } else {
         const int x8 = static_cast<int>(blockIdx.x >> 3);
         const int grp = x8 / n_rt;
@@ -1581,7 +1588,10 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
     *handled = true;
     const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&decode_mfma_kernel), mp.y.lds_bytes);
     if (rc != LF_OK) return rc;
-    hipLaunchKernelGGL(decode_mfma_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), mp.y.lds_bytes, stream, mp);
+    const dim3 grid = mp.n_rt == 1 && p.A.n_work <= 65535
+                          ? dim3(static_cast<unsigned>(p.L.n_kv), static_cast<unsigned>(p.A.n_work))
+                          : dim3(static_cast<unsigned>(blocks));
+    hipLaunchKernelGGL(decode_mfma_kernel, grid, dim3(kThreads), mp.y.lds_bytes, stream, mp);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);
     return launch_decode_reduce(p, stream);

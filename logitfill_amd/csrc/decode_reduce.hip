@@ -21,9 +21,8 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
     __shared__ float red[8];
     const int D = p.L.head_dim;
     const int g = p.g;
-    const int i = blockIdx.x % g;
-    const int h = (blockIdx.x / g) % p.L.n_kv;
-    const int b = blockIdx.x / (g * p.L.n_kv);
+    // grid (g, n_kv, batch): no divisions
+    const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int first = p.dense_splits ? b * p.dense_splits : p.A.seq_work[2 * b];
     const int count = p.dense_splits ? p.dense_splits : p.A.seq_work[2 * b + 1];
     const int tid = threadIdx.x;
@@ -107,7 +106,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
 
 int launch_decode_reduce(const DecodeParams& p, hipStream_t stream) {
     const int threads = p.L.head_dim < 64 ? 64 : p.L.head_dim > 256 ? 256 : p.L.head_dim;
-    hipLaunchKernelGGL(decode_reduce_kernel, dim3(p.L.batch * p.L.n_kv * p.g), dim3(threads), 0, stream, p);
+    hipLaunchKernelGGL(decode_reduce_kernel, dim3(p.g, p.L.n_kv, p.L.batch), dim3(threads), 0, stream, p);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? LF_OK : static_cast<int>(err);
 }
