@@ -252,6 +252,16 @@ class _LayerStore:
         is packed in place by the page-compress kernel (``cache.py:54-62`` then
         ``_flush`` :64-81).
         """
+        shape = key.shape
+        # one token for every sequence into residual pages that stay below full: the decode
+        # step's commit, checked and enqueued with as little host work as possible
+        if (lengths is None and len(shape) == 4 and shape[2] == 1 and shape == value.shape
+                and shape[0] == self.batch and shape[1] == self.n_kv and shape[3] == self.head_dim
+                and self._tail_k is not None and not self._pending and max(self.tail_lens) + 1 < self.page_size
+                and key.dtype == value.dtype and key.is_cuda and value.is_cuda
+                and key.is_contiguous() and value.is_contiguous()):
+            self._append_one(key, value)
+            return
         if key.shape != value.shape:
             raise ValueError("Key and Value pages do not match")
         B, H, T, D = (int(x) for x in key.shape)
@@ -260,11 +270,6 @@ class _LayerStore:
         if not key.is_cuda or not value.is_cuda:
             raise RuntimeError("logitfill_amd keeps the packed cache on a ROCm device (there is no CPU path)")
         P = self.page_size
-        if (T == 1 and lengths is None and self._tail_k is not None and not self._pending
-                and max(self.tail_lens) + 1 < P and key.dtype == value.dtype
-                and key.is_contiguous() and value.is_contiguous()):
-            self._append_one(key, value)
-            return
         lens = [T] * B if lengths is None else [int(x) for x in lengths]
         if len(lens) != B or min(lens) < 0 or max(lens) > T:
             raise ValueError("lengths must give 0 <= length <= T for every sequence")
@@ -345,10 +350,17 @@ class _LayerStore:
         the host copy of the lengths advances in step."""
         tail_len = self.tail_len_device()
         tk, tv = self._tail_k, self._tail_v
-        st = _native.load().lf_append_token(
-            tk.data_ptr(), tv.data_ptr(), _native.dtype_code(tk.dtype), int(tk.shape[2]), tail_len.data_ptr(),
-            key.data_ptr(), value.data_ptr(), _native.dtype_code(key.dtype), self.batch, self.n_kv, self.head_dim,
-            _native.current_stream_ptr(self.device))
+        # the arguments fixed while the tail buffers and the new rows' dtype stay, kept per layer
+        key_static = (tk.data_ptr(), tv.data_ptr(), tail_len.data_ptr(), key.dtype)
+        cached = self.__dict__.get("_lf_append_static")
+        if cached is None or cached[0] != key_static:
+            cached = (key_static, (tk.data_ptr(), tv.data_ptr(), _native.dtype_code(tk.dtype), int(tk.shape[2]),
+                                   tail_len.data_ptr()), _native.dtype_code(key.dtype))
+            self.__dict__["_lf_append_static"] = cached
+        _, (ptk, ptv, tdt, cap, ptl), ndt = cached
+        st = _native.load().lf_append_token(ptk, ptv, tdt, cap, ptl, key.data_ptr(), value.data_ptr(), ndt,
+                                            self.batch, self.n_kv, self.head_dim,
+                                            _native.current_stream_ptr(self.device))
         _native.check(st, "lf_append_token")
         self.tail_lens = [t + 1 for t in self.tail_lens]
 
@@ -539,7 +551,9 @@ class PackedKVManager:
         if key.shape[0] != self.batch_size:
             raise NotImplementedError(
                 f"this manager holds {self.batch_size} sequence(s); got a batch of {key.shape[0]}")
-        self.layers[layer_idx].append_batch(key.detach(), value.detach(), lengths)
+        if key.requires_grad or value.requires_grad:
+            key, value = key.detach(), value.detach()
+        self.layers[layer_idx].append_batch(key, value, lengths)
         if layer_idx == len(self.layers) - 1:
             self.seq_len = self.layers[layer_idx].length
 

@@ -401,18 +401,16 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
 
 def _kernel_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
                       value_new: torch.Tensor, scaling: float) -> torch.Tensor:
-    """Decode through the HIP kernels (replaces ``reference.py:59-109``)."""
+    """Decode through the HIP kernels (replaces ``reference.py:59-109``).  The tensors go to
+    ``decode_into`` in their ``[B, heads, q_len, D]`` form (for one token the same memory as
+    ``[B, heads, D]``), copied only when not contiguous: this runs once per layer and step."""
     B, n_q, q_len, D = query.shape
-    if q_len == 1:
-        q = query.reshape(B, n_q, D).contiguous()
-        kn = key_new.reshape(B, manager.n_kv, D).contiguous()
-        vn = value_new.reshape(B, manager.n_kv, D).contiguous()
-        out = torch.empty(B, n_q, D, dtype=query.dtype, device=query.device)
-    else:
-        q, kn, vn = query.contiguous(), key_new.contiguous(), value_new.contiguous()
-        out = torch.empty(B, n_q, q_len, D, dtype=query.dtype, device=query.device)
+    q = query if query.is_contiguous() else query.contiguous()
+    kn = key_new if key_new.is_contiguous() else key_new.contiguous()
+    vn = value_new if value_new.is_contiguous() else value_new.contiguous()
+    out = torch.empty(B, n_q, q_len, D, dtype=query.dtype, device=query.device)
     decode_into(manager, layer_idx, q, kn, vn, scaling, out)
-    return out.view(B, n_q, q_len, D)
+    return out
 
 
 # Query rows per workgroup of the matrix-core decode kernel: rows beyond it ((n_q / n_kv) * q_len
