@@ -312,13 +312,18 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     layer = manager.layers[layer_idx]
     layer.flush()  # deferred residual pages of this layer, if any
     B, D = layer.batch, layer.head_dim
-    q_len = int(query.shape[2]) if query.dim() == 4 else 1
-    tok = (q_len,) if query.dim() == 4 else ()
-    _expect(query, (B, manager.n_q, *tok, D), "query")
-    _expect(out, (B, manager.n_q, *tok, D), "out")
+    qshape = query.shape
+    q_len = int(qshape[2]) if len(qshape) == 4 else 1
+    tok = (q_len,) if len(qshape) == 4 else ()
+    want_q = (B, manager.n_q, *tok, D)
+    if qshape != want_q or out.shape != want_q:
+        _expect(query, want_q, "query")
+        _expect(out, want_q, "out")
     if key_new is not None:
-        _expect(key_new, (B, manager.n_kv, *tok, D), "key_new")
-        _expect(value_new, (B, manager.n_kv, *tok, D), "value_new")
+        want_kv = (B, manager.n_kv, *tok, D)
+        if key_new.shape != want_kv or value_new.shape != want_kv:
+            _expect(key_new, want_kv, "key_new")
+            _expect(value_new, want_kv, "value_new")
     kernel = kernel_choice() if kernel is None else kernel
     P = layer.page_size
     hist_pages = tuple(h // P for h in layer.hist_lens)
@@ -346,18 +351,23 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
         plan = DecodePlan(list(hist_pages), layer.n_kv, pages_per_split, layer.device, res_pages)
         layer.decode_plan = plan
     lib = _native.load()
-    nbytes = lib.lf_decode_workspace_bytes(manager.n_q * q_len, layer.head_dim, plan.n_work)
-    ws = None if noalloc else manager.workspace(nbytes)
+    wkey = (manager.n_q * q_len, layer.head_dim)
+    ws_need = plan.__dict__.get("_lf_ws_bytes")
+    if ws_need is None or ws_need[0] != wkey:
+        ws_need = (wkey, lib.lf_decode_workspace_bytes(wkey[0], wkey[1], plan.n_work))
+        plan.__dict__["_lf_ws_bytes"] = ws_need
+    ws = None if noalloc else manager.workspace(ws_need[1])
     tail_k, tail_v = layer.tail_buffers()
     if key_new is not None and value_new.dtype != key_new.dtype:
         raise TypeError("key_new and value_new must share a dtype")
     tail_len = layer.tail_len_device()
     # Every field but the four per-call tensors is fixed while the plan, the buffers and the
-    # call's settings stay the same: the argument block is kept on the layer and reused.
-    static_key = (plan, None if ws is None else (ws.data_ptr(), ws.numel()),
-                  None if tail_k is None else (tail_k.data_ptr(), tail_v.data_ptr(), tail_k.dtype, int(tail_k.shape[2])),
-                  tail_len.data_ptr(), query.dtype, out.dtype, None if key_new is None else key_new.dtype,
-                  manager.n_q, float(scaling), kernel, q_len)
+    # call's settings stay the same: the argument block is kept on the layer and reused.  The
+    # buffers are compared by identity (each one's pointer is fixed for its lifetime; the cache
+    # entry holds them, so an id cannot be reused while it is kept).
+    held = (plan, ws, tail_k, tail_v, tail_len)
+    static_key = (id(plan), id(ws), id(tail_k), id(tail_v), id(tail_len), query.dtype, out.dtype,
+                  None if key_new is None else key_new.dtype, manager.n_q, float(scaling), kernel, q_len)
     cached_args = layer.__dict__.get("_lf_decode_args")
     if cached_args is not None and cached_args[0] == static_key:
         a = cached_args[1]
@@ -385,7 +395,7 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
         a.workspace_bytes = 0 if ws is None else ws.numel()
         a.kernel = kernel
         a.q_len = q_len
-        layer.__dict__["_lf_decode_args"] = (static_key, a)
+        layer.__dict__["_lf_decode_args"] = (static_key, a, held)
     a.query = query.data_ptr()
     a.out = out.data_ptr()
     a.k_new = 0 if key_new is None else key_new.data_ptr()
