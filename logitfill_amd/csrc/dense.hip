@@ -13,8 +13,9 @@
 //           bf16 hi (columns 0..7) and lo (columns 8..15), so one DPP add recombines them.
 //   values  O = P' . V with P' = 2^(s - m) split hi (rows 0..7) / lo (rows 8..15): the score
 //           accumulator layout is the A-operand layout, so probabilities feed the second MFMA in
-//           place.  V pages arrive by LDS-DMA one page ahead (row-major); each lane gathers its 8
-//           tokens of one channel with 16-bit LDS reads.
+//           place.  V pages arrive by LDS-DMA one page ahead (row-major, 16-byte chunks XOR-
+//           swizzled by row); each lane takes its 8 tokens of one channel with two transpose
+//           reads (ds_read_b64_tr_b16).
 //
 // Partials (o, m, l) per (split, head) go to the workspace; decode_reduce_kernel merges them.
 #include "decode_common.hpp"
@@ -122,13 +123,18 @@ __global__ __launch_bounds__(kThreads, 2) void dense_decode_kernel(DenseParams p
 #pragma unroll
     for (int t = 0; t < 2; ++t) kp[t] = p.k + kvbase + 32 * kb;
     const uint32_t ring = lds_addr(vring);
-    // V DMA instruction i of wave w: block j = 4 i + w = tokens 4 j .. 4 j + 3, 16 chunks each
+    // V DMA instruction i of wave w: block j = 4 i + w = tokens 4 j .. 4 j + 3, 16 chunks each.
+    // Row r's 16-byte chunk k lands at chunk position k ^ 2 (r % 8): the transpose reads of the
+    // value product (rows r0 .. r0 + 7 of one column pair per half wave) then hit 64 distinct
+    // banks.
     auto v_dma = [&](int page, int slot) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int j = 4 * i + wave;
-            const int tok = min(t0 + page * kPageTok + 4 * j + (lane >> 4), t1 - 1);
-            dma16(p.v + kvbase + static_cast<int64_t>(tok) * p.st + 8 * (lane & 15), ring + slot * kVTile + 1024 * j);
+            const int row = 4 * j + (lane >> 4);
+            const int tok = min(t0 + page * kPageTok + row, t1 - 1);
+            const int chunk = (lane & 15) ^ (2 * (row & 7));
+            dma16(p.v + kvbase + static_cast<int64_t>(tok) * p.st + 8 * chunk, ring + slot * kVTile + 1024 * j);
         }
     };
     auto k_load = [&](int page, uint4 (&kr)[2][4]) {
@@ -154,8 +160,13 @@ __global__ __launch_bounds__(kThreads, 2) void dense_decode_kernel(DenseParams p
         k_load(0, kcur);
     }
     for (int page = 0; page < pages; ++page) {
-        // V(page) and K(page) landed; every wave is done with page - 1 (its V slot is free)
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // V(page) and K(page) landed; every wave is done with page - 1 (its V slot is free).  The
+        // wait is the builtin, not inline asm, so the compiler knows K(page) is in registers and
+        // adds no wait of its own before the score products (which, with the V DMA of page + 1
+        // ahead of it in the counter, would hold the scores until that page had landed too).
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) expcnt(7) lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
         if (page + 1 < pages) {
             v_dma(page + 1, (page + 1) & 1);
             k_load(page + 1, knext);
@@ -224,17 +235,23 @@ __global__ __launch_bounds__(kThreads, 2) void dense_decode_kernel(DenseParams p
         }
         m_run = m_new;
         l_run += psum;
-        // ---- values: B operand lane (n16, kb) = V[token of k][16 nt + n16] from the LDS page ----
-        const uint16_t* vt = reinterpret_cast<const uint16_t*>(vring + (page & 1) * kVTile);
-        const int r0 = 32 * wave + 4 * kb;
+        // ---- values: B operand lane (n16, kb) = V[token of k][16 nt + n16] from the LDS page,
+        // tokens r0 .. r0 + 3 and r0 + 16 .. r0 + 19 (r0 = 32 wave + 4 kb): two transpose reads
+        // (ds_read_b64_tr_b16: lane i of a 16-lane group passes row i / 4, columns 4 (i % 4) ..
+        // + 3 of a 4 x 16 block and receives column i) ----
+        unsigned char* vt = vring + (page & 1) * kVTile;
+        const int rr = 32 * wave + 4 * kb + (n16 >> 2);
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
-            const int c = 16 * nt + n16;
-            uint16_t e[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) e[j] = vt[(r0 + (j & 3) + 16 * (j >> 2)) * kD + c];
-            const uint4 bu = {e[0] | (static_cast<uint32_t>(e[1]) << 16), e[2] | (static_cast<uint32_t>(e[3]) << 16),
-                              e[4] | (static_cast<uint32_t>(e[5]) << 16), e[6] | (static_cast<uint32_t>(e[7]) << 16)};
+            const int ch = 2 * nt + ((n16 >> 1) & 1);
+            const int ra = rr, rb = rr + 16;
+            typedef short v4i16 __attribute__((ext_vector_type(4)));
+            const v4i16 ta = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(
+                (lds_void*)(vt + ra * (kD * 2) + 16 * (ch ^ (2 * (ra & 7))) + 8 * (n16 & 1))));
+            const v4i16 tb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(
+                (lds_void*)(vt + rb * (kD * 2) + 16 * (ch ^ (2 * (rb & 7))) + 8 * (n16 & 1))));
+            const uint2 ua = __builtin_bit_cast(uint2, ta), ub = __builtin_bit_cast(uint2, tb);
+            const uint4 bu = {ua.x, ua.y, ub.x, ub.y};
             float4v o4 = {O[nt][0], O[nt][1], O[nt][2], O[nt][3]};
             o4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap, __builtin_bit_cast(bf16x8, bu), o4, 0, 0, 0);
             O[nt][0] = o4[0]; O[nt][1] = o4[1]; O[nt][2] = o4[2]; O[nt][3] = o4[3];

@@ -140,7 +140,8 @@ def test_token_by_token_commit_matches_bulk(gpu):
 
 def test_batched_ragged_commits_and_growth(gpu):
     """Batch of 3 with ragged prefills (130, 7, 511 tokens), then 200 one-token commits;
-    capacity starts at one page and grows; every sequence matches its own oracle store."""
+    capacity starts at one page and grows; every sequence matches its own oracle store, and
+    the page-major Key scale/min copy matches the reference arrays after the growth."""
     n_kv, D = 2, 128
     lens = [130, 7, 511]
     steps = 200
@@ -163,6 +164,7 @@ def test_batched_ragged_commits_and_growth(gpu):
         n = lens[b] + steps
         store = oracle_store(levels, f32(data[b].key[0, :, :n]), f32(data[b].value[0, :, :n]))
         assert_history_equal(layer, b, store)
+        _check_page_copy(layer, b)  # the page-major scale/min copy survives every growth
     assert layer.capacity >= 640
 
 
