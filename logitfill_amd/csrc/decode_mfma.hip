@@ -115,15 +115,17 @@ __device__ __forceinline__ void dma_barrier(int n) {
 // in flight (__syncthreads would also wait for it).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// a[t] for a run-time t in 0..3 (or 0..2) through selects: a dynamic index into the kernel
-// argument would copy the whole argument block to scratch memory.
+// a[t] for a run-time t in 0..3 (or 0..2) of a kernel-argument array, through selects over
+// SGPR copies.  A dynamic index into the argument block would copy it to scratch memory; a plain
+// select chain with a per-lane t the compiler turns into a select of *addresses* and one vector
+// load from the argument block per lane -- a memory round trip each, in the prologue's
+// dependent chain.  The empty asm pins the four values in SGPRs (scalar loads, already
+// prefetched), so the select is four VALU ops.
 template <class T>
 __device__ __forceinline__ T sel4(const T (&a)[4], int t) {
-    return t == 0 ? a[0] : t == 1 ? a[1] : t == 2 ? a[2] : a[3];
-}
-template <class T>
-__device__ __forceinline__ T sel3(const T (&a)[3], int t) {
-    return t == 0 ? a[0] : t == 1 ? a[1] : a[2];
+    T a0 = a[0], a1 = a[1], a2 = a[2], a3 = a[3];
+    asm volatile("" : "+s"(a0), "+s"(a1), "+s"(a2), "+s"(a3));
+    return t == 0 ? a0 : t == 1 ? a1 : t == 2 ? a2 : a3;
 }
 
 // LDS-DMA: each lane's 16 bytes at ``g`` land at lds + 16 * lane.  Issued through asm so the
@@ -187,8 +189,8 @@ __device__ __forceinline__ void block_slots(int tier, int lb, int (&slot)[8]) {
 // Is local block ``lb`` of ``tier`` backed by stored words?  (Selects, no branches.)
 __device__ __forceinline__ bool block_live(const lf_packed_layer& L, int tier, int lb) {
     const int v = tier == 0 ? 4 * (lb >> 3) + (lb & 3) : tier == 1 ? lb : tier == 2 ? 2 * lb : 8 * lb;
-    const int lim = tier == 0 ? L.k_words[0] : tier == 1 ? L.k_words[1] : tier == 2 ? L.k_words[2] : L.k_width[3];
-    return v < lim;
+    const int lims[4] = {L.k_words[0], L.k_words[1], L.k_words[2], L.k_width[3]};
+    return v < sel4(lims, tier);
 }
 
 // int2, half H of word w: registers r = (code 4H+r, code 4H+r+8); even r: bits to mantissa
@@ -969,10 +971,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const int kb = lane >> 4;   // lane group
     const int row0 = 8 * rt;              // this tile's rows row0 .. row0 + g - 1 of the kv head's p.g
     const int g = min(8, p.g - row0);
-    const int b = A.work[4 * item + 0];
-    const int pbeg = A.work[4 * item + 1];
-    const int pend = A.work[4 * item + 2];
-    const int kind = A.work[4 * item + 3];
+    // The work record through the constant address space: one scalar load (the item is uniform),
+    // which skips the vector memory pipeline's longer round trip in the prologue's dependent
+    // chain.  The list is written before the launch, so the scalar cache (invalidated at
+    // dispatch) cannot hold a stale copy.
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    typedef const __attribute__((address_space(4))) i32x4 ci32x4;
+    const i32x4 rec = ((ci32x4*)A.work)[item];
+    const int b = rec[0];
+    const int pbeg = rec[1];
+    const int pend = rec[2];
+    const int kind = rec[3];
     // Tier-table entries of this thread's Key-slot block (used by items with pages, below): they
     // depend only on the kv head, so their loads go out while the work record is in flight.  Thread tid owns block gb = tid / 4 (K-step gb / 4); tier_index entries
     // are read whatever the tier count, which decides afterwards which are real slots.
@@ -988,8 +997,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     int slot[8];
     block_slots(tier, lb, slot);
     if (live) {
-        const int32_t* tix = sel4(L.tier_index, tier) + h * width;
-        count = sel4(L.tier_count, tier)[h];
+        // global-memory pointers again (the SGPR pin of sel4 hides where they came from; a flat
+        // load would also count against lgkmcnt, which every LDS wait below waits for)
+        typedef const __attribute__((address_space(1))) int32_t gint;
+        const gint* tix = (const gint*)sel4(L.tier_index, tier) + h * width;
+        count = ((const gint*)sel4(L.tier_count, tier))[h];
 #pragma unroll
         for (int pos = 0; pos < 8; ++pos) craw[pos] = tix[min(slot[pos], width - 1)];
     }
@@ -1067,17 +1079,23 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
             for (int pos = 0; pos < 8; ++pos) chan[pos] = live && slot[pos] < count ? craw[pos] : -1;
             __syncthreads();  // qlin complete
             const float* qlin = reinterpret_cast<const float*>(ck);
+            // All 16 reads go out unconditionally (channel 0 for a padding slot) and are waited
+            // for once: the empty asm takes every value, so the compiler cannot sink a read into
+            // the branch of its select (it did: 16 reads, each behind an exec branch and its own
+            // LDS wait).
             float qv[2][8];
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const int n = n0 + r;
+            for (int r = 0; r < 2; ++r)
 #pragma unroll
-                for (int pos = 0; pos < 8; ++pos) {
-                    // read unconditionally (channel 0 for a padding slot), then select: no branch
-                    const float x = qlin[n * kD + max(chan[pos], 0)];
-                    qv[r][pos] = chan[pos] >= 0 && n < g ? x : 0.f;
-                }
-            }
+                for (int pos = 0; pos < 8; ++pos) qv[r][pos] = qlin[(n0 + r) * kD + max(chan[pos], 0)];
+            asm volatile("" : "+v"(qv[0][0]), "+v"(qv[0][1]), "+v"(qv[0][2]), "+v"(qv[0][3]), "+v"(qv[0][4]),
+                              "+v"(qv[0][5]), "+v"(qv[0][6]), "+v"(qv[0][7]), "+v"(qv[1][0]), "+v"(qv[1][1]),
+                              "+v"(qv[1][2]), "+v"(qv[1][3]), "+v"(qv[1][4]), "+v"(qv[1][5]), "+v"(qv[1][6]),
+                              "+v"(qv[1][7]));
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int pos = 0; pos < 8; ++pos) qv[r][pos] = chan[pos] >= 0 && n0 + r < g ? qv[r][pos] : 0.f;
             if (own) {
                 _Float16* qs16 = reinterpret_cast<_Float16*>(ck + kCkQs);
 #pragma unroll
