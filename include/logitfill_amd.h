@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 7
+#define LF_ABI_VERSION 8
 
 /* Element types of query / residual / output tensors. */
 enum lf_dtype { LF_BF16 = 0, LF_FP16 = 1, LF_FP32 = 2 };
@@ -199,7 +199,18 @@ typedef struct lf_decode_args {
                                                  [batch][n_q][q_len][head_dim], k_new/v_new
                                                  [batch][n_kv][q_len][head_dim], and the
                                                  workspace is sized for n_q * q_len rows  */
+    const int32_t* work_host;                 /* optional (NULL): host copies of work and  */
+    const int32_t* seq_work_host;             /* seq_work, the same values; a plan of at
+                                                 most LF_INLINE_WORK items (LF_INLINE_SEQ
+                                                 sequences) then travels in the kernels'
+                                                 argument blocks, which saves each workgroup
+                                                 a dependent read of device memory; read
+                                                 during the call only                    */
 } lf_decode_args;
+
+/* Plan sizes that travel inline in the kernel arguments when the host copies are given. */
+#define LF_INLINE_WORK 160
+#define LF_INLINE_SEQ 128
 
 /* Workspace bytes for lf_decode_attention with ``n_work`` items: the fp32
  * partials [n_work][n_q][head_dim + 2] of the split-K items. */

@@ -86,6 +86,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", c_void_p), ("workspace_bytes", c_int64),
         ("kernel", c_int32),
         ("q_len", c_int32),
+        ("work_host", c_void_p), ("seq_work_host", c_void_p),
     ]
 
 
@@ -115,7 +116,7 @@ _SIGNATURES = {
     "lf_noalloc_scratch_bytes": (c_int64, []),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 _LIB = None
 
 

@@ -61,33 +61,66 @@ __device__ __forceinline__ void load8_as_f32(const void* base, int64_t idx, int 
 // cached each of those waits is a cache hit instead of a memory round trip.  The loaded values are
 // discarded (s40..s55 are clobbered); the asm declares no memory clobber, so loads of read-only
 // data may still be scalar loads.
-#define LF_ARG_LINE(off) "s_load_dwordx16 s[40:55], %0, " #off "\n\t"
+#define LF_ARG_LINE(off) "s_load_dwordx16 s[40:55], %[kp], " #off "\n\t"
 #define LF_ARG_LINES6 LF_ARG_LINE(0) LF_ARG_LINE(64) LF_ARG_LINE(128) LF_ARG_LINE(192) LF_ARG_LINE(256) LF_ARG_LINE(320)
 #define LF_ARG_CLOBBERS "s40", "s41", "s42", "s43", "s44", "s45", "s46", "s47", "s48", "s49", "s50", "s51", \
     "s52", "s53", "s54", "s55"
+#define LF_ARG_LINES(lines)                                                                          \
+    LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) LF_ARG_LINE(512) LF_ARG_LINE(576)
+// One asm statement per line count (6..10), with ``EXTRA`` loads before the single wait.
+#define LF_PREFETCH(EXTRA, ...)                                                                      \
+    if constexpr (lines == 6)                                                                        \
+        asm volatile(LF_ARG_LINES6 EXTRA "s_waitcnt lgkmcnt(0)" __VA_ARGS__ : LF_ARG_CLOBBERS);         \
+    else if constexpr (lines == 7)                                                                   \
+        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) EXTRA "s_waitcnt lgkmcnt(0)" __VA_ARGS__ : LF_ARG_CLOBBERS); \
+    else if constexpr (lines == 8)                                                                   \
+        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) EXTRA "s_waitcnt lgkmcnt(0)"       \
+                     __VA_ARGS__ : LF_ARG_CLOBBERS);                                                 \
+    else if constexpr (lines == 9)                                                                   \
+        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) LF_ARG_LINE(512) EXTRA            \
+                     "s_waitcnt lgkmcnt(0)" __VA_ARGS__ : LF_ARG_CLOBBERS);                          \
+    else                                                                                             \
+        asm volatile(LF_ARG_LINES(10) EXTRA "s_waitcnt lgkmcnt(0)" __VA_ARGS__ : LF_ARG_CLOBBERS);
 template <int Bytes>
 __device__ __forceinline__ void prefetch_args() {
     constexpr int lines = (Bytes + 63) / 64;
     static_assert(lines >= 6 && lines <= 10, "prefetch_args: add the line count of this argument block");
     const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
-    if constexpr (lines == 6)
-        asm volatile(LF_ARG_LINES6 "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
-    else if constexpr (lines == 7)
-        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
-    else if constexpr (lines == 8)
-        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
-    else if constexpr (lines == 9)
-        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) LF_ARG_LINE(512) "s_waitcnt lgkmcnt(0)" ::"s"(kp)
-                     : LF_ARG_CLOBBERS);
-    else
-        asm volatile(LF_ARG_LINES6 LF_ARG_LINE(384) LF_ARG_LINE(448) LF_ARG_LINE(512) LF_ARG_LINE(576)
-                     "s_waitcnt lgkmcnt(0)" ::"s"(kp) : LF_ARG_CLOBBERS);
+    LF_PREFETCH("", ::[kp] "s"(kp))
 }
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+// prefetch_args of the first ``Bytes`` bytes plus one record of the argument block at byte offset
+// ``off`` (uniform), loaded in the same round and returned: a plan entry that travels in the
+// kernel arguments arrives with them instead of one dependent memory round trip later.
+template <int Bytes>
+__device__ __forceinline__ i32x4 prefetch_args_rec4(uint32_t off) {
+    constexpr int lines = (Bytes + 63) / 64;
+    static_assert(lines >= 6 && lines <= 10, "prefetch_args: add the line count of this argument block");
+    const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+    i32x4 rec;
+    LF_PREFETCH("s_load_dwordx4 %[rec], %[kp], %[off]\n\t", : [rec] "=s"(rec) : [kp] "s"(kp), [off] "s"(off))
+    return rec;
+}
+template <int Bytes>
+__device__ __forceinline__ i32x2 prefetch_args_rec2(uint32_t off) {
+    constexpr int lines = (Bytes + 63) / 64;
+    static_assert(lines >= 6 && lines <= 10, "prefetch_args: add the line count of this argument block");
+    const auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+    i32x2 rec;
+    LF_PREFETCH("s_load_dwordx2 %[rec], %[kp], %[off]\n\t", : [rec] "=s"(rec) : [kp] "s"(kp), [off] "s"(off))
+    return rec;
+}
+#undef LF_PREFETCH
+#undef LF_ARG_LINES
 #undef LF_ARG_CLOBBERS
 #undef LF_ARG_LINES6
 #undef LF_ARG_LINE
 
-// Merge the partials of every sequence into ``out`` (enqueued after a decode kernel).
+// Merge the partials of every sequence into ``out`` (enqueued after a decode kernel).  With the
+// host copy of seq_work and at most LF_INLINE_SEQ sequences, the (first, count) pairs go into
+// the reduce kernel's arguments.
 int launch_decode_reduce(const DecodeParams& p, hipStream_t stream);
 
 }  // namespace lf

@@ -39,6 +39,8 @@
 // each lane's 8 codes for one 16-channel tile are two LDS dwords.
 #include <type_traits>
 
+#include <cstring>
+
 #include "decode_common.hpp"
 
 namespace lf {
@@ -172,7 +174,11 @@ struct MfmaParams {
     UnpackBits k;
     int res_mfma;  // residual pass: 0 VALU, 1 bf16 matrix cores, 2 fp16 matrix cores (residual_mfma)
     int n_rt;      // row tiles per kv head: ceil(p.g / 8)
+    int inline_work;  // 1: work_inline holds the plan (2-D grid, n_work <= LF_INLINE_WORK)
+    int pad_[3];
+    int32_t work_inline[4 * LF_INLINE_WORK];  // the work list, when inline_work
 };
+static_assert(sizeof(MfmaParams) <= 4096, "kernel arguments are limited to 4 KB");
 
 // Tier-local ranks of positions 0..7 of local block ``lb``.  Register r of a block (positions
 // 2r, 2r+1) holds the code pair the unpack helpers below produce: int2 -- word 4 (lb / 8) + lb % 4,
@@ -929,7 +935,11 @@ __device__ __forceinline__ void merge_partials(const DecodeParams& p, int item, 
 }
 
 __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp) {
-    prefetch_args<sizeof(MfmaParams)>();
+    // The argument block before the inline plan, and this workgroup's inline work record (the
+    // launch uses a 2-D grid (n_kv, items) whenever the record is inline, so the item is
+    // blockIdx.y; otherwise the slot read is ignored).
+    const i32x4 rec_arg = prefetch_args_rec4<offsetof(MfmaParams, work_inline)>(
+        static_cast<uint32_t>(offsetof(MfmaParams, work_inline)) + 16u * min(blockIdx.y, LF_INLINE_WORK - 1u));
     const DecodeParams& p = mp.p;
     const MfmaLayout& y = mp.y;
     const UnpackBits kv = vgpr_bits(mp.k);
@@ -975,9 +985,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     // which skips the vector memory pipeline's longer round trip in the prologue's dependent
     // chain.  The list is written before the launch, so the scalar cache (invalidated at
     // dispatch) cannot hold a stale copy.
-    typedef int i32x4 __attribute__((ext_vector_type(4)));
     typedef const __attribute__((address_space(4))) i32x4 ci32x4;
-    const i32x4 rec = ((ci32x4*)A.work)[item];
+    const i32x4 rec = mp.inline_work ? rec_arg : ((ci32x4*)A.work)[item];
     const int b = rec[0];
     const int pbeg = rec[1];
     const int pend = rec[2];
@@ -1606,9 +1615,12 @@ int launch_decode_mfma(const DecodeParams& p, hipStream_t stream, bool* handled)
     *handled = true;
     const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&decode_mfma_kernel), mp.y.lds_bytes);
     if (rc != LF_OK) return rc;
-    const dim3 grid = mp.n_rt == 1 && p.A.n_work <= 65535
-                          ? dim3(static_cast<unsigned>(p.L.n_kv), static_cast<unsigned>(p.A.n_work))
-                          : dim3(static_cast<unsigned>(blocks));
+    const bool grid2d = mp.n_rt == 1 && p.A.n_work <= 65535;
+    const dim3 grid = grid2d ? dim3(static_cast<unsigned>(p.L.n_kv), static_cast<unsigned>(p.A.n_work))
+                             : dim3(static_cast<unsigned>(blocks));
+    // the plan inline in the arguments (its slot is blockIdx.y, so only with the 2-D grid)
+    mp.inline_work = grid2d && p.A.work_host != nullptr && p.A.n_work <= LF_INLINE_WORK;
+    if (mp.inline_work) std::memcpy(mp.work_inline, p.A.work_host, sizeof(int32_t) * 4 * p.A.n_work);
     hipLaunchKernelGGL(decode_mfma_kernel, grid, dim3(kThreads), mp.y.lds_bytes, stream, mp);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return static_cast<int>(err);

@@ -6,6 +6,9 @@
 //     out[b][h*g + i][c] = sum_k w_k o_k[c] / sum_k w_k l_k,
 // the merge of reference.py:44-56's single softmax over all tokens.  Items with
 // no tokens carry m = -inf and weigh nothing.
+#include <cstddef>
+#include <cstring>
+
 #include "decode_common.hpp"
 
 namespace lf {
@@ -15,16 +18,27 @@ constexpr int kReduceLds = 2048;  // items whose weights are kept in LDS (more: 
 constexpr int kFastItems = 32;    // up to this many items: one round of loads per thread, no LDS
                                   // (at most the 64 lanes of a wave)
 
-__global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
-    prefetch_args<sizeof(DecodeParams)>();
+struct ReduceParams {
+    DecodeParams p;
+    int inline_seq;  // 1: seq_inline holds seq_work (at most LF_INLINE_SEQ sequences)
+    int pad_;
+    int32_t seq_inline[2 * LF_INLINE_SEQ];
+};
+static_assert(sizeof(ReduceParams) <= 4096, "kernel arguments are limited to 4 KB");
+
+__global__ __launch_bounds__(256) void decode_reduce_kernel(ReduceParams rp) {
+    // the argument block and this sequence's inline (first, count), in one round of loads
+    const i32x2 seq_arg = prefetch_args_rec2<offsetof(ReduceParams, seq_inline)>(
+        static_cast<uint32_t>(offsetof(ReduceParams, seq_inline)) + 8u * min(blockIdx.z, LF_INLINE_SEQ - 1u));
+    const DecodeParams& p = rp.p;
     __shared__ float w[kReduceLds];
     __shared__ float red[8];
     const int D = p.L.head_dim;
     const int g = p.g;
     // grid (g, n_kv, batch): no divisions
     const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int first = p.dense_splits ? b * p.dense_splits : p.A.seq_work[2 * b];
-    const int count = p.dense_splits ? p.dense_splits : p.A.seq_work[2 * b + 1];
+    const int first = p.dense_splits ? b * p.dense_splits : rp.inline_seq ? seq_arg[0] : p.A.seq_work[2 * b];
+    const int count = p.dense_splits ? p.dense_splits : rp.inline_seq ? seq_arg[1] : p.A.seq_work[2 * b + 1];
     const int tid = threadIdx.x;
     const int nw = blockDim.x / kWave;
 
@@ -106,7 +120,11 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeParams p) {
 
 int launch_decode_reduce(const DecodeParams& p, hipStream_t stream) {
     const int threads = p.L.head_dim < 64 ? 64 : p.L.head_dim > 256 ? 256 : p.L.head_dim;
-    hipLaunchKernelGGL(decode_reduce_kernel, dim3(p.g, p.L.n_kv, p.L.batch), dim3(threads), 0, stream, p);
+    ReduceParams rp;
+    rp.p = p;
+    rp.inline_seq = !p.dense_splits && p.A.seq_work_host != nullptr && p.L.batch <= LF_INLINE_SEQ;
+    if (rp.inline_seq) std::memcpy(rp.seq_inline, p.A.seq_work_host, sizeof(int32_t) * 2 * p.L.batch);
+    hipLaunchKernelGGL(decode_reduce_kernel, dim3(p.g, p.L.n_kv, p.L.batch), dim3(threads), 0, stream, rp);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? LF_OK : static_cast<int>(err);
 }

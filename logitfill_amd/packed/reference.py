@@ -279,6 +279,9 @@ class DecodePlan:
         self.n_work = len(work) // 4
         self.work = _native.upload(work, torch.int32, device)
         self.seq_work = _native.upload(seq, torch.int32, device)
+        # host copies: a small plan travels in the kernels' arguments (lf_decode_args.work_host)
+        self.work_host = np.ascontiguousarray(work, dtype=np.int32)
+        self.seq_work_host = np.ascontiguousarray(seq, dtype=np.int32)
         self.pages_per_split = pages_per_split
 
 
@@ -391,6 +394,8 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
         a.work = plan.work.data_ptr()
         a.n_work = plan.n_work
         a.seq_work = plan.seq_work.data_ptr()
+        a.work_host = plan.work_host.ctypes.data
+        a.seq_work_host = plan.seq_work_host.ctypes.data
         a.workspace = 0 if ws is None else ws.data_ptr()
         a.workspace_bytes = 0 if ws is None else ws.numel()
         a.kernel = kernel

@@ -115,3 +115,35 @@ def test_dispatch_order_split_matches_the_oracle(gpu, B, n_q, n_kv, pages, tail)
     res = residual_pages([tail])
     assert [seq[2 * b + 1] for b in range(B)] == [-(-(pages + res) // z) for z in sizes]
     _check_against_oracle(st, d, out, [0, B - 1], d.levels, n_q, n_kv, tail)
+
+
+@pytest.mark.parametrize("kernel,pps", [(_native.KERNEL_MFMA, None), (_native.KERNEL_MFMA, 1),
+                                        (_native.KERNEL_VALU, 3)])
+def test_plan_in_the_kernel_arguments_matches_the_device_plan(gpu, kernel, pps):
+    """The host copies of the plan (lf_decode_args.work_host / seq_work_host) put the work
+    records and the sequences' item ranges into the kernels' argument blocks; without them the
+    kernels read the device plan.  Same outputs bit for bit, and against the oracle.  With
+    1-page items 8 sequences x 15 items (120 <= LF_INLINE_WORK = 160) stay inline; 9 sequences
+    x 23 items (207) read their work records from the device list while their sequence ranges
+    stay inline."""
+    n_q, n_kv, tail = 28, 4, 45
+    for B, pages in ((8, 12), (9, 20)):
+        if pps != 1 and pages == 20:
+            continue
+        d, mgr, st = _layer(gpu, B, n_q, n_kv, pages, tail, seed=73 + pages)
+        outs = []
+        for inline in (True, False):
+            if not inline:  # the same cached argument block without the host copies
+                a = st.__dict__["_lf_decode_args"][1]
+                a.work_host, a.seq_work_host = 0, 0
+            out = torch.empty(B, n_q, D, dtype=torch.float32, device=gpu)
+            decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=kernel, pages_per_split=pps)
+            torch.cuda.synchronize()
+            if inline:
+                assert st.__dict__["_lf_decode_args"][1].work_host != 0
+            outs.append(out)
+        if pps == 1:
+            assert (st.decode_plan.n_work > 160) == (pages == 20)
+        print(f"inline plan: B {B} pages {pages} pps {pps} kernel {kernel} items {st.decode_plan.n_work}", flush=True)
+        assert torch.equal(outs[0], outs[1])
+        _check_against_oracle(st, d, outs[0], (0, B - 1), d.levels, n_q, n_kv, tail)

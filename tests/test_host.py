@@ -62,7 +62,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
         assert name in _native._SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.lf_abi_version() == 7
+    assert lib.lf_abi_version() == _native.ABI_VERSION == 8
     assert b"gfx950" in lib.lf_build_info()
 
 
