@@ -227,15 +227,16 @@ int64_t lf_decode_workspace_bytes(int32_t n_q, int32_t head_dim, int32_t n_work)
  * with q head i reading kv head i / (n_q / n_kv).  With q_len > 1 new tokens (chunked
  * scoring / speculative decoding; reference reference.py:18-27,48), query token j sees the
  * whole history and tail and the new tokens 0..j (right-aligned causal mask); the (head,
- * token) pairs are served as n_q * q_len query rows, by the VALU kernel (rows per kv head
- * <= 16; the MFMA kernel takes q_len 1 only).  Split-K over packed pages,
- * then a second kernel merges the splits' softmax partials; accumulation in fp32; output
- * rounded to ``out_dtype``.  Requires bit_v == 2 (as the reference kernel,
- * reference.py:62), n_q % n_kv == 0, head_dim a power of two in 8 .. 512, at most
- * 16 query rows per kv head (n_q / n_kv * q_len) and at most 64 Value groups;
- * other shapes return LF_E_UNSUPPORTED (the Python layer then runs the dense
- * dequantise-then-attend path on the device, as the reference falls back to its
- * dense path, reference.py:105-108).
+ * token) pairs are served as n_q * q_len query rows, in tiles of rows across workgroups (any
+ * number of rows per kv head).  Split-K over packed pages, then a second kernel merges the
+ * splits' softmax partials; accumulation in fp32; output rounded to ``out_dtype``.  Requires
+ * bit_v == 2 (as the reference kernel, reference.py:62), n_q % n_kv == 0, head_dim a power of
+ * two in 8 .. 1024 (as kernel.cu:224-230) and at most 64 Value groups; other shapes return
+ * LF_E_UNSUPPORTED (the Python layer then runs the dense dequantise-then-attend path on the
+ * device, as the reference falls back to its dense path, reference.py:105-108).  ``kernel``
+ * 0 takes the matrix-core kernel where its layout applies (head_dim 128, pages and Key groups
+ * of 128 tokens, one Value group per row, some integer Key tier, the page-major Key scale/min
+ * copy present, 16-byte aligned rows) and the general VALU kernel otherwise.
  */
 int32_t lf_decode_attention(const lf_packed_layer* layer, const lf_decode_args* args, void* stream);
 
