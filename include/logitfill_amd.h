@@ -168,7 +168,12 @@ int32_t lf_pack_pages_multi(const lf_packed_layer* layers_dev, const lf_packed_l
  * valid input (sequences in any order, items of any sizes, several calls'
  * lists concatenated with b and the first items shifted): the matrix-core
  * kernel dispatches it in list order (workgroup item * n_kv + h), which the
- * Python layer uses to put larger items first.
+ * Python layer uses to put larger items first.  An item's partial goes to the
+ * workspace slot of its list position, or, when kind's bits 8..30 hold a value
+ * s in 1 .. n_work, to slot s - 1: a list may then give the items in any
+ * dispatch order while seq_work names each sequence's consecutive slots (the
+ * Python layer's paired plan for a batch of equal sequences, where the
+ * workgroups dispatched first, one per CU, take the larger items).
  */
 int32_t lf_plan_decode(const int32_t* hist_pages, int32_t batch, int32_t pages_per_split, int32_t residual_pages,
                        int32_t* work_out, int32_t work_cap, int32_t* seq_work_out);

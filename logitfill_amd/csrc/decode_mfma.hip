@@ -990,7 +990,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     const int b = rec[0];
     const int pbeg = rec[1];
     const int pend = rec[2];
-    const int kind = rec[3];
+    const int kind = rec[3] & 0xff;
+    // the item's partial slot: kind bits 8.. hold slot + 1 when the plan lists its items out of
+    // slot order (any value past the workspace's n_work falls back to the item's own index)
+    const int part_slot = static_cast<unsigned>(rec[3] >> 8) - 1u < static_cast<unsigned>(A.n_work) ? (rec[3] >> 8) - 1 : item;
     // Tier-table entries of this thread's Key-slot block (used by items with pages, below): they
     // depend only on the kv head, so their loads go out while the work record is in flight.  Thread tid owns block gb = tid / 4 (K-step gb / 4); tier_index entries
     // are read whatever the tier count, which decides afterwards which are real slots.
@@ -1510,8 +1513,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     }
 
     // ---- merge the wave partials and store this item's partial ----
-    if (kind == 2) merge_partials<2 * kWaves>(p, item, h, row0, g, wstat, red, tid);
-    else merge_partials<kWaves>(p, item, h, row0, g, wstat, red, tid);
+    if (kind == 2) merge_partials<2 * kWaves>(p, part_slot, h, row0, g, wstat, red, tid);
+    else merge_partials<kWaves>(p, part_slot, h, row0, g, wstat, red, tid);
 }
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }

@@ -65,7 +65,9 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
     const int g = min(kMaxG, p.g - row0);
     const int* w4 = A.work + 4 * item;
     const int b = w4[0];
-    const int pbeg = w4[1], pend = w4[2], kind = w4[3];
+    const int pbeg = w4[1], pend = w4[2], kind = w4[3] & 0xff;
+    // partial slot: kind bits 8.. hold slot + 1 for plans listed out of slot order
+    const int part_slot = static_cast<unsigned>(w4[3] >> 8) - 1u < static_cast<unsigned>(A.n_work) ? (w4[3] >> 8) - 1 : item;
 
     int off[4];
     off[0] = 0;
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
 
     // Partials: o per lane-channel, m uniform, l reduced across the wave.
     for (int i = 0; i < g; ++i) {
-        float* r = part_rec(p, item, h, row0 + i);
+        float* r = part_rec(p, part_slot, h, row0 + i);
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc)
             if (lane + 64 * cc < D) r[lane + 64 * cc] = o[cc][i];

@@ -57,14 +57,17 @@ def _decode(d, mgr, gpu, scaling, pages_per_split=None, out_dtype=None):
 
 def test_headline_shape_full_size(gpu):
     """c2: 16 sequences x (256 pages + 100 residual + the new token), the bench's plan (the
-    dispatch-order split: sequences 0-7 in 7 items of about 37 pages, 8-15 in 9 of about 29,
-    the residual in each sequence's first item); sequence 0 of the first group and 9 of the
-    second checked."""
+    paired plan on 256 CUs: every sequence's 4 first items of 36 pages listed before all
+    second items of 29, 29, 29 and 25 pages + the residual, partials in per-sequence slots);
+    the first, a middle and the last sequence checked."""
     B, n_q, n_kv = 16, 28, 4
     d, mgr = _build(gpu, B, n_q, n_kv, [256] * B, [100] * B, 2.5, seed=11)
     scaling = 128 ** -0.5
     out = _decode(d, mgr, gpu, scaling)
-    for b in (0, 9):
+    plan = mgr.layers[0].decode_plan
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert plan.pages_per_split == ("paired", 36) and plan.n_work == 128
+    for b in (0, 9, 15):
         print(f"c2 full size: sequence {b}", flush=True)
         assert_decode_close(out[b], _oracle(d, mgr, b, n_q, n_kv, scaling))
 

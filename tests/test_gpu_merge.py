@@ -8,7 +8,7 @@ import torch
 
 from logitfill_amd import _native, synth
 from logitfill_amd.packed import PackedKVManager
-from logitfill_amd.packed.reference import decode_into, residual_pages
+from logitfill_amd.packed.reference import age_split, choose_pages_per_split, decode_into, residual_pages
 from oracle import attention as oatt
 from tests.helpers import assert_decode_close, f32
 
@@ -101,19 +101,32 @@ def test_back_to_back_layers_share_the_workspace(gpu):
 
 
 @pytest.mark.parametrize("B,n_q,n_kv,pages,tail", [(8, 12, 2, 200, 50), (4, 28, 4, 256, 20)])
-def test_dispatch_order_split_matches_the_oracle(gpu, B, n_q, n_kv, pages, tail):
-    """Batches of equal sequences whose plan fills one round take the dispatch-order split
-    (the first sequences in fewer, larger items): the plan holds two item sizes, the larger
-    first, and sequences of both groups match the oracle."""
+def test_dispatch_order_splits_match_the_oracle(gpu, B, n_q, n_kv, pages, tail):
+    """Batches of equal sequences whose plan fills one round: the planner's choice (on 256 CUs
+    the paired plan, first items listed first, partials in per-sequence slots) and the
+    two-size dispatch-order split (the first sequences in fewer, larger items: two item sizes,
+    the larger first) both match the oracle."""
     d, mgr, st = _layer(gpu, B, n_q, n_kv, pages, tail, seed=74 + B)
+    res = residual_pages([tail])
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     out = torch.empty(B, n_q, D, dtype=torch.float32, device=gpu)
     decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=_native.KERNEL_MFMA)
     torch.cuda.synchronize()
-    sizes = st.decode_plan.pages_per_split
-    assert isinstance(sizes, tuple) and len(set(sizes)) == 2 and sizes[0] > sizes[-1]
+    choice = st.decode_plan.pages_per_split
+    if cus == 256:
+        assert isinstance(choice, tuple) and choice[0] == "paired"
+        assert st.decode_plan.n_work * n_kv == 2 * cus
+    print(f"dispatch-order: planner's choice {choice}", flush=True)
+    _check_against_oracle(st, d, out, [0, B // 2, B - 1], d.levels, n_q, n_kv, tail)
+    size = choose_pages_per_split([pages] * B, n_kv, res, gpu)
+    sizes = tuple(age_split([pages] * B, n_kv, res, size, cus))
+    assert len(set(sizes)) == 2 and sizes[0] > sizes[-1]
+    decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=_native.KERNEL_MFMA,
+                pages_per_split=sizes)
+    torch.cuda.synchronize()
     seq = st.decode_plan.seq_work.cpu().tolist()
-    res = residual_pages([tail])
     assert [seq[2 * b + 1] for b in range(B)] == [-(-(pages + res) // z) for z in sizes]
+    print("dispatch-order: two-size split", flush=True)
     _check_against_oracle(st, d, out, [0, B - 1], d.levels, n_q, n_kv, tail)
 
 
@@ -147,3 +160,25 @@ def test_plan_in_the_kernel_arguments_matches_the_device_plan(gpu, kernel, pps):
         print(f"inline plan: B {B} pages {pages} pps {pps} kernel {kernel} items {st.decode_plan.n_work}", flush=True)
         assert torch.equal(outs[0], outs[1])
         _check_against_oracle(st, d, outs[0], (0, B - 1), d.levels, n_q, n_kv, tail)
+
+
+@pytest.mark.parametrize("kernel", [_native.KERNEL_MFMA, _native.KERNEL_VALU])
+def test_paired_plan_merges_to_the_oracle(gpu, kernel):
+    """The paired plan (items listed first-items-first, each partial in its sequence's slot
+    range through the kind field): 4 sequences x 200 pages, 4 kv heads, 16 first items of 7
+    pages and 16 second items per sequence on 256 CUs; both kernels against the oracle, and
+    the same outputs as the planner's own contiguous plan."""
+    if torch.cuda.get_device_properties(gpu).multi_processor_count != 256:
+        pytest.skip("the plan below is sized for 256 CUs")
+    B, n_q, n_kv, pages, tail = 4, 28, 4, 200, 45
+    d, mgr, st = _layer(gpu, B, n_q, n_kv, pages, tail, seed=79)
+    res = residual_pages([tail])
+    outs = []
+    for pps in (("paired", 7), 25):
+        out = torch.empty(B, n_q, D, dtype=torch.float32, device=gpu)
+        decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=kernel, pages_per_split=pps)
+        torch.cuda.synchronize()
+        outs.append(out)
+    print(f"paired plan: kernel {kernel} residual {res}", flush=True)
+    _check_against_oracle(st, d, outs[0], range(B), d.levels, n_q, n_kv, tail)
+    torch.testing.assert_close(outs[0], outs[1], rtol=2e-3, atol=2e-4)

@@ -11,7 +11,7 @@ import pytest
 
 from logitfill_amd import _native, synth
 from logitfill_amd.packed.reference import (ALONE_FACTOR, ITEM_OVERHEAD_PAGES, LATE_SLOWDOWN, age_split,
-                                            choose_pages_per_split,
+                                            choose_pages_per_split, paired_plan, paired_split,
                                             plan_work, residual_pages)
 
 SLOTS = 512  # 256 CUs x 2 workgroups
@@ -177,3 +177,41 @@ def test_age_split_declines_other_batches():
     assert age_split([64] * 8, 2, residual_pages([37]), 3, 256) is None
     assert age_split([256] * 16, 4, RES, 20, 256) is None
     assert age_split([256], 4, RES, 33, 256) is None
+
+
+def test_paired_plan_c2():
+    """c2 (16 x 256 pages + a 4-page residual, 4 kv heads, 256 CUs): 4 first items of 36 pages
+    per sequence, listed (dispatched) before every sequence's 4 second items of 29, 29, 29 and
+    25 pages + the residual; 512 workgroups = two per CU, each CU a first and a second item of
+    65 pages together.  Every page once, each sequence's partials in its own consecutive slots,
+    the residual once per sequence on its last item."""
+    hist, n_kv, res, cus = [256] * 16, 4, residual_pages([100]), 256
+    choice = paired_split(hist, n_kv, res, cus)
+    assert choice == ("paired", 36)
+    k = cus // (16 * n_kv)
+    work, seq = paired_plan(hist, k, choice[1], res)
+    items = [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)]
+    assert len(items) * n_kv == 2 * cus
+    first_half = items[:len(items) // 2]
+    assert all(p1 - p0 == 36 and (kind & 0xff) == 0 for _, p0, p1, kind in first_half)
+    slots = [(kind >> 8) - 1 for *_, kind in items]
+    assert sorted(slots) == list(range(len(items)))
+    for b in range(16):
+        first, count = seq[2 * b], seq[2 * b + 1]
+        mine = sorted((p0, p1, kind & 0xff, (kind >> 8) - 1) for bb, p0, p1, kind in items if bb == b)
+        assert count == 2 * k and sorted(s for *_, s in mine) == list(range(first, first + count))
+        assert mine[0][0] == 0 and mine[-1][1] == 256
+        assert all(mine[j][1] == mine[j + 1][0] for j in range(len(mine) - 1))
+        assert [m[2] for m in mine].count(2) == 1 and mine[-1][2] == 2 and mine[-1][1] - mine[-1][0] == 25
+        # the first and second items of a CU together: 36 + 29 = 65 = (256 + 4) / 4
+        assert sorted(set(m[1] - m[0] for m in mine)) == [25, 29, 36]
+
+
+def test_paired_split_declines_other_batches():
+    """Ragged lengths, a CU count the batch x kv heads does not divide, no pages, a pairing
+    that would leave a second item without a page."""
+    assert paired_split([256, 200] * 8, 4, RES, 256) is None
+    assert paired_split([256] * 12, 4, RES, 256) is None
+    assert paired_split([0] * 16, 4, RES, 256) is None
+    assert paired_split([6] * 16, 4, RES, 256) is None
+    assert paired_split([256] * 8, 4, RES, 256) == ("paired", int(round(0.56 * 260 / 8)))
