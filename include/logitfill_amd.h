@@ -214,7 +214,7 @@ typedef struct lf_decode_args {
 } lf_decode_args;
 
 /* Plan sizes that travel inline in the kernel arguments when the host copies are given. */
-#define LF_INLINE_WORK 160
+#define LF_INLINE_WORK 208
 #define LF_INLINE_SEQ 128
 
 /* Workspace bytes for lf_decode_attention with ``n_work`` items: the fp32

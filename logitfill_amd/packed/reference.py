@@ -229,60 +229,101 @@ def _age_split(hist_pages: tuple, n_kv: int, residual_pages: int, pages_per_spli
 # the paired plan at first-item sizes 33..39 pages of a 65-page pair: 36-37 best (67.8 us
 # against 69.9 for the two-size split).
 PAIR_FIRST_SHARE = 0.56
+# Small batches (the uniform plan leaves each workgroup a CU to itself, the prologue
+# dominates): the first items take this share of a CU's pages and the rest follow as 2-page
+# items, the residual as an item of its own.  Measured on c1 (8 x 64 pages, 2 kv heads, 256
+# CUs): first items of 3 pages + 2-page items 18.02 us against 19.32 for the uniform 5-page
+# plan; 4-page first items and no second items 18.28; 3 + 3-4 pages 20.26; the residual on
+# the last 2-page item 22.72; more than two workgroups per CU 24.5-25.6.
+SMALL_FIRST_SHARE = 0.75
+SMALL_SECOND_PAGES = 2
 
 
-def paired_split(hist_pages: list[int], n_kv: int, residual_pages: int, cus: int):
-    """("paired", first_size) for a batch of equal sequences whose items can pair up on the
-    CUs, or None.  Every sequence is cut into 2 k items, k = cus / (batch x n_kv): k items of
-    ``first_size`` pages, dispatched first (one workgroup per CU), and k smaller ones that
-    share the CUs with them, so both workgroups of a CU finish together (``paired_plan``)."""
+def paired_split(hist_pages: list[int], n_kv: int, residual_pages: int, cus: int, pages_per_split: int):
+    """("paired", first_size, second_size) for a batch of equal sequences whose items can pair
+    up on the CUs, or None.  Every sequence gets k = cus / (batch x n_kv) first items of
+    ``first_size`` pages, listed (dispatched) before any other item, one workgroup per CU:
+      - second_size 0 (the uniform plan ``pages_per_split`` fills one round of two workgroups
+        per CU): k second items share the rest, the residual on the last; both workgroups of
+        a CU finish together;
+      - second_size > 0 (the uniform plan leaves every workgroup a CU of its own): the rest in
+        items of second_size pages and the residual as an item of its own.
+    See ``paired_plan``."""
     B = len(hist_pages)
-    if B < 1 or n_kv <= 0 or cus <= 0 or len(set(hist_pages)) != 1 or hist_pages[0] <= 0:
+    if B < 1 or n_kv <= 0 or cus <= 0 or pages_per_split <= 0 or len(set(hist_pages)) != 1 or hist_pages[0] <= 0:
         return None
     if cus % (B * n_kv):
         return None
     k = cus // (B * n_kv)
-    work = int(hist_pages[0]) + int(residual_pages)
-    first = int(round(PAIR_FIRST_SHARE * work / k))
-    rest = work - k * first                    # the second items' work, residual included
-    # every second item keeps at least a page, the last one (which takes the residual) too
-    if first < 1 or rest // k - residual_pages < 1:
-        return None
-    return ("paired", first)
+    P = int(hist_pages[0])
+    work = P + int(residual_pages)
+    k0 = -(-work // int(pages_per_split))        # the uniform plan's items per sequence
+    wgs = B * n_kv * k0
+    if 0.9 * 2 * cus <= wgs <= 2 * cus:
+        first = int(round(PAIR_FIRST_SHARE * work / k))
+        rest = work - k * first                    # the second items' work, residual included
+        # every second item keeps at least a page, the last one (which takes the residual) too
+        if first < 1 or rest // k - residual_pages < 1:
+            return None
+        return ("paired", first, 0)
+    if wgs <= cus and k >= 2:
+        first = max(1, int(round(SMALL_FIRST_SHARE * P / k)))
+        rest = P - k * first
+        if rest < 0:
+            return None
+        n_second = -(-rest // SMALL_SECOND_PAGES)
+        if B * n_kv * (k + n_second + 1) > 2 * cus:
+            return None
+        return ("paired", first, SMALL_SECOND_PAGES)
+    return None
 
 
-def paired_plan(hist_pages: list[int], k: int, first: int, residual_pages: int) -> tuple[list[int], list[int]]:
-    """Work list and seq_work of the paired plan: the k first items of every sequence, then the
-    k second items of every sequence (list order = dispatch order), each item's partial slot
-    in its kind field (bits 8.. = slot + 1) so that sequence b's 2 k partials take slots
-    2 k b .. 2 k b + 2 k - 1.  The residual rides on each sequence's last item (kind 2)."""
+def paired_plan(hist_pages: list[int], k: int, first: int, residual_pages: int,
+                second: int = 0) -> tuple[list[int], list[int]]:
+    """Work list and seq_work of a paired plan: the k first items of every sequence, then every
+    sequence's other items (list order = dispatch order), each item's partial slot in its kind
+    field (bits 8.. = slot + 1) so that each sequence's partials take consecutive slots.
+    ``second`` 0: k second items sharing the rest of the work, the residual riding on the last
+    (kind 2); ``second`` > 0: the rest in items of ``second`` pages, then a residual-only item
+    (kind 1)."""
     B = len(hist_pages)
-    if k < 1 or first < 1:
-        raise ValueError("paired plan needs k >= 1 items of >= 1 page")
-    firsts, seconds = [], []
+    if k < 1 or first < 1 or second < 0:
+        raise ValueError("paired plan needs k >= 1 first items of >= 1 page")
+    firsts, others, counts = [], [], []
     for b in range(B):
         P = int(hist_pages[b])
-        rest = P + residual_pages - k * first
-        sizes = [rest // k + (1 if j < rest % k else 0) for j in range(k)]
-        sizes[-1] -= residual_pages
-        if min(sizes) < 1:
-            raise ValueError("paired plan leaves a second item without a page")
+        if second == 0:
+            rest = P + residual_pages - k * first
+            sizes = [rest // k + (1 if j < rest % k else 0) for j in range(k)]
+            sizes[-1] -= residual_pages
+        else:
+            rest = P - k * first
+            sizes = [min(second, rest - second * j) for j in range(-(-rest // second))] if rest > 0 else []
+        if sizes and min(sizes) < 1 or P < k * first:
+            raise ValueError("paired plan leaves an item without a page")
+        n = k + len(sizes) + (1 if second else 0)
+        base = sum(counts)
+        counts.append(n)
         p = 0
         for j in range(k):
-            firsts.append((b, p, p + first, 0, 2 * k * b + j))
+            firsts.append((b, p, p + first, 0, base + j))
             p += first
-        for j in range(k):
-            kind = 2 if j == k - 1 else 0
-            seconds.append((b, p, p + sizes[j], kind, 2 * k * b + k + j))
-            p += sizes[j]
+        for j, z in enumerate(sizes):
+            kind = 2 if second == 0 and j == len(sizes) - 1 else 0
+            others.append((b, p, p + z, kind, base + k + j))
+            p += z
+        if second:
+            others.append((b, p, p, 1, base + n - 1))
         if p != P:
             raise ValueError("paired plan does not cover the history")
     work = []
-    for b, p0, p1, kind, slot in firsts + seconds:
+    for b, p0, p1, kind, slot in firsts + others:
         work += [b, p0, p1, kind | ((slot + 1) << 8)]
     seq = []
-    for b in range(B):
-        seq += [2 * k * b, 2 * k]
+    base = 0
+    for n in counts:
+        seq += [base, n]
+        base += n
     return work, seq
 
 
@@ -331,7 +372,7 @@ def plan_work(hist_pages: list[int], sizes: list[int], residual_pages: int) -> t
 class DecodePlan:
     """Device work list for one layer's current history lengths (rebuilt when they change).
     ``pages_per_split``: one size for every sequence, a tuple of per-sequence sizes, or
-    ("paired", first_size) for ``paired_plan`` on the device's CU count."""
+    ("paired", first_size, second_size) for ``paired_plan`` on the device's CU count."""
 
     def __init__(self, hist_pages: list[int], n_kv: int, pages_per_split, device, residual_pages: int,
                  cus: int | None = None):
@@ -340,7 +381,7 @@ class DecodePlan:
             if cus is None:
                 cus = _cu_count(device)
             work, seq = paired_plan(list(hist_pages), cus // (batch * n_kv), int(pages_per_split[1]),
-                                    residual_pages)
+                                    residual_pages, int(pages_per_split[2]))
             self.key = (tuple(hist_pages), pages_per_split, residual_pages)
         else:
             sizes = [pages_per_split] * batch if isinstance(pages_per_split, int) else list(pages_per_split)
@@ -416,9 +457,8 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
             size = choose_pages_per_split(list(hist_pages), layer.n_kv * tiles, res_pages, layer.device)
             if age and choice_key[2] is None:
                 cus = _cu_count(layer.device)
-                paired = paired_split(list(hist_pages), layer.n_kv, res_pages, cus)
-                # the pairing replaces the two-size split where both apply (c2: 69.9 -> 67.8 us)
-                if paired is not None and age_split(list(hist_pages), layer.n_kv, res_pages, size, cus) is not None:
+                paired = paired_split(list(hist_pages), layer.n_kv, res_pages, cus, size)
+                if paired is not None:
                     size = paired
                 else:
                     sizes = age_split(list(hist_pages), layer.n_kv, res_pages, size, cus)

@@ -66,7 +66,7 @@ def test_headline_shape_full_size(gpu):
     out = _decode(d, mgr, gpu, scaling)
     plan = mgr.layers[0].decode_plan
     if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
-        assert plan.pages_per_split == ("paired", 36) and plan.n_work == 128
+        assert plan.pages_per_split == ("paired", 36, 0) and plan.n_work == 128
     for b in (0, 9, 15):
         print(f"c2 full size: sequence {b}", flush=True)
         assert_decode_close(out[b], _oracle(d, mgr, b, n_q, n_kv, scaling))

@@ -136,11 +136,11 @@ def test_plan_in_the_kernel_arguments_matches_the_device_plan(gpu, kernel, pps):
     """The host copies of the plan (lf_decode_args.work_host / seq_work_host) put the work
     records and the sequences' item ranges into the kernels' argument blocks; without them the
     kernels read the device plan.  Same outputs bit for bit, and against the oracle.  With
-    1-page items 8 sequences x 15 items (120 <= LF_INLINE_WORK = 160) stay inline; 9 sequences
-    x 23 items (207) read their work records from the device list while their sequence ranges
-    stay inline."""
+    1-page items 8 sequences x 15 items (120 <= LF_INLINE_WORK = 208) stay inline; 10
+    sequences x 23 items (230) read their work records from the device list while their
+    sequence ranges stay inline."""
     n_q, n_kv, tail = 28, 4, 45
-    for B, pages in ((8, 12), (9, 20)):
+    for B, pages in ((8, 12), (10, 20)):
         if pps != 1 and pages == 20:
             continue
         d, mgr, st = _layer(gpu, B, n_q, n_kv, pages, tail, seed=73 + pages)
@@ -156,25 +156,29 @@ def test_plan_in_the_kernel_arguments_matches_the_device_plan(gpu, kernel, pps):
                 assert st.__dict__["_lf_decode_args"][1].work_host != 0
             outs.append(out)
         if pps == 1:
-            assert (st.decode_plan.n_work > 160) == (pages == 20)
+            assert (st.decode_plan.n_work > 208) == (pages == 20)
         print(f"inline plan: B {B} pages {pages} pps {pps} kernel {kernel} items {st.decode_plan.n_work}", flush=True)
         assert torch.equal(outs[0], outs[1])
         _check_against_oracle(st, d, outs[0], (0, B - 1), d.levels, n_q, n_kv, tail)
 
 
-@pytest.mark.parametrize("kernel", [_native.KERNEL_MFMA, _native.KERNEL_VALU])
-def test_paired_plan_merges_to_the_oracle(gpu, kernel):
-    """The paired plan (items listed first-items-first, each partial in its sequence's slot
-    range through the kind field): 4 sequences x 200 pages, 4 kv heads, 16 first items of 7
-    pages and 16 second items per sequence on 256 CUs; both kernels against the oracle, and
-    the same outputs as the planner's own contiguous plan."""
+@pytest.mark.parametrize("kernel,choice", [(_native.KERNEL_MFMA, ("paired", 7, 0)),
+                                           (_native.KERNEL_VALU, ("paired", 7, 0)),
+                                           (_native.KERNEL_MFMA, ("paired", 9, 2)),
+                                           (_native.KERNEL_VALU, ("paired", 9, 2))])
+def test_paired_plan_merges_to_the_oracle(gpu, kernel, choice):
+    """The paired plans (items listed first-items-first, each partial in its sequence's slot
+    range through the kind field): 4 sequences x 200 pages, 4 kv heads, 16 first items per
+    sequence on 256 CUs, then 16 second items sharing the rest with the residual on the last,
+    or 2-page items and a residual-only item; both kernels against the oracle, and the same
+    outputs as a contiguous plan."""
     if torch.cuda.get_device_properties(gpu).multi_processor_count != 256:
         pytest.skip("the plan below is sized for 256 CUs")
     B, n_q, n_kv, pages, tail = 4, 28, 4, 200, 45
     d, mgr, st = _layer(gpu, B, n_q, n_kv, pages, tail, seed=79)
     res = residual_pages([tail])
     outs = []
-    for pps in (("paired", 7), 25):
+    for pps in (choice, 25):
         out = torch.empty(B, n_q, D, dtype=torch.float32, device=gpu)
         decode_into(mgr, 0, d.query, d.key_new, d.value_new, D ** -0.5, out, kernel=kernel, pages_per_split=pps)
         torch.cuda.synchronize()

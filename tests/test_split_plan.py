@@ -186,10 +186,10 @@ def test_paired_plan_c2():
     65 pages together.  Every page once, each sequence's partials in its own consecutive slots,
     the residual once per sequence on its last item."""
     hist, n_kv, res, cus = [256] * 16, 4, residual_pages([100]), 256
-    choice = paired_split(hist, n_kv, res, cus)
-    assert choice == ("paired", 36)
+    choice = paired_split(hist, n_kv, res, cus, choose_pages_per_split(hist, n_kv, res))
+    assert choice == ("paired", 36, 0)
     k = cus // (16 * n_kv)
-    work, seq = paired_plan(hist, k, choice[1], res)
+    work, seq = paired_plan(hist, k, choice[1], res, choice[2])
     items = [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)]
     assert len(items) * n_kv == 2 * cus
     first_half = items[:len(items) // 2]
@@ -207,11 +207,35 @@ def test_paired_plan_c2():
         assert sorted(set(m[1] - m[0] for m in mine)) == [25, 29, 36]
 
 
+def test_paired_plan_c1_small_batch():
+    """c1 (8 x 64 pages + a 37-token residual, 2 kv heads, 256 CUs; the uniform plan's 224
+    workgroups each have a CU of their own): 16 first items of 3 pages per sequence, listed
+    before all others, then 8 items of 2 pages and a residual-only item (kind 1): 25 items per
+    sequence, 400 workgroups; every page once, per-sequence consecutive slots."""
+    hist, n_kv, res, cus = [64] * 8, 2, residual_pages([37]), 256
+    choice = paired_split(hist, n_kv, res, cus, choose_pages_per_split(hist, n_kv, res))
+    assert choice == ("paired", 3, 2)
+    work, seq = paired_plan(hist, 16, 3, res, 2)
+    items = [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)]
+    assert len(items) == 8 * 25 and len(items) * n_kv == 400
+    assert all(p1 - p0 == 3 and kind & 0xff == 0 for _, p0, p1, kind in items[:8 * 16])
+    assert sorted((kind >> 8) - 1 for *_, kind in items) == list(range(len(items)))
+    for b in range(8):
+        first, count = seq[2 * b], seq[2 * b + 1]
+        mine = sorted(((kind >> 8) - 1, p0, p1, kind & 0xff) for bb, p0, p1, kind in items if bb == b)
+        assert count == 25 and [m[0] for m in mine] == list(range(first, first + 25))
+        pages = sorted((p0, p1) for _, p0, p1, k in mine if k != 1)
+        assert pages[0][0] == 0 and pages[-1][1] == 64 and all(pages[j][1] == pages[j + 1][0] for j in range(23))
+        assert [m[3] for m in mine].count(1) == 1 and mine[-1][3] == 1 and mine[-1][1] == mine[-1][2]
+
+
 def test_paired_split_declines_other_batches():
     """Ragged lengths, a CU count the batch x kv heads does not divide, no pages, a pairing
-    that would leave a second item without a page."""
-    assert paired_split([256, 200] * 8, 4, RES, 256) is None
-    assert paired_split([256] * 12, 4, RES, 256) is None
-    assert paired_split([0] * 16, 4, RES, 256) is None
-    assert paired_split([6] * 16, 4, RES, 256) is None
-    assert paired_split([256] * 8, 4, RES, 256) == ("paired", int(round(0.56 * 260 / 8)))
+    that would leave a second item without a page, a plan between the two regimes."""
+    assert paired_split([256, 200] * 8, 4, RES, 256, 33) is None
+    assert paired_split([256] * 12, 4, RES, 256, 33) is None
+    assert paired_split([0] * 16, 4, RES, 256, 33) is None
+    assert paired_split([20] * 16, 4, RES, 256, 3) is None       # 4 pages of work per second item
+    assert paired_split([6] * 16, 4, RES, 256, 3) == ("paired", 1, 2)  # small regime: 384 workgroups
+    assert paired_split([256] * 8, 4, RES, 256, 17) == ("paired", int(round(0.56 * 260 / 8)), 0)
+    assert paired_split([256] * 16, 4, RES, 256, 45) is None     # 384 workgroups: neither regime
