@@ -212,7 +212,7 @@ def decode_point(cfg, layers, steps, warmup, kernel, pages_per_split, dev, q_len
     return ms_step * 1e3 / layers, tot / layers, pay / layers, wall_ms
 
 
-def time_real_step(cfg, layers, steps, dev):
+def time_real_step(cfg, layers, steps, dev, fused=False):
     """A full decode step through the drop-in API, as a model's attention layers drive it
     (reference qwen2_attention.py:234-255): for every layer ``packed_attention`` over the packed
     history, the residual page and the new token, then ``commit`` of the new token; after the
@@ -220,7 +220,9 @@ def time_real_step(cfg, layers, steps, dev):
     defers flushes).  The residual starts ``steps // 2`` tokens short of a full page, so the
     timed steps cross one page boundary (a flush and a new decode plan).  Returns (GPU us per
     step from HIP events on the stream, host wall us per step, enqueue-only host us per step,
-    steps, pages flushed per layer)."""
+    steps, pages flushed per layer).  ``fused``: ``packed_attention(..., commit=True)``, the
+    commit folded into the decode launch while no page fills (as ``logitfill_amd.qwen2`` runs
+    the model's layers)."""
     import torch
 
     from logitfill_amd.packed.reference import packed_attention
@@ -236,8 +238,11 @@ def time_real_step(cfg, layers, steps, dev):
 
     def one_step():
         for layer, (q, kn, vn) in enumerate(ins):
-            packed_attention(mgr, layer, q, kn, vn, scaling)
-            mgr.commit(layer, kn, vn)
+            if fused:
+                packed_attention(mgr, layer, q, kn, vn, scaling, commit=True)
+            else:
+                packed_attention(mgr, layer, q, kn, vn, scaling)
+                mgr.commit(layer, kn, vn)
         mgr.flush_pending()
 
     one_step()  # warm-up: plans, workspace, pinned staging buffers
@@ -260,7 +265,7 @@ def time_real_step(cfg, layers, steps, dev):
     return start.elapsed_time(end) * 1e3 / n, wall * 1e6 / n, t_enq * 1e6 / n, n, flushed
 
 
-def time_graph_step(cfg, layers, replays, dev):
+def time_graph_step(cfg, layers, replays, dev, fused=False):
     """The same decode step (every layer's packed_attention, then the one-token commit, which
     appends on the device) captured once in a HIP graph and replayed ``replays`` times, as a
     serving loop launches it; the residual starts at 20 tokens so no replay fills a page.
@@ -276,8 +281,11 @@ def time_graph_step(cfg, layers, replays, dev):
 
     def one_step():
         for layer, (q, kn, vn) in enumerate(ins):
-            packed_attention(mgr, layer, q, kn, vn, scaling)
-            mgr.commit(layer, kn, vn)
+            if fused:
+                packed_attention(mgr, layer, q, kn, vn, scaling, commit=True)
+            else:
+                packed_attention(mgr, layer, q, kn, vn, scaling)
+                mgr.commit(layer, kn, vn)
 
     one_step()
     torch.cuda.synchronize(dev)
@@ -653,6 +661,16 @@ def main():
             legs[f"graph_step_{name}"] = round(time.perf_counter() - t0, 2)
             result["decode_step"][name]["graph_us_per_step"] = round(g_us, 1)
             result["decode_step"][name]["graph_us_per_layer"] = round(g_us / c["layers"], 2)
+            # the same step with the commit folded into the decode launch (logitfill_amd.qwen2)
+            t0 = time.perf_counter()
+            f_us, f_wall, f_enq, _, f_flushed = time_real_step(c, c["layers"], 40, dev, fused=True)
+            fg_us = time_graph_step(c, c["layers"], 60, dev, fused=True)
+            legs[f"fused_step_{name}"] = round(time.perf_counter() - t0, 2)
+            result["decode_step"][name]["fused_commit"] = {
+                "what": "packed_attention(..., commit=True): the one-token commit appended inside the decode "
+                        "launch while no residual page fills (the page-filling step commits as before)",
+                "us_per_layer": round(f_us / c["layers"], 2), "host_enqueue_us_per_step": round(f_enq, 1),
+                "graph_us_per_layer": round(fg_us / c["layers"], 2), "pages_flushed_per_layer": f_flushed}
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         t0 = time.perf_counter()

@@ -211,6 +211,12 @@ typedef struct lf_decode_args {
                                                  argument blocks, which saves each workgroup
                                                  a dependent read of device memory; read
                                                  during the call only                    */
+    int32_t commit_new;                       /* 1: also append k_new / v_new (q_len rows)
+                                                 to the tail at tail_len[b] and advance
+                                                 tail_len, as lf_append_token would after
+                                                 the call; needs tail buffers and, for every
+                                                 sequence, tail_len + q_len < page_size (a
+                                                 row past tail_cap is not written)        */
 } lf_decode_args;
 
 /* Plan sizes that travel inline in the kernel arguments when the host copies are given. */

@@ -87,6 +87,7 @@ class DecodeArgs(ctypes.Structure):
         ("kernel", c_int32),
         ("q_len", c_int32),
         ("work_host", c_void_p), ("seq_work_host", c_void_p),
+        ("commit_new", c_int32),
     ]
 
 

@@ -104,6 +104,8 @@ int32_t decode_checked(const lf_packed_layer* layer, const lf_decode_args* args,
     if (A.n_work <= 0 || static_cast<int64_t>(A.n_work) * layer->n_kv > 0x7fffffff) return LF_E_SHAPE;
     if (workspace_bytes < lf_decode_workspace_bytes(static_cast<int32_t>(rows), D, A.n_work)) return LF_E_WORKSPACE;
     if (A.kernel < 0 || A.kernel > 2) return LF_E_SHAPE;
+    if (A.commit_new != 0 && A.commit_new != 1) return LF_E_SHAPE;
+    if (A.commit_new && (!A.k_new || A.tail_cap < q_len)) return LF_E_SHAPE;  // rows to append, room for them
 
     DecodeParams p;
     p.L = *layer;

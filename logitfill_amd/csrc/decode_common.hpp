@@ -118,6 +118,26 @@ __device__ __forceinline__ i32x2 prefetch_args_rec2(uint32_t off) {
 #undef LF_ARG_LINES6
 #undef LF_ARG_LINE
 
+// The commit folded into the decode (lf_decode_args.commit_new): the workgroup that owns
+// sequence b's residual for kv head h (row tile 0) copies the new rows into the tail buffer at
+// the device-side tail length every decode workgroup reads; nothing in the launch reads those
+// rows (the residual pass takes the new tokens from k_new / v_new).  The reduce kernel then
+// advances the length, after every decode workgroup has read it.
+__device__ __forceinline__ void commit_new_rows(const DecodeParams& p, int b, int h, int tid, int nthreads) {
+    const lf_decode_args& A = p.A;
+    const int tl = A.tail_len[b];
+    const int D = p.L.head_dim, q_len = p.q_len;
+    if (tl < 0 || tl + q_len > A.tail_cap) return;  // the host keeps it below; bounds safety
+    for (int e = tid; e < q_len * D; e += nthreads) {
+        const int t = e / D, c = e - t * D;
+        const int64_t bh = static_cast<int64_t>(b) * p.L.n_kv + h;
+        const int64_t src = (bh * q_len + t) * D + c;
+        const int64_t dst = (bh * A.tail_cap + tl + t) * D + c;
+        store_from_f32(const_cast<void*>(A.tail_k), dst, A.tail_dtype, load_as_f32(A.k_new, src, A.new_dtype));
+        store_from_f32(const_cast<void*>(A.tail_v), dst, A.tail_dtype, load_as_f32(A.v_new, src, A.new_dtype));
+    }
+}
+
 // Merge the partials of every sequence into ``out`` (enqueued after a decode kernel).  With the
 // host copy of seq_work and at most LF_INLINE_SEQ sequences, the (first, count) pairs go into
 // the reduce kernel's arguments.

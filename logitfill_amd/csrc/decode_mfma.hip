@@ -1515,6 +1515,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_mfma_kernel(MfmaParams mp)
     // ---- merge the wave partials and store this item's partial ----
     if (kind == 2) merge_partials<2 * kWaves>(p, part_slot, h, row0, g, wstat, red, tid);
     else merge_partials<kWaves>(p, part_slot, h, row0, g, wstat, red, tid);
+    if (A.commit_new && kind != 0 && rt == 0) commit_new_rows(p, b, h, tid, kThreads);
 }
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }

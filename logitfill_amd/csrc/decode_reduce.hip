@@ -37,6 +37,9 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(ReduceParams rp) {
     const int g = p.g;
     // grid (g, n_kv, batch): no divisions
     const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    // the folded commit: every decode workgroup has read tail_len[b]; advance it once
+    if (p.A.commit_new && !p.dense_splits && h == 0 && i == 0 && threadIdx.x == 0)
+        const_cast<int32_t*>(p.A.tail_len)[b] += p.q_len;
     const int first = p.dense_splits ? b * p.dense_splits : rp.inline_seq ? seq_arg[0] : p.A.seq_work[2 * b];
     const int count = p.dense_splits ? p.dense_splits : rp.inline_seq ? seq_arg[1] : p.A.seq_work[2 * b + 1];
     const int tid = threadIdx.x;

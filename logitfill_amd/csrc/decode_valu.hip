@@ -303,6 +303,7 @@ __global__ __launch_bounds__(64) void decode_valu_kernel(DecodeParams p) {
             r[D + 1] = lt;
         }
     }
+    if (A.commit_new && kind != 0 && blockIdx.z == 0) commit_new_rows(p, b, h, lane, 64);
 }
 
 template <int D>

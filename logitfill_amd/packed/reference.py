@@ -414,7 +414,7 @@ def kernel_choice() -> int:
 
 def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new, scaling: float,
                 out: torch.Tensor, kernel: int | None = None, pages_per_split: int | None = None,
-                noalloc: bool = False) -> None:
+                noalloc: bool = False, commit: bool = False) -> bool:
     """Enqueue the fused decode kernel for layer ``layer_idx`` writing ``out``.
 
     One new token: ``query/out [B, n_q, D]``, ``key_new/value_new [B, n_kv, D]`` or None.
@@ -423,6 +423,10 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     (reference ``reference.py:18-27,48``).  Everything is enqueued on the current stream;
     nothing synchronises.  ``noalloc`` calls ``lf_decode_attention_noalloc`` (the partials in
     the library's per-GPU scratch array instead of the manager's workspace).
+
+    ``commit``: also append the new tokens to the layer, in the same launch
+    (``lf_decode_args.commit_new``), when no residual page fills; returns whether it did --
+    when it did not, the caller commits as usual (``PackedKVManager.commit``).
     """
     layer = manager.layers[layer_idx]
     layer.flush()  # deferred residual pages of this layer, if any
@@ -468,7 +472,16 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
         pages_per_split = cached[1]
     plan = layer.decode_plan
     if plan is None or plan.key != (hist_pages, pages_per_split, res_pages):
-        plan = DecodePlan(list(hist_pages), layer.n_kv, pages_per_split, layer.device, res_pages)
+        # the layers of a manager share their history lengths, so one plan serves them all (its
+        # device lists are only read): built by the first layer after a change, found by the rest
+        shared = manager.__dict__.setdefault("_lf_plans", {})
+        pkey = (hist_pages, pages_per_split, res_pages, layer.n_kv, str(layer.device))
+        plan = shared.get(pkey)
+        if plan is None:
+            if len(shared) >= 8:
+                shared.clear()
+            plan = DecodePlan(list(hist_pages), layer.n_kv, pages_per_split, layer.device, res_pages)
+            shared[pkey] = plan
         layer.decode_plan = plan
     lib = _native.load()
     wkey = (manager.n_q * q_len, layer.head_dim)
@@ -522,6 +535,9 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     a.out = out.data_ptr()
     a.k_new = 0 if key_new is None else key_new.data_ptr()
     a.v_new = 0 if key_new is None else value_new.data_ptr()
+    # the commit folds into the launch while every sequence's residual page stays below full
+    fold = commit and key_new is not None and tail_k is not None and max(layer.tail_lens) + q_len < P
+    a.commit_new = 1 if fold else 0
     stream = _native.current_stream_ptr(layer.device)
     if noalloc:
         st = lib.lf_decode_attention_noalloc(layer.layer_struct(), a, stream)
@@ -529,20 +545,24 @@ def decode_into(manager, layer_idx: int, query: torch.Tensor, key_new, value_new
     else:
         st = lib.lf_decode_attention(layer.layer_struct(), a, stream)
         _native.check(st, "lf_decode_attention")
+    if fold:
+        layer.tail_lens = [t + q_len for t in layer.tail_lens]
+    return fold
 
 
 def _kernel_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
-                      value_new: torch.Tensor, scaling: float) -> torch.Tensor:
+                      value_new: torch.Tensor, scaling: float, commit: bool = False):
     """Decode through the HIP kernels (replaces ``reference.py:59-109``).  The tensors go to
     ``decode_into`` in their ``[B, heads, q_len, D]`` form (for one token the same memory as
-    ``[B, heads, D]``), copied only when not contiguous: this runs once per layer and step."""
+    ``[B, heads, D]``), copied only when not contiguous: this runs once per layer and step.
+    Returns (output, whether the commit was folded into the launch)."""
     B, n_q, q_len, D = query.shape
     q = query if query.is_contiguous() else query.contiguous()
     kn = key_new if key_new.is_contiguous() else key_new.contiguous()
     vn = value_new if value_new.is_contiguous() else value_new.contiguous()
     out = torch.empty(B, n_q, q_len, D, dtype=query.dtype, device=query.device)
-    decode_into(manager, layer_idx, q, kn, vn, scaling, out)
-    return out
+    folded = decode_into(manager, layer_idx, q, kn, vn, scaling, out, commit=commit)
+    return out, folded
 
 
 # Query rows per workgroup of the matrix-core decode kernel: rows beyond it ((n_q / n_kv) * q_len
@@ -583,7 +603,7 @@ def kernel_unsupported_reason(manager, q_len: int = 1) -> str | None:
 
 
 def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torch.Tensor,
-                     value_new: torch.Tensor, scaling: float) -> torch.Tensor:
+                     value_new: torch.Tensor, scaling: float, *, commit: bool = False) -> torch.Tensor:
     """``reference.py:112-116``: ``query [B, n_q, q_len, D]`` -> ``[B, n_q, q_len, D]``.
 
     Shapes the decode kernels serve run the HIP split-K decode.  Others take the dense
@@ -591,6 +611,12 @@ def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torc
     (``reference.py:62-68,105-108``) -- but not silently: each fallback is counted in
     ``DENSE_FALLBACKS``, warned about once per reason, and raises instead when the environment
     sets ``LOGITFILL_AMD_STRICT=1``.
+
+    ``commit`` (extension, keyword only): also append ``key_new / value_new`` to the layer,
+    as ``manager.commit(layer_idx, key_new, value_new)`` right after the call would (the
+    reference model's order, ``qwen2_attention.py:223-256``).  While no residual page fills
+    the append runs inside the decode launch (one launch per layer fewer); otherwise, and on
+    the dense path, through ``manager.commit``.
     """
     if not query.is_cuda:
         raise RuntimeError("logitfill_amd runs on ROCm devices only (there is no CPU path)")
@@ -600,7 +626,13 @@ def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torc
         cache[q_len] = kernel_unsupported_reason(manager, q_len)
     reason = cache[q_len]
     if reason is None:
-        return _kernel_attention(manager, layer_idx, query, key_new, value_new, scaling)
+        out, folded = _kernel_attention(manager, layer_idx, query, key_new, value_new, scaling, commit)
+        if commit:
+            if not folded:
+                manager.commit(layer_idx, key_new, value_new)
+            elif layer_idx == len(manager.layers) - 1:
+                manager.seq_len = manager.layers[layer_idx].length
+        return out
     if os.environ.get("LOGITFILL_AMD_STRICT", "") == "1":
         raise _native.LFError(_native.LF_E_UNSUPPORTED, reason, "packed_attention")
     DENSE_FALLBACKS[reason] += 1
@@ -608,4 +640,7 @@ def packed_attention(manager, layer_idx: int, query: torch.Tensor, key_new: torc
         _WARNED.add(reason)
         warnings.warn(f"packed_attention: {reason}; running the dense dequantise-then-attend path on the device",
                       RuntimeWarning, stacklevel=2)
-    return reference_attention(manager, layer_idx, query, key_new, value_new, scaling)
+    out = reference_attention(manager, layer_idx, query, key_new, value_new, scaling)
+    if commit:
+        manager.commit(layer_idx, key_new, value_new)
+    return out

@@ -48,9 +48,13 @@ def _make_forward(attn, manager, attention_fn):
         past = manager.layer_length(layer_idx)
         if past == 0:
             out = _dense_attention(attn, query, key, value, attention_mask, kwargs)
+            manager.commit(layer_idx, key, value)
+        elif attention_fn is packed_attention:
+            # attention then commit, the commit folded into the decode launch where it can be
+            out = packed_attention(manager, layer_idx, query, key, value, attn.scaling, commit=True).transpose(1, 2)
         else:
             out = attention_fn(manager, layer_idx, query, key, value, attn.scaling).transpose(1, 2)
-        manager.commit(layer_idx, key, value)
+            manager.commit(layer_idx, key, value)
         if past_key_values is not None and hasattr(past_key_values, "note_layer"):
             past_key_values.note_layer(layer_idx, manager.seq_len)  # LogitFillCache (qwen2_attention.py:254-255)
         out = out.reshape(*input_shape, -1).contiguous()
