@@ -189,3 +189,35 @@ def test_padded_value_words_accepted():
 
     assert value_words(8, 2) == 1 and value_words(128, 2) == 8 and value_words(24, 4) == 3
     assert value_words(100, 8) == 25 and value_words(12, 8) == 3
+
+
+def test_decode_commit_arguments_rejected_before_launch():
+    """lf_decode_args.commit_new: only 0 or 1, and 1 needs the new rows and room for them in the
+    tail; each of these calls returns LF_E_SHAPE from the host checks, before anything touches
+    a device (the pointers are placeholders that are never dereferenced)."""
+    lib = _native.load()
+    fake = 0x1000
+    L = _native.PackedLayer()
+    L.batch, L.n_kv, L.head_dim, L.page_size, L.k_group = 2, 4, 128, 128, 128
+    L.cap_tokens, L.cap_kgroups = 1024, 8
+    L.k_width[:] = [64, 32, 32, 0]
+    L.k_words[:] = [4, 4, 8]
+    for t in range(3):
+        L.k_code[t] = L.k_scale[t] = L.k_min[t] = fake
+        L.tier_index[t] = L.tier_count[t] = fake
+    L.bit_v, L.v_group, L.v_groups, L.v_words = 2, 128, 1, 8
+    L.v_code = L.v_scale = L.v_min = fake
+    a = _native.DecodeArgs()
+    a.query = a.out = a.work = a.seq_work = a.tail_len = fake
+    a.k_new = a.v_new = a.tail_k = a.tail_v = fake
+    a.q_dtype = a.out_dtype = a.tail_dtype = a.new_dtype = _native.LF_BF16
+    a.n_q, a.q_len, a.n_work, a.tail_cap, a.scaling = 28, 1, 4, 128, 1.0
+    a.workspace, a.workspace_bytes = fake, 1 << 30
+    a.commit_new = 2
+    assert lib.lf_decode_attention(L, a, None) == -2
+    a.commit_new, a.tail_cap = 1, 0
+    assert lib.lf_decode_attention(L, a, None) == -2          # no tail rows to append into
+    a.tail_cap, a.q_len = 128, 200
+    assert lib.lf_decode_attention(L, a, None) == -2          # more new rows than the tail holds
+    a.q_len, a.k_new, a.v_new = 1, 0, 0
+    assert lib.lf_decode_attention(L, a, None) == -2          # nothing to append
