@@ -199,6 +199,7 @@ def decode_point(cfg, layers, steps, warmup, kernel, pages_per_split, dev, q_len
 
     mgr, inputs = build_state(cfg, layers, dev, q_len=q_len)
     ms_step, wall_ms = time_decode(mgr, inputs, steps, warmup, kernel, pages_per_split)
+    split = plan_text(mgr.layers[0].decode_plan)
     n_q, n_kv, D = cfg["n_q"], cfg["n_kv"], cfg["head_dim"]
     pages, resid, _ = seq_lengths(cfg)
     tot, pay = 0, 0
@@ -209,7 +210,21 @@ def decode_point(cfg, layers, steps, warmup, kernel, pages_per_split, dev, q_len
             pay += pl
     del mgr, inputs
     torch.cuda.empty_cache()
-    return ms_step * 1e3 / layers, tot / layers, pay / layers, wall_ms
+    return ms_step * 1e3 / layers, tot / layers, pay / layers, wall_ms, split
+
+
+def plan_text(plan) -> str:
+    """The decode plan the planner chose, in words (reported beside the timing)."""
+    pps = plan.pages_per_split
+    if isinstance(pps, tuple) and pps and pps[0] == "paired":
+        how = (f"paired: the first-dispatched workgroups take {pps[1]}-page items, the rest shares the CUs"
+               if pps[2] == 0 else
+               f"paired small batch: {pps[1]}-page first items, then {pps[2]}-page items and residual-only items")
+    elif isinstance(pps, tuple):
+        how = f"two-size dispatch-order split: {max(pps)} and {min(pps)} pages per item"
+    else:
+        how = f"{pps} pages per item"
+    return f"{how}; {plan.n_work} items"
 
 
 def time_real_step(cfg, layers, steps, dev, fused=False):
@@ -566,7 +581,7 @@ def main():
     kernel = {"auto": _native.KERNEL_AUTO, "valu": _native.KERNEL_VALU, "mfma": _native.KERNEL_MFMA}[args.kernel]
     print(f"[bench] building {layers} layers of {args.config} and timing ...", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
-    us_layer, bytes_launch, pay_launch, wall_ms = decode_point(cfg, layers, args.steps, args.warmup, kernel,
+    us_layer, bytes_launch, pay_launch, wall_ms, split = decode_point(cfg, layers, args.steps, args.warmup, kernel,
                                                                args.pages_per_split, dev)
     legs["decode"] = round(time.perf_counter() - t0, 2)
     ms_step = us_layer * layers / 1e3
@@ -590,7 +605,7 @@ def main():
         "data": "synthetic (seeded logitfill_amd.synth: K~N(0,1)*LogNormal channel scale + outliers, V,Q~N)",
         "config": {"workload": f"{args.config}: packed decode attention, {layers} layers x batch {B}, "
                                f"{n_q}q/{n_kv}kv heads, D {D}, {context_text(cfg)}, target_bit {cfg['target_bit']}",
-                   "kernel": args.kernel, "layers": layers, "batch": B},
+                   "kernel": args.kernel, "layers": layers, "batch": B, "split": split},
         "hbm_gbs": round(achieved, 1),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
         "payload_gbs": round(pay_bytes / layers / launch_s / 1e9, 1),
@@ -629,7 +644,7 @@ def main():
             nl = n_layers or c["layers"]
             print(f"[bench] {name} ({nl} layers) ...", file=sys.stderr, flush=True)
             t0 = time.perf_counter()
-            us_x, bytes_x, pay_x, _ = decode_point(c, nl, 10, 2, kernel, None, dev, q_len=q_len)
+            us_x, bytes_x, pay_x, _, split_x = decode_point(c, nl, 10, 2, kernel, None, dev, q_len=q_len)
             legs[name] = round(time.perf_counter() - t0, 2)
             tokens = (f", {q_len} new query tokens per sequence (speculative decoding: the right-aligned causal "
                       f"mask on the new tokens, {c['n_q'] // c['n_kv'] * q_len} query rows per kv head)"
@@ -640,7 +655,7 @@ def main():
                            "us_per_layer_step": round(us_x, 2), "bytes_per_layer_step": int(bytes_x),
                            "hbm_gbs": round(bytes_x / us_x / 1e3, 1),
                            "hbm_frac": round(bytes_x / us_x / 1e3 / HBM_PEAK_GBS, 4),
-                           "payload_gbs": round(pay_x / us_x / 1e3, 1)}
+                           "payload_gbs": round(pay_x / us_x / 1e3, 1), "split": split_x}
         result["other_configs"] = extra
     if not args.no_step and args.layers is None:
         for name in (args.config, "c1") if args.config != "c1" else (args.config,):
