@@ -134,3 +134,19 @@ def test_config4_full_batch_bench_plan(gpu):
         print(f"c4 batch 32: sequence {b}, {pages[b]} pages + {resid[b]}, "
               f"{int((work[:, 0] == b).sum())} items", flush=True)
         assert_decode_close(out[b], _oracle(d, mgr, b, n_q, n_kv, scaling))
+
+
+def test_single_64k_sequence_paired_plan(gpu):
+    """One sequence at the largest BASELINE context (512 pages = 64K tokens + a 100-token
+    residual), 40 q / 8 kv heads (c4's head shape): the planner pairs its items on 256 CUs --
+    32 first items of 9 pages listed before 32 second items sharing the rest, partials in the
+    sequence's 64 slots -- and the output meets the bar against the oracle."""
+    B, n_q, n_kv = 1, 40, 8
+    d, mgr = _build(gpu, B, n_q, n_kv, [512], [100], 2.5, seed=17)
+    scaling = 128 ** -0.5
+    out = _decode(d, mgr, gpu, scaling)
+    plan = mgr.layers[0].decode_plan
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert plan.pages_per_split == ("paired", 9, 0) and plan.n_work == 64
+    print("single 64K sequence, paired plan", flush=True)
+    assert_decode_close(out[0], _oracle(d, mgr, 0, n_q, n_kv, scaling))
