@@ -3,7 +3,8 @@
 ``manager.commit`` (reference ``qwen2_attention.py:223-256``, ``cache.py:135-140``): two managers
 built from the same data decode the same tokens step by step across a residual page boundary;
 every step's output is bit-identical and so are the layers' lengths, tail rows and packed
-pages, for both decode kernels and for two new tokens per step."""
+pages, for both decode kernels, for two new tokens per step and for a 32-head group on one kv
+head (four row tiles per kv head, the first of which commits)."""
 import pytest
 import torch
 
@@ -44,10 +45,11 @@ def _same_state(a, b):
             assert torch.equal(va[k], vb[k]), (s, k)
 
 
-@pytest.mark.parametrize("kernel,q_len", [("auto", 1), ("valu", 1), ("auto", 2)])
-def test_folded_commit_matches_attention_then_commit(gpu, monkeypatch, kernel, q_len):
+@pytest.mark.parametrize("kernel,q_len,n_q,n_kv", [("auto", 1, 28, 4), ("valu", 1, 28, 4), ("auto", 2, 28, 4),
+                                                  ("auto", 1, 32, 1)])
+def test_folded_commit_matches_attention_then_commit(gpu, monkeypatch, kernel, q_len, n_q, n_kv):
     monkeypatch.setenv("LOGITFILL_AMD_KERNEL", kernel)
-    B, n_q, n_kv, pages, tail = 3, 28, 4, 6, 122
+    B, pages, tail = 3, 6, 122
     d = synth.make_layer(B, n_q, n_kv, D, pages * 128 + 128, 2.5, seed=83, device=gpu)
     ref, fused = (_manager(gpu, d, B, n_q, n_kv, pages, tail) for _ in range(2))
     gen = torch.Generator(device=gpu).manual_seed(5)
@@ -62,7 +64,7 @@ def test_folded_commit_matches_attention_then_commit(gpu, monkeypatch, kernel, q
         out_f = packed_attention(fused, 0, q, k, v, D ** -0.5, commit=True)
         torch.cuda.synchronize()
         folded += int(before + q_len < 128)
-        print(f"folded commit: kernel {kernel} q_len {q_len} step {step} tail {before}", flush=True)
+        print(f"folded commit: kernel {kernel} q_len {q_len} heads {n_q}/{n_kv} step {step} tail {before}", flush=True)
         assert torch.equal(out_r, out_f)
         _same_state(ref, fused)
     assert ref.layers[0].hist_lens[0] == (pages + 1) * 128 and 0 < folded < 8
