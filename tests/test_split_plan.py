@@ -7,6 +7,7 @@ independent of the closed-form cost the chooser minimises."""
 import ctypes
 import heapq
 
+import numpy as np
 import pytest
 
 from logitfill_amd import _native, synth
@@ -239,3 +240,43 @@ def test_paired_split_declines_other_batches():
     assert paired_split([6] * 16, 4, RES, 256, 3) == ("paired", 1, 2)  # small regime: 384 workgroups
     assert paired_split([256] * 8, 4, RES, 256, 17) == ("paired", int(round(0.56 * 260 / 8)), 0)
     assert paired_split([256] * 16, 4, RES, 256, 45) is None     # 384 workgroups: neither regime
+
+
+def test_paired_plan_valid_wherever_chosen():
+    """Wherever ``paired_split`` chooses a paired plan (equal sequences of 1-600 pages, batch
+    1-64, 1-8 kv heads, residual costs 3-4 pages, 64-304 CUs), ``paired_plan`` builds it: every
+    page of every sequence in exactly one item, one residual carrier per sequence (the last
+    second item, or a residual-only item in the small-batch form), per-sequence consecutive
+    partial slots, no page-less item but the residual-only one, and at most two workgroups per
+    CU."""
+    rng = np.random.default_rng(7)
+    chosen = 0
+    for _ in range(3000):
+        B = int(rng.integers(1, 65))
+        n_kv = int(rng.choice([1, 2, 4, 8]))
+        P = int(rng.integers(1, 601))
+        res = int(rng.choice([3, 4]))
+        cus = int(rng.choice([64, 80, 128, 256, 304]))
+        hist = [P] * B
+        choice = paired_split(hist, n_kv, res, cus, choose_pages_per_split(hist, n_kv, res) if cus == 256 else
+                              max(1, -(-n_kv * B * (P + res) // (2 * cus))))
+        if choice is None:
+            continue
+        chosen += 1
+        k = cus // (B * n_kv)
+        work, seq = paired_plan(hist, k, choice[1], res, choice[2])
+        items = [tuple(work[4 * i:4 * i + 4]) for i in range(len(work) // 4)]
+        assert len(items) * n_kv <= 2 * cus, (B, n_kv, P, res, cus, choice)
+        assert sorted((kind >> 8) - 1 for *_, kind in items) == list(range(len(items)))
+        assert items[:B * k] == sorted(items[:B * k], key=lambda it: (it[0], it[1]))  # first items lead
+        for b in range(B):
+            first, count = seq[2 * b], seq[2 * b + 1]
+            mine = sorted(((kind >> 8) - 1, p0, p1, kind & 0xff) for bb, p0, p1, kind in items if bb == b)
+            assert [m[0] for m in mine] == list(range(first, first + count))
+            spans = sorted((p0, p1) for _, p0, p1, kd in mine if kd != 1)
+            assert spans[0][0] == 0 and spans[-1][1] == P
+            assert all(a[1] == c[0] for a, c in zip(spans, spans[1:])) and all(p1 > p0 for p0, p1 in spans)
+            kinds = [m[3] for m in mine]
+            assert kinds.count(1) + kinds.count(2) == 1
+            assert (kinds.count(1) == 1) == (choice[2] > 0)
+    assert chosen > 50
