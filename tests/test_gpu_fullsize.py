@@ -150,3 +150,21 @@ def test_single_64k_sequence_paired_plan(gpu):
         assert plan.pages_per_split == ("paired", 9, 0) and plan.n_work == 64
     print("single 64K sequence, paired plan", flush=True)
     assert_decode_close(out[0], _oracle(d, mgr, 0, n_q, n_kv, scaling))
+
+
+@pytest.mark.parametrize("kernel", [_native.KERNEL_MFMA, _native.KERNEL_VALU])
+def test_target_4_tier_mix(gpu, kernel):
+    """c2's head shape at target 4.0 (Key 6.0 bits: up to 34 int8 and 13 fp16 channels per kv
+    head, the widest tier mix BASELINE names), 4 sequences x 64 pages + a 100-token residual,
+    with both decode kernels: every sequence meets the bar against the oracle."""
+    B, n_q, n_kv = 4, 28, 4
+    d, mgr = _build(gpu, B, n_q, n_kv, [64] * B, [100] * B, 4.0, seed=19)
+    assert mgr.layers[0].widths[3] > 8 and mgr.layers[0].words[2] >= 8
+    scaling = 128 ** -0.5
+    q = d.query
+    out = torch.empty(q.shape, dtype=q.dtype, device=gpu)
+    decode_into(mgr, 0, q, d.key_new, d.value_new, scaling, out, kernel=kernel)
+    torch.cuda.synchronize()
+    for b in range(B):
+        print(f"target 4.0: kernel {kernel}, sequence {b}", flush=True)
+        assert_decode_close(out[b], _oracle(d, mgr, b, n_q, n_kv, scaling))
